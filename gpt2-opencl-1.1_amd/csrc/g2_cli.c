@@ -1,0 +1,121 @@
+/*
+ * g2_cli.c -- ids-driven command-line driver (the reference's main(),
+ * main.c:1967-2200, without the tokenizer: prompts are token ids).
+ *
+ *   g2run (--model DIR | --synth small|medium|large|xl) [--seed S]
+ *         [--format fp32|fp16] [--path fused|reference]
+ *         (--ids 1,2,3 | --random-prompt P) [--max-tokens N] [--min-tokens N]
+ *
+ * Greedy decoding (temperature 0, repetition penalty off).  Prints the
+ * generated ids and a timing summary in the style of main.c:2162-2169.
+ */
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "g2hip.h"
+
+static int preset(const char *name, g2_config *c)
+{
+    static const struct { const char *n; int L, E, H; } p[] = {
+        { "small", 12, 768, 12 }, { "medium", 24, 1024, 16 },
+        { "large", 36, 1280, 20 }, { "xl", 48, 1600, 25 } };
+    for (size_t i = 0; i < sizeof p / sizeof p[0]; ++i)
+        if (!strcmp(name, p[i].n)) {
+            c->n_layer = p[i].L; c->n_embd = p[i].E; c->n_head = p[i].H;
+            c->n_ctx = 1024; c->vocab_size = 50257; c->ffn_dim = 4 * p[i].E;
+            return 0;
+        }
+    return -1;
+}
+
+static void die(const char *what, int rc)
+{
+    fprintf(stderr, "%s failed (%d): %s\n", what, rc, g2_last_error());
+    exit(EXIT_FAILURE);
+}
+
+int main(int argc, char **argv)
+{
+    const char *model_dir = NULL, *synth = NULL, *ids_arg = NULL;
+    unsigned long long seed = 0x67707432ULL;
+    int dtype = G2_F32, path = G2_PATH_FUSED, random_prompt = 0, max_new = 32, min_new = 1;
+    for (int i = 1; i < argc; ++i) {
+        const char *a = argv[i];
+        const char *v = i + 1 < argc ? argv[i + 1] : NULL;
+        if (!strcmp(a, "--model") && v) { model_dir = v; ++i; }
+        else if (!strcmp(a, "--synth") && v) { synth = v; ++i; }
+        else if (!strcmp(a, "--seed") && v) { seed = strtoull(v, NULL, 0); ++i; }
+        else if (!strcmp(a, "--format") && v) { dtype = !strcmp(v, "fp16") ? G2_F16 : G2_F32; ++i; }
+        else if (!strcmp(a, "--path") && v) { path = !strcmp(v, "reference") ? G2_PATH_REFERENCE : G2_PATH_FUSED; ++i; }
+        else if (!strcmp(a, "--ids") && v) { ids_arg = v; ++i; }
+        else if (!strcmp(a, "--random-prompt") && v) { random_prompt = atoi(v); ++i; }
+        else if (!strcmp(a, "--max-tokens") && v) { max_new = atoi(v); ++i; }
+        else if (!strcmp(a, "--min-tokens") && v) { min_new = atoi(v); ++i; }
+        else {
+            fprintf(stderr, "usage: %s (--model DIR | --synth small|medium|large|xl) [--seed S] "
+                            "[--format fp32|fp16] [--path fused|reference] "
+                            "(--ids a,b,c | --random-prompt P) [--max-tokens N] [--min-tokens N]\n", argv[0]);
+            return EXIT_FAILURE;
+        }
+    }
+    if ((!model_dir && !synth) || (!ids_arg && random_prompt <= 0)) {
+        fprintf(stderr, "need a model (--model/--synth) and a prompt (--ids/--random-prompt)\n");
+        return EXIT_FAILURE;
+    }
+    int rc = g2_init(0);
+    if (rc) die("g2_init", rc);
+    char name[128];
+    int cus = 0;
+    g2_device_name(name, sizeof name, &cus);
+    printf("Device: %s (%d CUs)\n", name, cus);
+
+    g2_model *m = NULL;
+    g2_config cfg;
+    if (synth) {
+        if (preset(synth, &cfg)) { fprintf(stderr, "unknown preset %s\n", synth); return EXIT_FAILURE; }
+        rc = g2_model_synth(&cfg, seed, dtype, path, &m);
+        if (rc) die("g2_model_synth", rc);
+    } else {
+        rc = g2_model_load(model_dir, dtype, path, &m);
+        if (rc) die("g2_model_load", rc);
+    }
+    g2_model_config(m, &cfg);
+    printf("Config: n_layer=%d n_embd=%d n_head=%d ffn=%d vocab=%d\n", cfg.n_layer, cfg.n_embd,
+           cfg.n_head, cfg.ffn_dim, cfg.vocab_size);
+    printf("Model VRAM: %.1f MiB\n", g2_model_weight_bytes(m) / 1048576.0);
+
+    int prompt[G2_MAX_SEQ];
+    int P = 0;
+    if (ids_arg) {
+        const char *s = ids_arg;
+        while (*s && P < G2_MAX_SEQ - 1) {
+            prompt[P++] = (int)strtol(s, (char **)&s, 10);
+            while (*s == ',' || *s == ' ') ++s;
+        }
+    } else {
+        unsigned long long x = seed ^ 0x5EEDULL;
+        P = random_prompt < G2_MAX_SEQ - 1 ? random_prompt : G2_MAX_SEQ - 1;
+        for (int i = 0; i < P; ++i) {
+            x = x * 6364136223846793005ULL + 1442695040888963407ULL;
+            prompt[i] = (int)((x >> 33) % (unsigned long long)cfg.vocab_size);
+        }
+    }
+    int *out = malloc(sizeof(int) * G2_MAX_SEQ);
+    double t[2] = { 0, 0 };
+    const int n = g2_generate(m, prompt, P, max_new, min_new, out, t);
+    if (n < 0) die("g2_generate", n);
+    printf("Generated:");
+    for (int i = 0; i < n; ++i) printf(" %d", out[i]);
+    printf("\n");
+    fprintf(stderr,
+            "Timing:\n"
+            "  prefill+first : %9.3f ms (%d prompt tokens, %.1f tok/s)\n"
+            "  decode (%3d steps): %9.3f ms (%.3f ms/token, %.1f tok/s)\n",
+            t[0], P, t[0] > 0 ? P / (t[0] * 1e-3) : 0.0, n - 1, t[1],
+            n > 1 ? t[1] / (n - 1) : 0.0, n > 1 && t[1] > 0 ? (n - 1) / (t[1] * 1e-3) : 0.0);
+    free(out);
+    g2_model_free(m);
+    g2_shutdown();
+    return EXIT_SUCCESS;
+}

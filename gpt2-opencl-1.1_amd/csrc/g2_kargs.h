@@ -1,0 +1,177 @@
+/*
+ * g2_kargs.h -- kernel argument blocks shared by the C99 host (g2_shim.c,
+ * g2_model.c) and the gfx950 device code (g2_kernels.hip).
+ *
+ * Every kernel takes exactly one of these structs by value, so a host launch
+ * is hipModuleLaunchKernel(f, grid, block, 0, stream, {&args}, NULL).  Only
+ * fixed-width scalars and pointers appear, so the layout is the same under
+ * gcc (x86-64) and clang (amdgcn).
+ */
+#ifndef G2_KARGS_H
+#define G2_KARGS_H
+
+#include <stdint.h>
+
+#define G2_KV_MAX_SEQ 1024   /* KV cache length and scores row stride (math.cl:18) */
+#define G2_EOS_ID 50256      /* end-of-text id (main.c:58) */
+
+/* Device-resident decode state (int32 words), read by the fused kernels so a
+ * captured graph can be replayed token after token without host writes. */
+enum {
+    G2S_POS = 0,      /* position processed by the next decode forward       */
+    G2S_TOK = 1,      /* token id at that position                           */
+    G2S_MIN_NEW = 2,  /* EOS is masked while G2S_NGEN < G2S_MIN_NEW          */
+    G2S_NGEN = 3,     /* tokens selected so far in this generation           */
+    G2S_ERR = 4,      /* sticky error bits set by kernels (bounds clamps)    */
+    G2S_IDS = 16,     /* ids selected, G2S_IDS + k for the k-th selection    */
+    G2S_WORDS = 16 + 1024
+};
+
+/* GEMM: C[M,N] = A[M,K] * op(B) with an epilogue.
+ * B layout G2_BKN: [K,N] row-major (the reference's device layout);
+ * B layout G2_BNK: [N,K] row-major (packed, output-major).
+ * Epilogues: store (C = acc + bias), gelu (C = gelu(acc + bias)),
+ * resid (C = C + (acc + bias), in place), qkv (columns < E to q_out[M,E],
+ * E..2E-1 to k_cache[(n-E)*S + pos0+m], 2E..3E-1 to v_cache[(pos0+m)*E + n-2E]). */
+typedef struct {
+    const float *A;
+    const void *B;
+    const float *bias;
+    float *C;
+    float *q_out;
+    float *k_cache;
+    float *v_cache;
+    int M, N, K;
+    int E, S, pos0;
+} g2_gemm_args;
+
+/* Reference-layout matvec, first pass: partial[split*N + n] = sum over the
+ * split's contiguous k-range of A[k] B[k*N + n]; grid (column tiles, splits). */
+typedef struct {
+    const float *A;
+    const void *B;
+    float *partial;
+    int N, K, rows_per_split;
+} g2_mvkn_args;
+
+/* Split-K partials with the reference's strided slices (math.cl:229-246). */
+typedef struct {
+    const float *A;
+    const void *B;
+    float *partial;
+    int N, K, kslice;
+} g2_mvsk_args;
+
+/* reduce_partial (math.cl:249-280), also the second pass of g2_matvec. */
+typedef struct {
+    const float *partial;
+    const float *bias;
+    const float *residual;
+    float *C;
+    int N, nslice, apply_gelu;
+} g2_reduce_args;
+
+typedef struct {
+    const float *x;
+    float *out;
+    const float *gamma;
+    const float *beta;
+    int E, rows;
+} g2_ln_args;
+
+typedef struct {
+    float *a;
+    const float *b;
+    int n;
+} g2_ew_args;
+
+/* Embedding; wte/wpe are f32 or f16 by kernel variant.  If state != NULL the
+ * single row uses state[G2S_TOK] at state[G2S_POS]; else ids[i] at start_pos+i. */
+typedef struct {
+    const void *wte;
+    const void *wpe;
+    float *out;
+    const int *ids;
+    const int *state;
+    int E, seq_len, start_pos;
+} g2_embed_args;
+
+typedef struct {
+    const float *qkv;
+    float *k_cache;
+    float *v_cache;
+    int start_pos, T, D, S;
+} g2_splitkv_args;
+
+typedef struct {
+    const float *qkv;
+    const float *k_cache;
+    float *scores;
+    int q_base, T, D, DH, NH, S;
+    float scale;
+} g2_scores_args;
+
+typedef struct {
+    float *scores;
+    int T, NH;
+} g2_softmax_args;
+
+typedef struct {
+    const float *scores;
+    const float *v_cache;
+    float *out;
+    int T, D, DH, out_base;
+} g2_attnout_args;
+
+/* Single-query attention, head dim 64, split over key chunks with an
+ * in-kernel merge.  T = T_fixed if > 0, else state[G2S_POS] + 1.
+ * part: [NH][max_chunks][2 + 64] floats; counter: [NH] (zero between uses). */
+typedef struct {
+    const float *q;
+    const float *k_cache;
+    const float *v_cache;
+    float *out;
+    const int *state;
+    float *part;
+    unsigned *counter;
+    int T_fixed, D, NH, S, max_chunks;
+    float scale;
+} g2_attn1q_args;
+
+/* Fused row-major matvec over packed weights W[N,K] (f32 or f16):
+ * acc[n] = sum_k W[n*K + k] * xin[k], where xin is x, or LayerNorm(x) with
+ * ln_g/ln_b when the LN variant is used.  Epilogue by kernel variant:
+ * store y = acc + bias; gelu; resid y = y + (acc + bias);
+ * qkv (q_out / k_cache / v_cache at state[G2S_POS]);
+ * argmax: y = acc (logits), first-max argmax with EOS masked while
+ * state[G2S_NGEN] < state[G2S_MIN_NEW], merged by the last work-group, which
+ * then appends the id to state[G2S_IDS + NGEN], sets TOK, POS+1 and NGEN+1. */
+typedef struct {
+    const void *W;
+    const float *x;
+    const float *ln_g;
+    const float *ln_b;
+    const float *bias;
+    float *y;
+    float *q_out;
+    float *k_cache;
+    float *v_cache;
+    int *state;
+    float *part;
+    unsigned *counter;
+    int N, K, E, S;
+    int advance;          /* argmax: 1 = update POS/TOK/NGEN, 0 = only IDS/TOK */
+} g2_rows_args;
+
+/* Causal attention over a prompt block: rows i < P of q[P,E]; keys/values
+ * j <= i from the transposed K cache and the V cache; head dim 64. */
+typedef struct {
+    const float *q;
+    const float *k_cache;
+    const float *v_cache;
+    float *out;
+    int P, E, NH, S;
+    float scale;
+} g2_attnp_args;
+
+#endif /* G2_KARGS_H */

@@ -1,0 +1,856 @@
+/*
+ * g2_kernels.hip -- gfx950 device code of the GPT-2 forward pass.
+ *
+ * Built with `hipcc --genco --offload-arch=gfx950` into one code object that
+ * the C99 host loads with hipModuleLoadData and launches with
+ * hipModuleLaunchKernel.  Every kernel is extern "C" and takes one argument
+ * block from g2_kargs.h by value.
+ *
+ * Two families:
+ *  - reference operators (same argument meaning as the math.cl kernels):
+ *    matmul, matvec, matvec split-K + reduce, layernorm, add, gelu, embed,
+ *    split_kv, attention scores / softmax / weighted sum;
+ *  - fused decode/prefill kernels over output-major packed weights:
+ *    LayerNorm-prologue matvecs with bias/GELU/residual/KV-scatter/argmax
+ *    epilogues, split single-query attention with an in-kernel merge, MFMA
+ *    GEMMs with the same epilogues, and causal prompt attention.
+ *
+ * Wavefronts are 64 lanes; work-groups are 256 threads (4 waves) unless a
+ * kernel says otherwise.  All accumulation is fp32; fp16 weights are widened
+ * in registers.
+ */
+#include <hip/hip_runtime.h>
+#include "g2_kargs.h"
+
+#define G2K extern "C" __global__ __launch_bounds__(256)
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+#define G2_MAXK 6400 /* largest K of a packed matvec (ffn of GPT-2 XL) */
+
+/* ---------------------------------------------------------------- helpers */
+
+/* tanh-approximate GELU, the formula of math.cl:21-23. */
+__device__ __forceinline__ float gelu_f(float v)
+{
+    return 0.5f * v * (1.0f + tanhf(0.7978845608f * (v + 0.044715f * v * v * v)));
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+/* Sum over a 256-thread work-group; every thread gets the total.  The four
+ * wave totals are added in wave order. */
+__device__ __forceinline__ float block_sum(float v, float *red4)
+{
+    v = wave_sum(v);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red4[wave] = v;
+    __syncthreads();
+    const float t = ((red4[0] + red4[1]) + red4[2]) + red4[3];
+    __syncthreads();
+    return t;
+}
+
+/* Loads/stores that other work-groups read after an agent-scope fence. */
+__device__ __forceinline__ float ld_agent(const float *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(float *p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ int clampi(int v, int lo, int hi)
+{
+    return v < lo ? lo : (v > hi ? hi : v);
+}
+
+/* Element access for f32 / f16 weight storage. */
+template <typename T> __device__ __forceinline__ float ldw(const T *p, size_t i);
+template <> __device__ __forceinline__ float ldw<float>(const float *p, size_t i) { return p[i]; }
+template <> __device__ __forceinline__ float ldw<_Float16>(const _Float16 *p, size_t i) { return (float)p[i]; }
+
+/* ======================================================================
+ * Reference operators
+ * ==================================================================== */
+
+/* ---- matvec, reference layout B[K,N] (launch_matvec, main.c:1554-1576) ---
+ * Pass 1: grid (ceil(N/256), splits).  Each work-group owns 256 columns (4 per
+ * lane) and a contiguous k-range of rows_per_split rows; wave w takes rows
+ * k0+w, k0+w+4, ...; the four wave sums are added in wave order into
+ * partial[split][n].  Pass 2 is g2k_reduce. */
+template <typename WT, bool VEC>
+__device__ void mvkn_impl(const g2_mvkn_args &a)
+{
+    __shared__ float red[4][256];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = blockIdx.x * 256 + lane * 4;
+    const int k0 = blockIdx.y * a.rows_per_split;
+    const int k1 = min(a.K, k0 + a.rows_per_split);
+    const WT *B = (const WT *)a.B;
+    float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+    if (VEC && col + 3 < a.N) {
+        int k = k0 + wave;
+        for (; k + 12 < k1; k += 16) {
+            float av[4];
+            float bv[4][4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const size_t base = (size_t)(k + 4 * u) * a.N + col;
+                av[u] = a.A[k + 4 * u];
+                if constexpr (sizeof(WT) == 4) {
+                    const f32x4 w = *(const f32x4 *)((const float *)B + base);
+                    bv[u][0] = w.x; bv[u][1] = w.y; bv[u][2] = w.z; bv[u][3] = w.w;
+                } else {
+                    const f16x4 w = *(const f16x4 *)((const _Float16 *)B + base);
+                    bv[u][0] = (float)w.x; bv[u][1] = (float)w.y;
+                    bv[u][2] = (float)w.z; bv[u][3] = (float)w.w;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                acc0 = fmaf(av[u], bv[u][0], acc0);
+                acc1 = fmaf(av[u], bv[u][1], acc1);
+                acc2 = fmaf(av[u], bv[u][2], acc2);
+                acc3 = fmaf(av[u], bv[u][3], acc3);
+            }
+        }
+        for (; k < k1; k += 4) {
+            const size_t base = (size_t)k * a.N + col;
+            const float av = a.A[k];
+            acc0 = fmaf(av, ldw(B, base + 0), acc0);
+            acc1 = fmaf(av, ldw(B, base + 1), acc1);
+            acc2 = fmaf(av, ldw(B, base + 2), acc2);
+            acc3 = fmaf(av, ldw(B, base + 3), acc3);
+        }
+    } else {
+        for (int k = k0 + wave; k < k1; k += 4) {
+            const size_t base = (size_t)k * a.N;
+            const float av = a.A[k];
+            if (col + 0 < a.N) acc0 = fmaf(av, ldw(B, base + col + 0), acc0);
+            if (col + 1 < a.N) acc1 = fmaf(av, ldw(B, base + col + 1), acc1);
+            if (col + 2 < a.N) acc2 = fmaf(av, ldw(B, base + col + 2), acc2);
+            if (col + 3 < a.N) acc3 = fmaf(av, ldw(B, base + col + 3), acc3);
+        }
+    }
+    red[wave][lane * 4 + 0] = acc0;
+    red[wave][lane * 4 + 1] = acc1;
+    red[wave][lane * 4 + 2] = acc2;
+    red[wave][lane * 4 + 3] = acc3;
+    __syncthreads();
+    const int t = threadIdx.x, n = blockIdx.x * 256 + t;
+    if (n < a.N)
+        a.partial[(size_t)blockIdx.y * a.N + n] =
+            ((red[0][t] + red[1][t]) + red[2][t]) + red[3][t];
+}
+
+G2K void g2k_mvkn_f32(const g2_mvkn_args a) { mvkn_impl<float, true>(a); }
+G2K void g2k_mvkn_f32_s(const g2_mvkn_args a) { mvkn_impl<float, false>(a); }
+G2K void g2k_mvkn_f16(const g2_mvkn_args a) { mvkn_impl<_Float16, true>(a); }
+G2K void g2k_mvkn_f16_s(const g2_mvkn_args a) { mvkn_impl<_Float16, false>(a); }
+
+/* ---- matvec4_sk (math.cl:229-246): slice s sums k = s, s+kslice, ... ------
+ * grid (ceil(N/4 / 256), kslice); one thread per (4 columns, slice). */
+template <typename WT>
+__device__ void mvsk_impl(const g2_mvsk_args &a)
+{
+    const int c4 = blockIdx.x * 256 + threadIdx.x;
+    const int s = blockIdx.y;
+    const int N4 = a.N >> 2;
+    if (c4 >= N4 || s >= a.kslice) return;
+    const WT *B = (const WT *)a.B;
+    float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+    for (int k = s; k < a.K; k += a.kslice) {
+        const size_t base = (size_t)k * a.N + (size_t)c4 * 4;
+        const float av = a.A[k];
+        acc0 = fmaf(av, ldw(B, base + 0), acc0);
+        acc1 = fmaf(av, ldw(B, base + 1), acc1);
+        acc2 = fmaf(av, ldw(B, base + 2), acc2);
+        acc3 = fmaf(av, ldw(B, base + 3), acc3);
+    }
+    float *p = a.partial + (size_t)s * a.N + (size_t)c4 * 4;
+    p[0] = acc0; p[1] = acc1; p[2] = acc2; p[3] = acc3;
+}
+
+G2K void g2k_mvsk_f32(const g2_mvsk_args a) { mvsk_impl<float>(a); }
+G2K void g2k_mvsk_f16(const g2_mvsk_args a) { mvsk_impl<_Float16>(a); }
+
+/* ---- reduce_partial (math.cl:249-280): slices added in order, then bias,
+ * residual, GELU.  residual may alias C (each n is read then written by the
+ * same thread). */
+G2K void g2k_reduce(const g2_reduce_args a)
+{
+    const int n = blockIdx.x * 256 + threadIdx.x;
+    if (n >= a.N) return;
+    float s = 0.f;
+    for (int k = 0; k < a.nslice; ++k) s += a.partial[(size_t)k * a.N + n];
+    if (a.bias) s += a.bias[n];
+    if (a.residual) s += a.residual[n];
+    if (a.apply_gelu) s = gelu_f(s);
+    a.C[n] = s;
+}
+
+/* ---- layernorm (math.cl:283-311): one work-group per row, two-pass mean and
+ * biased variance, eps 1e-5, out = (x-mean)*inv_std*gamma + beta. */
+G2K void g2k_layernorm(const g2_ln_args a)
+{
+    __shared__ float red4[4];
+    const int row = blockIdx.x;
+    if (row >= a.rows) return;
+    const float *x = a.x + (size_t)row * a.E;
+    float *o = a.out + (size_t)row * a.E;
+    float s = 0.f;
+    for (int i = threadIdx.x; i < a.E; i += 256) s += x[i];
+    const float mean = block_sum(s, red4) / (float)a.E;
+    float q = 0.f;
+    for (int i = threadIdx.x; i < a.E; i += 256) {
+        const float d = x[i] - mean;
+        q = fmaf(d, d, q);
+    }
+    const float var = block_sum(q, red4) / (float)a.E;
+    const float inv = 1.0f / sqrtf(var + 1e-5f);
+    for (int i = threadIdx.x; i < a.E; i += 256)
+        o[i] = fmaf((x[i] - mean) * inv, a.gamma[i], a.beta[i]);
+}
+
+/* ---- add_inplace (math.cl:314-322) and gelu (math.cl:325-330) ---------- */
+G2K void g2k_add(const g2_ew_args a)
+{
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < a.n; i += gridDim.x * 256)
+        a.a[i] += a.b[i];
+}
+
+G2K void g2k_gelu(const g2_ew_args a)
+{
+    for (int i = blockIdx.x * 256 + threadIdx.x; i < a.n; i += gridDim.x * 256)
+        a.a[i] = gelu_f(a.a[i]);
+}
+
+/* ---- embed (math.cl:333-350); grid (ceil(E/256), rows). With a state
+ * pointer the single row takes its token and position from the device. */
+template <typename T>
+__device__ void embed_impl(const g2_embed_args &a)
+{
+    const int d = blockIdx.x * 256 + threadIdx.x;
+    const int i = blockIdx.y;
+    if (d >= a.E || i >= a.seq_len) return;
+    int tok, pos;
+    if (a.state) {
+        tok = a.state[G2S_TOK];
+        pos = clampi(a.state[G2S_POS], 0, G2_KV_MAX_SEQ - 1);
+    } else {
+        tok = a.ids[i];
+        pos = a.start_pos + i;
+    }
+    tok = clampi(tok, 0, 0x7fffffff);
+    const T *wte = (const T *)a.wte, *wpe = (const T *)a.wpe;
+    a.out[(size_t)i * a.E + d] =
+        ldw(wte, (size_t)tok * a.E + d) + ldw(wpe, (size_t)pos * a.E + d);
+}
+
+G2K void g2k_embed_f32(const g2_embed_args a) { embed_impl<float>(a); }
+G2K void g2k_embed_f16(const g2_embed_args a) { embed_impl<_Float16>(a); }
+
+/* ---- split_kv (math.cl:367-383) ---------------------------------------- */
+G2K void g2k_split_kv(const g2_splitkv_args a)
+{
+    const long n = (long)blockIdx.x * 256 + threadIdx.x;
+    if (n >= (long)a.T * a.D) return;
+    const int i = (int)(n / a.D), d = (int)(n % a.D);
+    const int pos = a.start_pos + i;
+    a.k_cache[(size_t)d * a.S + pos] = a.qkv[(size_t)i * 3 * a.D + a.D + d];
+    a.v_cache[(size_t)pos * a.D + d] = a.qkv[(size_t)i * 3 * a.D + 2 * a.D + d];
+}
+
+/* ---- attn_scores_1q (math.cl:388-412); grid (NH, ceil(T/256)) ---------- */
+G2K void g2k_attn_scores(const g2_scores_args a)
+{
+    const int h = blockIdx.x, j = blockIdx.y * 256 + threadIdx.x;
+    if (h >= a.NH || j >= a.T) return;
+    const float *q = a.qkv + a.q_base + (size_t)h * a.DH;
+    const float *kc = a.k_cache + (size_t)h * a.DH * a.S + j;
+    float s = 0.f;
+    for (int k = 0; k < a.DH; ++k) s = fmaf(q[k], kc[(size_t)k * a.S], s);
+    a.scores[(size_t)h * a.S + j] = s * a.scale;
+}
+
+/* ---- attn_softmax_1q (math.cl:415-456): one work-group per head, in place,
+ * row stride G2_MAX_SEQ. */
+G2K void g2k_attn_softmax(const g2_softmax_args a)
+{
+    __shared__ float red4[4];
+    const int h = blockIdx.x;
+    if (h >= a.NH) return;
+    float *row = a.scores + (size_t)h * G2_KV_MAX_SEQ;
+    float mx = -1e30f;
+    for (int j = threadIdx.x; j < a.T; j += 256) mx = fmaxf(mx, row[j]);
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) red4[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    const float m = fmaxf(fmaxf(red4[0], red4[1]), fmaxf(red4[2], red4[3]));
+    __syncthreads();
+    float s = 0.f;
+    for (int j = threadIdx.x; j < a.T; j += 256) {
+        const float e = expf(row[j] - m);
+        row[j] = e;
+        s += e;
+    }
+    const float inv = 1.0f / block_sum(s, red4);
+    for (int j = threadIdx.x; j < a.T; j += 256) row[j] *= inv;
+}
+
+/* ---- attn_out_1q (math.cl:459-476): grid ceil(D/64), block 1024: lane d of
+ * the block's 64 dims, 16 waves split j (j = wave, wave+16, ...). */
+extern "C" __global__ __launch_bounds__(1024) void g2k_attn_out(const g2_attnout_args a)
+{
+    __shared__ float red[16][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int d = blockIdx.x * 64 + lane;
+    float o = 0.f;
+    if (d < a.D) {
+        const float *srow = a.scores + (size_t)(d / a.DH) * G2_KV_MAX_SEQ;
+        for (int j = wave; j < a.T; j += 16)
+            o = fmaf(srow[j], a.v_cache[(size_t)j * a.D + d], o);
+    }
+    red[wave][lane] = o;
+    __syncthreads();
+    if (wave == 0 && d < a.D) {
+        float s = 0.f;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) s += red[w][lane];
+        a.out[a.out_base + d] = s;
+    }
+}
+
+/* ======================================================================
+ * Single-query attention, head dim 64 (fused scores -> softmax -> PV)
+ *
+ * grid (NH, max_chunks), 256 threads.  Work-group (h, c) takes positions
+ * [64c, 64c+64) of head h: scores with lanes over positions (transposed K,
+ * 256-byte rows), a chunk-local softmax, the weighted V sum with lanes over
+ * the 64 dims, then writes (max, sum, o[64]) to part.  The last work-group
+ * of a head to finish (agent-scope counter) merges the chunk partials in
+ * chunk order with the usual max-rescaling and writes out[h*64 .. +64].
+ * ==================================================================== */
+G2K void g2k_attn_1q(const g2_attn1q_args a)
+{
+    __shared__ float qs[64];
+    __shared__ float pr[64];
+    __shared__ float red[4][64];
+    __shared__ float stat[2];
+    __shared__ int is_last;
+    const int h = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
+    const int T = clampi(a.T_fixed > 0 ? a.T_fixed : a.state[G2S_POS] + 1, 1, a.S);
+    const int nch = (T + 63) >> 6;
+    if (h >= a.NH || c >= nch || nch > a.max_chunks) return;
+    const int j0 = c * 64;
+    if (tid < 64) qs[tid] = a.q[h * 64 + tid];
+    __syncthreads();
+    {
+        const int jj = tid & 63, dg = tid >> 6, j = j0 + jj;
+        float s = 0.f;
+        if (j < T) {
+            const float *kp = a.k_cache + (size_t)(h * 64 + dg * 16) * a.S + j;
+#pragma unroll
+            for (int d = 0; d < 16; ++d) s = fmaf(qs[dg * 16 + d], kp[(size_t)d * a.S], s);
+        }
+        red[dg][jj] = s;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const bool ok = j0 + tid < T;
+        const float s = (((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid]) * a.scale;
+        const float m = wave_max(ok ? s : -INFINITY);
+        const float p = ok ? expf(s - m) : 0.f;
+        const float l = wave_sum(p);
+        pr[tid] = p;
+        if (tid == 0) { stat[0] = m; stat[1] = l; }
+    }
+    __syncthreads();
+    {
+        const int d = tid & 63, jg = tid >> 6;
+        float o = 0.f;
+#pragma unroll 4
+        for (int i = 0; i < 16; ++i) {
+            const int jj = jg + 4 * i, j = j0 + jj;
+            if (j < T) o = fmaf(pr[jj], a.v_cache[(size_t)j * a.D + h * 64 + d], o);
+        }
+        red[jg][d] = o;
+    }
+    __syncthreads();
+    const float o = tid < 64 ? ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid] : 0.f;
+    if (nch == 1) {
+        if (tid < 64) a.out[h * 64 + tid] = o / stat[1];
+        return;
+    }
+    float *pp = a.part + ((size_t)h * a.max_chunks + c) * 66;
+    if (tid < 64) {
+        st_agent(pp + 2 + tid, o);
+        if (tid == 0) { st_agent(pp, stat[0]); st_agent(pp + 1, stat[1]); }
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) {
+        const unsigned old = atomicAdd(&a.counter[h], 1u);
+        is_last = (old == (unsigned)(nch - 1));
+    }
+    __syncthreads();
+    if (!is_last) return;
+    __threadfence();
+    if (tid < 64) {
+        const float *hp = a.part + (size_t)h * a.max_chunks * 66;
+        float M = -INFINITY;
+        for (int cc = 0; cc < nch; ++cc) M = fmaxf(M, ld_agent(hp + (size_t)cc * 66));
+        float L = 0.f, acc = 0.f;
+        for (int cc = 0; cc < nch; ++cc) {
+            const float w = expf(ld_agent(hp + (size_t)cc * 66) - M);
+            L = fmaf(ld_agent(hp + (size_t)cc * 66 + 1), w, L);
+            acc = fmaf(ld_agent(hp + (size_t)cc * 66 + 2 + tid), w, acc);
+        }
+        a.out[h * 64 + tid] = acc / L;
+    }
+    if (tid == 0) a.counter[h] = 0u;
+}
+
+/* ======================================================================
+ * Fused row-major matvec over packed weights W[N,K] (decode hot path)
+ *
+ * 256 threads; wave w of work-group b takes R consecutive rows starting at
+ * (b*4 + w)*R and strides by gridDim.x*4*R.  Lanes stream 16-byte chunks of
+ * each row (4 fp32 or 8 fp16 weights), U chunks per row in flight, and
+ * multiply them with the input vector held in LDS; a butterfly over the wave
+ * gives the row sum.  The input vector is x, or LayerNorm(x) computed by
+ * every work-group in its prologue.
+ * ==================================================================== */
+enum { EPI_STORE = 0, EPI_GELU = 1, EPI_RESID = 2, EPI_QKV = 3, EPI_ARGMAX = 4 };
+
+template <typename WT> struct chunk_t;
+template <> struct chunk_t<float> { typedef f32x4 T; static constexpr int V = 4; };
+template <> struct chunk_t<_Float16> { typedef f16x8 T; static constexpr int V = 8; };
+
+template <typename WT>
+__device__ __forceinline__ float chunk_dot(const typename chunk_t<WT>::T &w, const float *xs)
+{
+    if constexpr (sizeof(WT) == 4) {
+        const f32x4 x = *(const f32x4 *)xs;
+        float s = w.x * x.x;
+        s = fmaf(w.y, x.y, s);
+        s = fmaf(w.z, x.z, s);
+        return fmaf(w.w, x.w, s);
+    } else {
+        const f32x4 x0 = *(const f32x4 *)xs;
+        const f32x4 x1 = *(const f32x4 *)(xs + 4);
+        float s = (float)w[0] * x0.x;
+        s = fmaf((float)w[1], x0.y, s);
+        s = fmaf((float)w[2], x0.z, s);
+        s = fmaf((float)w[3], x0.w, s);
+        s = fmaf((float)w[4], x1.x, s);
+        s = fmaf((float)w[5], x1.y, s);
+        s = fmaf((float)w[6], x1.z, s);
+        return fmaf((float)w[7], x1.w, s);
+    }
+}
+
+/* Better (value, index) under first-max: larger value, then lower index. */
+__device__ __forceinline__ bool am_better(float v1, int i1, float v2, int i2)
+{
+    return v1 > v2 || (v1 == v2 && i1 < i2);
+}
+
+template <typename WT, int EPI, bool LN, int R, int U>
+__device__ void rows_impl(const g2_rows_args &a)
+{
+    typedef typename chunk_t<WT>::T CT;
+    constexpr int V = chunk_t<WT>::V;
+    __shared__ __attribute__((aligned(16))) float xs[G2_MAXK];
+    __shared__ float red4[4];
+    __shared__ float amv[256];
+    __shared__ int ami[256];
+    __shared__ int is_last;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int K = a.K, N = a.N, C = K / V;
+
+    /* prologue: input vector (optionally LayerNorm'd) into LDS */
+    if (LN) {
+        float s = 0.f;
+        for (int k = tid; k < K; k += 256) {
+            const float v = a.x[k];
+            xs[k] = v;
+            s += v;
+        }
+        const float mean = block_sum(s, red4) / (float)K;
+        float q = 0.f;
+        for (int k = tid; k < K; k += 256) {
+            const float d = xs[k] - mean;
+            q = fmaf(d, d, q);
+        }
+        const float inv = 1.0f / sqrtf(block_sum(q, red4) / (float)K + 1e-5f);
+        for (int k = tid; k < K; k += 256)
+            xs[k] = fmaf((xs[k] - mean) * inv, a.ln_g[k], a.ln_b[k]);
+    } else {
+        for (int k = tid; k < K; k += 256) xs[k] = a.x[k];
+    }
+    __syncthreads();
+
+    int pos = 0;
+    if (EPI == EPI_QKV) pos = clampi(a.state[G2S_POS], 0, a.S - 1);
+    float best_v = -INFINITY;
+    int best_i = 0x7fffffff;
+    int masked = -1;
+    if (EPI == EPI_ARGMAX)
+        masked = a.state[G2S_NGEN] < a.state[G2S_MIN_NEW] ? G2_EOS_ID : -1;
+
+    const CT *W = (const CT *)a.W;
+    for (int row0 = (blockIdx.x * 4 + wave) * R; row0 < N; row0 += gridDim.x * 4 * R) {
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = 0.f;
+        for (int c0 = lane; c0 < C; c0 += 64 * U) {
+            CT w[R][U];
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int c = c0 + 64 * u;
+                    if (c < C && row0 + r < N) w[r][u] = W[(size_t)(row0 + r) * C + c];
+                }
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int c = c0 + 64 * u;
+                    if (c < C && row0 + r < N) acc[r] += chunk_dot<WT>(w[r][u], xs + c * V);
+                }
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
+        float v = acc[0];
+#pragma unroll
+        for (int r = 1; r < R; ++r)
+            if (lane == r) v = acc[r];
+        const int n = row0 + lane;
+        if (lane < R && n < N) {
+            if (EPI == EPI_STORE) {
+                if (a.bias) v += a.bias[n];
+                a.y[n] = v;
+            } else if (EPI == EPI_GELU) {
+                if (a.bias) v += a.bias[n];
+                a.y[n] = gelu_f(v);
+            } else if (EPI == EPI_RESID) {
+                if (a.bias) v += a.bias[n];
+                a.y[n] = v + a.y[n];
+            } else if (EPI == EPI_QKV) {
+                if (a.bias) v += a.bias[n];
+                const int E = a.E;
+                if (n < E) a.q_out[n] = v;
+                else if (n < 2 * E) a.k_cache[(size_t)(n - E) * a.S + pos] = v;
+                else a.v_cache[(size_t)pos * E + (n - 2 * E)] = v;
+            } else {
+                a.y[n] = v;
+                const float mv = (n == masked) ? -1e30f : v;
+                if (am_better(mv, n, best_v, best_i)) { best_v = mv; best_i = n; }
+            }
+        }
+    }
+
+    if (EPI == EPI_ARGMAX) {
+        amv[tid] = best_v;
+        ami[tid] = best_i;
+        __syncthreads();
+        for (int s = 128; s > 0; s >>= 1) {
+            if (tid < s && am_better(amv[tid + s], ami[tid + s], amv[tid], ami[tid])) {
+                amv[tid] = amv[tid + s];
+                ami[tid] = ami[tid + s];
+            }
+            __syncthreads();
+        }
+        if (tid == 0) {
+            st_agent(a.part + 2 * blockIdx.x, amv[0]);
+            st_agent(a.part + 2 * blockIdx.x + 1, __int_as_float(ami[0]));
+        }
+        __threadfence();
+        __syncthreads();
+        if (tid == 0) {
+            const unsigned old = atomicAdd(a.counter, 1u);
+            is_last = (old == gridDim.x - 1);
+        }
+        __syncthreads();
+        if (!is_last) return;
+        __threadfence();
+        float bv = -INFINITY;
+        int bi = 0x7fffffff;
+        for (int b = tid; b < (int)gridDim.x; b += 256) {
+            const float v = ld_agent(a.part + 2 * b);
+            const int i = __float_as_int(ld_agent(a.part + 2 * b + 1));
+            if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
+        }
+        amv[tid] = bv;
+        ami[tid] = bi;
+        __syncthreads();
+        for (int s = 128; s > 0; s >>= 1) {
+            if (tid < s && am_better(amv[tid + s], ami[tid + s], amv[tid], ami[tid])) {
+                amv[tid] = amv[tid + s];
+                ami[tid] = ami[tid + s];
+            }
+            __syncthreads();
+        }
+        if (tid == 0) {
+            const int tok = (ami[0] >= 0 && ami[0] < N) ? ami[0] : 0;
+            const int ng = clampi(a.state[G2S_NGEN], 0, G2S_WORDS - G2S_IDS - 1);
+            a.state[G2S_IDS + ng] = tok;
+            a.state[G2S_TOK] = tok;
+            if (a.advance) {
+                a.state[G2S_NGEN] = ng + 1;
+                a.state[G2S_POS] = a.state[G2S_POS] + 1;
+            }
+            *a.counter = 0u;
+        }
+    }
+}
+
+#define G2_ROWS(name, WT, EPI, LN, R, U) \
+    G2K void name(const g2_rows_args a) { rows_impl<WT, EPI, LN, R, U>(a); }
+
+G2_ROWS(g2k_rows_f32_store, float, EPI_STORE, false, 2, 4)
+G2_ROWS(g2k_rows_f16_store, _Float16, EPI_STORE, false, 2, 4)
+G2_ROWS(g2k_rows_f32_ln_store, float, EPI_STORE, true, 2, 4)
+G2_ROWS(g2k_rows_f16_ln_store, _Float16, EPI_STORE, true, 2, 4)
+G2_ROWS(g2k_rows_f32_ln_qkv, float, EPI_QKV, true, 2, 4)
+G2_ROWS(g2k_rows_f16_ln_qkv, _Float16, EPI_QKV, true, 2, 4)
+G2_ROWS(g2k_rows_f32_resid, float, EPI_RESID, false, 2, 4)
+G2_ROWS(g2k_rows_f16_resid, _Float16, EPI_RESID, false, 2, 4)
+G2_ROWS(g2k_rows_f32_ln_gelu, float, EPI_GELU, true, 2, 4)
+G2_ROWS(g2k_rows_f16_ln_gelu, _Float16, EPI_GELU, true, 2, 4)
+G2_ROWS(g2k_rows_f32_ln_argmax, float, EPI_ARGMAX, true, 2, 4)
+G2_ROWS(g2k_rows_f16_ln_argmax, _Float16, EPI_ARGMAX, true, 2, 4)
+
+/* ======================================================================
+ * MFMA GEMM (prefill and the reference matmul)
+ *
+ * Tile 64x64x16, 256 threads = 2x2 waves of 32x32, each wave a 2x2 grid of
+ * v_mfma_f32_16x16x4f32.  A [M,K] fp32 row-major; B [K,N] (BKN) or [N,K]
+ * (BNK), fp32 or fp16 (widened when staged to LDS).  LDS tiles hold
+ * As[m][k] and Bs[n][k] so both fragments read 4 consecutive k per lane
+ * group.  Epilogues as in g2_gemm_args.
+ * MFMA 16x16x4 f32 operand layout: lane l supplies A[l%16][l/16] and
+ * B[l/16][l%16]; the result lane l holds rows 4*(l/16)+r, column l%16.
+ * ==================================================================== */
+enum { GEPI_STORE = 0, GEPI_GELU = 1, GEPI_RESID = 2, GEPI_QKV = 3 };
+
+template <typename BT, bool BNK, int EPI>
+__device__ void gemm_impl(const g2_gemm_args &a)
+{
+    constexpr int BM = 64, BN = 64, BK = 16, LDK = BK + 1;
+    __shared__ float As[BM * LDK];
+    __shared__ float Bs[BN * LDK];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int M = a.M, N = a.N, K = a.K;
+    const BT *B = (const BT *)a.B;
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    for (int k0 = 0; k0 < K; k0 += BK) {
+        /* A tile: thread -> row tid/4, k (tid%4)*4 .. +3 */
+        {
+            const int r = tid >> 2, kq = (tid & 3) * 4;
+            const int gm = m0 + r, gk = k0 + kq;
+            float v[4] = {0.f, 0.f, 0.f, 0.f};
+            if (gm < M) {
+                const float *ap = a.A + (size_t)gm * K + gk;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (gk + e < K) v[e] = ap[e];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) As[r * LDK + kq + e] = v[e];
+        }
+        /* B tile into Bs[n][k] */
+        if (BNK) {
+            const int r = tid >> 2, kq = (tid & 3) * 4;
+            const int gn = n0 + r, gk = k0 + kq;
+            float v[4] = {0.f, 0.f, 0.f, 0.f};
+            if (gn < N) {
+                const size_t base = (size_t)gn * K + gk;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (gk + e < K) v[e] = ldw(B, base + e);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) Bs[r * LDK + kq + e] = v[e];
+        } else {
+            const int kr = tid >> 4, nq = (tid & 15) * 4;
+            const int gk = k0 + kr, gn = n0 + nq;
+            float v[4] = {0.f, 0.f, 0.f, 0.f};
+            if (gk < K) {
+                const size_t base = (size_t)gk * N + gn;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (gn + e < N) v[e] = ldw(B, base + e);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) Bs[(nq + e) * LDK + kr] = v[e];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 4) {
+            float af[2], bf[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                af[i] = As[(wm * 32 + i * 16 + (lane & 15)) * LDK + kk + (lane >> 4)];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                bf[j] = Bs[(wn * 32 + j * 16 + (lane & 15)) * LDK + kk + (lane >> 4)];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
+                const int n = n0 + wn * 32 + j * 16 + (lane & 15);
+                if (m >= M || n >= N) continue;
+                float v = acc[i][j][r];
+                if (a.bias) v += a.bias[n];
+                if (EPI == GEPI_STORE) {
+                    a.C[(size_t)m * N + n] = v;
+                } else if (EPI == GEPI_GELU) {
+                    a.C[(size_t)m * N + n] = gelu_f(v);
+                } else if (EPI == GEPI_RESID) {
+                    a.C[(size_t)m * N + n] = v + a.C[(size_t)m * N + n];
+                } else {
+                    const int E = a.E, pos = a.pos0 + m;
+                    if (n < E) a.q_out[(size_t)m * E + n] = v;
+                    else if (n < 2 * E) a.k_cache[(size_t)(n - E) * a.S + pos] = v;
+                    else a.v_cache[(size_t)pos * E + (n - 2 * E)] = v;
+                }
+            }
+}
+
+#define G2_GEMM(name, BT, BNK, EPI) \
+    G2K void name(const g2_gemm_args a) { gemm_impl<BT, BNK, EPI>(a); }
+
+G2_GEMM(g2k_gemm_kn_f32, float, false, GEPI_STORE)
+G2_GEMM(g2k_gemm_kn_f16, _Float16, false, GEPI_STORE)
+G2_GEMM(g2k_gemm_nk_f32_store, float, true, GEPI_STORE)
+G2_GEMM(g2k_gemm_nk_f16_store, _Float16, true, GEPI_STORE)
+G2_GEMM(g2k_gemm_nk_f32_gelu, float, true, GEPI_GELU)
+G2_GEMM(g2k_gemm_nk_f16_gelu, _Float16, true, GEPI_GELU)
+G2_GEMM(g2k_gemm_nk_f32_resid, float, true, GEPI_RESID)
+G2_GEMM(g2k_gemm_nk_f16_resid, _Float16, true, GEPI_RESID)
+G2_GEMM(g2k_gemm_nk_f32_qkv, float, true, GEPI_QKV)
+G2_GEMM(g2k_gemm_nk_f16_qkv, _Float16, true, GEPI_QKV)
+
+/* ======================================================================
+ * Causal attention over a prompt (prefill), head dim 64
+ *
+ * grid (NH, ceil(P/64)), 256 threads: thread (r = tid/4, g = tid%4) owns
+ * query row r of the block, keys g*16..g*16+15 of each key block for the
+ * scores and dims g*16..g*16+15 of the output.  Key blocks 0..qb are staged
+ * in LDS (K transposed as in the cache, V row-major); online softmax.
+ * ==================================================================== */
+G2K void g2k_attn_prefill(const g2_attnp_args a)
+{
+    constexpr int LD = 65;
+    __shared__ float Qs[64 * LD];
+    __shared__ float Kt[64 * LD];
+    __shared__ float Vs[64 * LD];
+    __shared__ float Ps[64 * LD];
+    const int h = blockIdx.x, qb = blockIdx.y, tid = threadIdx.x;
+    const int r = tid >> 2, g = tid & 3;
+    const int i = qb * 64 + r;
+    const bool row_ok = i < a.P;
+    if (h >= a.NH || qb * 64 >= a.P) return;
+    for (int idx = tid; idx < 64 * 64; idx += 256) {
+        const int rr = idx >> 6, d = idx & 63, ii = qb * 64 + rr;
+        Qs[rr * LD + d] = ii < a.P ? a.q[(size_t)ii * a.E + h * 64 + d] : 0.f;
+    }
+    float o[16];
+#pragma unroll
+    for (int d = 0; d < 16; ++d) o[d] = 0.f;
+    float m = -INFINITY, l = 0.f;
+    for (int kb = 0; kb <= qb; ++kb) {
+        __syncthreads();
+        for (int idx = tid; idx < 64 * 64; idx += 256) {
+            const int d = idx >> 6, key = idx & 63, j = kb * 64 + key;
+            Kt[d * LD + key] = j < a.P ? a.k_cache[(size_t)(h * 64 + d) * a.S + j] : 0.f;
+        }
+        for (int idx = tid; idx < 64 * 64; idx += 256) {
+            const int key = idx >> 6, d = idx & 63, j = kb * 64 + key;
+            Vs[key * LD + d] = j < a.P ? a.v_cache[(size_t)j * a.E + h * 64 + d] : 0.f;
+        }
+        __syncthreads();
+        float s[16];
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) s[kk] = 0.f;
+        for (int d = 0; d < 64; ++d) {
+            const float qv = Qs[r * LD + d];
+#pragma unroll
+            for (int kk = 0; kk < 16; ++kk) s[kk] = fmaf(qv, Kt[d * LD + g * 16 + kk], s[kk]);
+        }
+        float bm = -INFINITY;
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+            const int j = kb * 64 + g * 16 + kk;
+            s[kk] = (row_ok && j <= i) ? s[kk] * a.scale : -INFINITY;
+            bm = fmaxf(bm, s[kk]);
+        }
+        bm = fmaxf(bm, __shfl_xor(bm, 1));
+        bm = fmaxf(bm, __shfl_xor(bm, 2));
+        const float mn = fmaxf(m, bm);
+        const float ms = mn == -INFINITY ? 0.f : mn;
+        const float alpha = expf(m - ms);
+        float ps = 0.f;
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+            const float p = expf(s[kk] - ms);
+            Ps[r * LD + g * 16 + kk] = p;
+            ps += p;
+        }
+        ps += __shfl_xor(ps, 1);
+        ps += __shfl_xor(ps, 2);
+        l = fmaf(l, alpha, ps);
+        m = mn;
+        __syncthreads();
+#pragma unroll
+        for (int d = 0; d < 16; ++d) o[d] *= alpha;
+        for (int key = 0; key < 64; ++key) {
+            const float p = Ps[r * LD + key];
+#pragma unroll
+            for (int d = 0; d < 16; ++d) o[d] = fmaf(p, Vs[key * LD + g * 16 + d], o[d]);
+        }
+    }
+    if (row_ok) {
+        const float inv = 1.0f / l;
+#pragma unroll
+        for (int d = 0; d < 16; ++d) a.out[(size_t)i * a.E + h * 64 + g * 16 + d] = o[d] * inv;
+    }
+}

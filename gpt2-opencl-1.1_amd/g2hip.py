@@ -1,0 +1,410 @@
+"""ctypes binding of libg2hip.so, the C ABI declared in include/g2hip.h.
+
+Mirrors the reference's operator surface (main.c launch_* helpers, math.cl
+kernels) with the same names and argument meaning, plus the model entry
+points (prefill/decode/greedy/generate).  Device buffers are `DevBuf`
+objects (a device pointer and a byte size).  Every failing call raises
+`G2Error` carrying the library's error code and message.
+
+The library must have been built in this directory (`make -B` here, or
+`__graft_entry__.build()`); importing this module without it raises
+ImportError -- there is no fallback implementation.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libg2hip.so")
+HEADER_PATH = os.path.join(os.path.dirname(_HERE), "include", "g2hip.h")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(f"{LIB_PATH} is not built; run make in {_HERE}")
+_lib = C.CDLL(LIB_PATH)
+
+G2_OK, G2_E_ARG, G2_E_STATE, G2_E_IO, G2_E_FORMAT, G2_E_LIMIT, G2_E_NOMEM, G2_E_HIP = 0, -1, -2, -3, -4, -5, -6, -7
+F32, F16 = 0, 1
+PATH_REFERENCE, PATH_FUSED = 0, 1
+MAX_SEQ = 1024
+EOS = 50256
+
+
+class G2Error(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"g2 error {code}: {msg}")
+        self.code = code
+
+
+class Config(C.Structure):
+    _fields_ = [("n_layer", C.c_int), ("n_embd", C.c_int), ("n_head", C.c_int),
+                ("n_ctx", C.c_int), ("vocab_size", C.c_int), ("ffn_dim", C.c_int)]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+
+def make_config(n_layer, n_embd, n_head, vocab_size=50257, ffn_dim=None, n_ctx=1024):
+    return Config(n_layer, n_embd, n_head, n_ctx, vocab_size, ffn_dim or 4 * n_embd)
+
+
+PRESETS = {
+    "small": (12, 768, 12), "medium": (24, 1024, 16),
+    "large": (36, 1280, 20), "xl": (48, 1600, 25),
+}
+
+
+def preset(name):
+    L, E, H = PRESETS[name]
+    return make_config(L, E, H)
+
+
+_vp = C.c_void_p
+_i = C.c_int
+_f = C.c_float
+_sz = C.c_size_t
+
+
+def _sig(name, res, *args):
+    fn = getattr(_lib, name)
+    fn.restype = res
+    fn.argtypes = list(args)
+    return fn
+
+
+_sig("g2_last_error", C.c_char_p)
+for _n, _a in {
+    "g2_init": [_i], "g2_shutdown": [], "g2_device_name": [C.c_char_p, _i, C.POINTER(_i)],
+    "g2_alloc": [C.POINTER(_vp), _sz], "g2_free": [_vp], "g2_upload": [_vp, _vp, _sz],
+    "g2_upload_rect": [_vp, _sz, _vp, _sz, _sz, _sz], "g2_copy": [_vp, _vp, _sz],
+    "g2_download": [_vp, _vp, _sz], "g2_memset": [_vp, _i, _sz], "g2_sync": [],
+    "g2_matmul": [_vp, _vp, _vp, _vp, _i, _i, _i], "g2_matmul_f16": [_vp, _vp, _vp, _vp, _i, _i, _i],
+    "g2_matvec": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i],
+    "g2_matvec_f16": [_vp, _vp, _vp, _vp, _vp, _i, _i, _i],
+    "g2_matvec_sk": [_vp, _vp, _vp, _i, _i, _i], "g2_matvec_sk_f16": [_vp, _vp, _vp, _i, _i, _i],
+    "g2_reduce_partial": [_vp, _vp, _vp, _vp, _i, _i, _i],
+    "g2_layernorm": [_vp, _vp, _vp, _vp, _i, _i], "g2_add": [_vp, _vp, _i], "g2_gelu": [_vp, _i],
+    "g2_embed": [_vp, _vp, _vp, _i, _i, _i, _vp],
+    "g2_split_kv": [_vp, _vp, _vp, _i, _i, _i, _i],
+    "g2_attn_scores_1q": [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f],
+    "g2_attn_softmax_1q": [_vp, _i, _i], "g2_attn_out_1q": [_vp, _vp, _vp, _i, _i, _i, _i],
+    "g2_attn_1q": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f],
+    "g2_config_load": [C.c_char_p, C.POINTER(Config)], "g2_config_parse": [C.c_char_p, C.POINTER(Config)],
+    "g2_model_load": [C.c_char_p, _i, _i, C.POINTER(_vp)],
+    "g2_model_synth": [C.POINTER(Config), C.c_uint64, _i, _i, C.POINTER(_vp)],
+    "g2_model_from_host": [C.POINTER(Config), _vp, _vp, _vp, _vp, C.POINTER(_vp), _i, _i, C.POINTER(_vp)],
+    "g2_model_free": [_vp], "g2_model_config": [_vp, C.POINTER(Config)],
+    "g2_model_set_kslice": [_vp, _i],
+    "g2_prefill": [_vp, _vp, _i], "g2_decode": [_vp, _i, _i], "g2_read_logits": [_vp, _vp, _i],
+    "g2_sample_greedy": [_vp, _vp, _i, _i, _f],
+    "g2_generate": [_vp, _vp, _i, _i, _i, _vp, C.POINTER(C.c_double)],
+    "g2_decode_run": [_vp, _i, _i, _i, _i, _vp, C.POINTER(C.c_double)],
+}.items():
+    _sig(_n, _i, *_a)
+_sig("g2_synth_normal", None, _vp, _sz, C.c_uint64, C.c_uint32, _f)
+_sig("g2_synth_tensor_id", C.c_uint32, _i, _i)
+_sig("g2_convert_f16", None, _vp, _vp, _sz)
+_sig("g2_model_weight_bytes", _sz, _vp)
+
+
+def last_error():
+    return _lib.g2_last_error().decode(errors="replace")
+
+
+def check(rc):
+    if rc < 0:
+        raise G2Error(rc, last_error())
+    return rc
+
+
+def exported_symbols():
+    """Names of every function prototype declared in include/g2hip.h."""
+    import re
+    text = open(HEADER_PATH).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(g2_[a-z0-9_]+)\s*\(", text)))
+
+
+# ---------------------------------------------------------------- runtime
+
+def init(device=0):
+    check(_lib.g2_init(device))
+
+
+def shutdown():
+    check(_lib.g2_shutdown())
+
+
+def device_name():
+    buf = C.create_string_buffer(256)
+    cus = C.c_int(0)
+    check(_lib.g2_device_name(buf, 256, C.byref(cus)))
+    return buf.value.decode(), cus.value
+
+
+def sync():
+    check(_lib.g2_sync())
+
+
+class DevBuf:
+    """A device allocation (freed explicitly or when garbage-collected)."""
+
+    def __init__(self, nbytes):
+        p = _vp()
+        check(_lib.g2_alloc(C.byref(p), nbytes))
+        self.ptr = p.value
+        self.nbytes = nbytes
+
+    @property
+    def value(self):
+        return self.ptr
+
+    def free(self):
+        if self.ptr:
+            _lib.g2_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def offset(self, nbytes):
+        """Raw device pointer nbytes into the buffer (no ownership)."""
+        return self.ptr + nbytes
+
+    def upload(self, arr):
+        arr = np.ascontiguousarray(arr)
+        assert arr.nbytes <= self.nbytes
+        check(_lib.g2_upload(self.ptr, arr.ctypes.data, arr.nbytes))
+        return self
+
+    def download(self, dtype=np.float32, count=None):
+        dtype = np.dtype(dtype)
+        count = self.nbytes // dtype.itemsize if count is None else count
+        out = np.empty(count, dtype=dtype)
+        check(_lib.g2_download(out.ctypes.data, self.ptr, out.nbytes))
+        return out
+
+
+def to_device(arr):
+    arr = np.ascontiguousarray(arr)
+    return DevBuf(max(arr.nbytes, 4)).upload(arr)
+
+
+def _p(x):
+    if x is None:
+        return None
+    if isinstance(x, DevBuf):
+        return x.ptr
+    return int(x)
+
+
+# ---------------------------------------------------------------- operators
+
+def matmul(A, B, bias, Cb, M, N, K, f16=False):
+    fn = _lib.g2_matmul_f16 if f16 else _lib.g2_matmul
+    check(fn(_p(A), _p(B), _p(bias), _p(Cb), M, N, K))
+
+
+def matvec(A, B, bias, residual, Cb, N, K, apply_gelu=0, f16=False):
+    fn = _lib.g2_matvec_f16 if f16 else _lib.g2_matvec
+    check(fn(_p(A), _p(B), _p(bias), _p(residual), _p(Cb), N, K, int(apply_gelu)))
+
+
+def matvec_sk(A, B, partial, N, K, kslice, f16=False):
+    fn = _lib.g2_matvec_sk_f16 if f16 else _lib.g2_matvec_sk
+    check(fn(_p(A), _p(B), _p(partial), N, K, kslice))
+
+
+def reduce_partial(partial, bias, residual, Cb, N, kslice, apply_gelu=0):
+    check(_lib.g2_reduce_partial(_p(partial), _p(bias), _p(residual), _p(Cb), N, kslice, int(apply_gelu)))
+
+
+def layernorm(x, out, gamma, beta, n_embd, seq_len):
+    check(_lib.g2_layernorm(_p(x), _p(out), _p(gamma), _p(beta), n_embd, seq_len))
+
+
+def add(a, b, n):
+    check(_lib.g2_add(_p(a), _p(b), n))
+
+
+def gelu(x, n):
+    check(_lib.g2_gelu(_p(x), n))
+
+
+def embed(wte, wpe, out, n_embd, seq_len, start_pos, ids):
+    check(_lib.g2_embed(_p(wte), _p(wpe), _p(out), n_embd, seq_len, start_pos, _p(ids)))
+
+
+def split_kv(qkv, k_cache, v_cache, start_pos, T, D, max_seq):
+    check(_lib.g2_split_kv(_p(qkv), _p(k_cache), _p(v_cache), start_pos, T, D, max_seq))
+
+
+def attn_scores_1q(qkv, k_cache, scores, q_base, T_kv, D, DH, NH, max_seq, scale):
+    check(_lib.g2_attn_scores_1q(_p(qkv), _p(k_cache), _p(scores), q_base, T_kv, D, DH, NH, max_seq, scale))
+
+
+def attn_softmax_1q(scores, T_kv, NH):
+    check(_lib.g2_attn_softmax_1q(_p(scores), T_kv, NH))
+
+
+def attn_out_1q(scores, v_cache, out, T_kv, D, DH, out_base):
+    check(_lib.g2_attn_out_1q(_p(scores), _p(v_cache), _p(out), T_kv, D, DH, out_base))
+
+
+def attn_1q(qkv, k_cache, v_cache, out, q_base, T_kv, D, NH, max_seq, out_base, scale):
+    check(_lib.g2_attn_1q(_p(qkv), _p(k_cache), _p(v_cache), _p(out), q_base, T_kv, D, NH,
+                          max_seq, out_base, scale))
+
+
+# ---------------------------------------------------------------- host-only
+
+def config_parse(json_text):
+    cfg = Config()
+    check(_lib.g2_config_parse(json_text.encode(), C.byref(cfg)))
+    return cfg
+
+
+def config_load(directory):
+    cfg = Config()
+    check(_lib.g2_config_load(directory.encode(), C.byref(cfg)))
+    return cfg
+
+
+def synth_normal(n, seed, tensor_id, std=0.02):
+    out = np.empty(n, dtype=np.float32)
+    _lib.g2_synth_normal(out.ctypes.data, n, seed, tensor_id, std)
+    return out
+
+
+def synth_tensor_id(layer, which):
+    return _lib.g2_synth_tensor_id(layer, which)
+
+
+def convert_f16(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    _lib.g2_convert_f16(out.ctypes.data, x.ctypes.data, x.size)
+    return out
+
+
+def synth_weights(cfg, seed, f16_round=False):
+    """Host copy of the synthetic random-init weights g2_model_synth builds:
+    dict with wte [V,E], wpe [1024,E], lnf_w, lnf_b and `layers`, a list of
+    12-tuples (ln1_w, ln1_b, qkv_w, qkv_b, proj_w, proj_b, ln2_w, ln2_b, fc_w,
+    fc_b, fc2_w, fc2_b) with matrices in the Conv1D [in,out] layout.  With
+    f16_round the matrices and embeddings are rounded to fp16 values (kept
+    as float32), i.e. what the fp16 weight format stores."""
+    E, F, V = cfg.n_embd, cfg.ffn_dim, cfg.vocab_size
+
+    def rnd(a):
+        return a.astype(np.float16).astype(np.float32) if f16_round else a
+
+    wte = rnd(synth_normal(V * E, seed, synth_tensor_id(-1, 1)).reshape(V, E))
+    wpe = rnd(synth_normal(MAX_SEQ * E, seed, synth_tensor_id(-1, 2)).reshape(MAX_SEQ, E))
+    ones_e, zeros_e = np.ones(E, np.float32), np.zeros(E, np.float32)
+    layers = []
+    for l in range(cfg.n_layer):
+        mats = []
+        for w, (i, o) in enumerate([(E, 3 * E), (E, E), (E, F), (F, E)]):
+            mats.append(rnd(synth_normal(i * o, seed, synth_tensor_id(l, w)).reshape(i, o)))
+        layers.append((ones_e, zeros_e, mats[0], np.zeros(3 * E, np.float32), mats[1], zeros_e,
+                       ones_e, zeros_e, mats[2], np.zeros(F, np.float32), mats[3], zeros_e))
+    return {"wte": wte, "wpe": wpe, "lnf_w": ones_e, "lnf_b": zeros_e, "layers": layers}
+
+
+# ---------------------------------------------------------------- model
+
+class Model:
+    """A GPT-2 model resident on the GPU (g2_model handle)."""
+
+    def __init__(self, handle):
+        self.h = handle
+        cfg = Config()
+        check(_lib.g2_model_config(self.h, C.byref(cfg)))
+        self.cfg = cfg
+
+    @classmethod
+    def synth(cls, cfg, seed, dtype=F32, path=PATH_FUSED):
+        h = _vp()
+        check(_lib.g2_model_synth(C.byref(cfg), seed, dtype, path, C.byref(h)))
+        return cls(h.value)
+
+    @classmethod
+    def load(cls, directory, dtype=F32, path=PATH_FUSED):
+        h = _vp()
+        check(_lib.g2_model_load(directory.encode(), dtype, path, C.byref(h)))
+        return cls(h.value)
+
+    @classmethod
+    def from_host(cls, cfg, weights, dtype=F32, path=PATH_FUSED):
+        keep = []
+
+        def ptr(a):
+            a = np.ascontiguousarray(a, dtype=np.float32)
+            keep.append(a)
+            return a.ctypes.data
+
+        flat = (_vp * (12 * cfg.n_layer))()
+        for l, lw in enumerate(weights["layers"]):
+            for s, a in enumerate(lw):
+                flat[12 * l + s] = ptr(a)
+        h = _vp()
+        check(_lib.g2_model_from_host(C.byref(cfg), ptr(weights["wte"]), ptr(weights["wpe"]),
+                                      ptr(weights["lnf_w"]), ptr(weights["lnf_b"]), flat,
+                                      dtype, path, C.byref(h)))
+        return cls(h.value)
+
+    def free(self):
+        if self.h:
+            _lib.g2_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def set_kslice(self, ks):
+        check(_lib.g2_model_set_kslice(self.h, ks))
+
+    def weight_bytes(self):
+        return _lib.g2_model_weight_bytes(self.h)
+
+    def prefill(self, ids):
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        check(_lib.g2_prefill(self.h, ids.ctypes.data, len(ids)))
+
+    def decode(self, token, pos):
+        check(_lib.g2_decode(self.h, int(token), int(pos)))
+
+    def logits(self, n=None):
+        n = self.cfg.vocab_size if n is None else n
+        out = np.empty(n, dtype=np.float32)
+        check(_lib.g2_read_logits(self.h, out.ctypes.data, n))
+        return out
+
+    def sample_greedy(self, ctx, forbid_eos=False, rep_penalty=1.0):
+        ctx = np.ascontiguousarray(ctx, dtype=np.int32)
+        return check(_lib.g2_sample_greedy(self.h, ctx.ctypes.data, len(ctx), int(forbid_eos), rep_penalty))
+
+    def generate(self, prompt, max_new, min_new=None):
+        prompt = np.ascontiguousarray(prompt, dtype=np.int32)
+        min_new = max_new if min_new is None else min_new
+        out = np.empty(MAX_SEQ, dtype=np.int32)
+        t = (C.c_double * 2)()
+        n = check(_lib.g2_generate(self.h, prompt.ctypes.data, len(prompt), max_new, min_new,
+                                   out.ctypes.data, t))
+        return out[:n].copy(), (t[0], t[1])
+
+    def decode_run(self, token, start_pos, n_steps, forbid_eos=True):
+        out = np.empty(n_steps, dtype=np.int32)
+        ms = C.c_double(0)
+        check(_lib.g2_decode_run(self.h, int(token), int(start_pos), int(n_steps), int(forbid_eos),
+                                 out.ctypes.data, C.byref(ms)))
+        return out, ms.value
