@@ -1,0 +1,167 @@
+#!/usr/bin/env python3
+"""Benchmark: GPT-2 XL (1.5B) fp16-weight batch-1 greedy decode on one MI355X.
+
+Workload (the configuration the headline metric is quoted on): GPT-2 XL
+(48 layers, n_embd 1600, 25 heads, ffn 6400, vocab 50257), fp16 weights with
+fp32 accumulation, synthetic random-init weights N(0, 0.02), a 512-token
+random prompt, then greedy decoding to fill the 1024-position context.
+
+One step = the workload's whole decode phase: 511 greedy decode forwards at
+positions 512..1022, each selecting its token on the device and feeding it
+to the next, replayed from the same prefilled KV cache every step.  The
+timed region covers K steps; `value` is decode tokens per second over it.
+Prefill throughput (prompt tokens / prefill time) is reported beside it.
+
+roofline: the dominant kernel is the decode step itself (one replayed graph
+per token); achieved = algorithmic bytes per step / the step's mean duration
+from HIP events on the library stream, bytes per token from the formula
+  w*(L*(3E^2 + E^2 + 2EF) + E*V) + kvb*2*L*E*T + 4*(13*L*E + 2E) + w*2E + kvb*2*L*E
+(weights, K/V reads over T = pos+1 positions, biases and LayerNorm
+parameters, embedding rows, K/V writes), against MI355X's 8 TB/s HBM peak.
+
+cpu_baseline: the CPU oracle (a C restatement of the reference kernels with
+their accumulation order) on the host's cores, decoding a bounded sample of
+the same workload -- a few forwards at positions 512.. over the KV cache the
+GPU prefill produced.
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "gpt2-opencl-1.1_amd"))
+
+METRIC = "batch-1 decode tok/s + % HBM roofline (GPT-2 XL fp16); prefill tok/s"
+SEED = 0x67707432
+PROMPT_LEN = 512
+HBM_PEAK_GBS = 8000.0
+
+
+def step_bytes(cfg, w_bytes, kv_bytes, positions):
+    """Algorithmic HBM bytes of decode forwards at the given positions."""
+    L, E, F, V = cfg.n_layer, cfg.n_embd, cfg.ffn_dim, cfg.vocab_size
+    fixed = w_bytes * (L * (3 * E * E + E * E + 2 * E * F) + E * V) + 4 * (13 * L * E + 2 * E) \
+        + w_bytes * 2 * E + kv_bytes * 2 * L * E
+    return sum(fixed + kv_bytes * 2 * L * E * (p + 1) for p in positions)
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(g2, m, cfg, token, n_steps=4):
+    """Time the oracle on the same workload sample: n_steps decode forwards
+    at positions 512.. over the GPU-prefilled KV cache."""
+    sys.path.insert(0, ROOT)
+    from oracle import oracle
+    t0 = time.perf_counter()
+    w = g2.synth_weights(cfg, SEED, f16_round=True)
+    om = oracle.Model(cfg, w, kslice=4)
+    del w
+    for l in range(cfg.n_layer):
+        k, v = m.read_kv(l)
+        om.set_kv(l, k, v)
+    log(f"cpu oracle ready in {time.perf_counter() - t0:.1f}s")
+    om.decode(token, PROMPT_LEN)  # untimed first forward (page-in)
+    tok = om.greedy([token], forbid_eos=True)
+    t0 = time.perf_counter()
+    for s in range(n_steps):
+        om.decode(tok, PROMPT_LEN + 1 + s)
+        tok = om.greedy([tok], forbid_eos=True)
+    dt = time.perf_counter() - t0
+    cores = oracle.num_threads()
+    om.close()
+    return {"value": round(n_steps / dt, 3), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"{n_steps} greedy decode forwards of GPT-2 XL (fp16-rounded weights held as fp32) at "
+                      f"positions {PROMPT_LEN + 1}..{PROMPT_LEN + n_steps} over the GPU-prefilled KV cache, "
+                      f"{cores} OpenMP threads, {dt:.2f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--config", default="xl", choices=["small", "medium", "large", "xl"])
+    ap.add_argument("--fp32", action="store_true", help="fp32 weights instead of fp16")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} (WORLD_SIZE {world}) is not "
+              f"supported. The batch-1 decode shards by output columns across GPUs only in design "
+              f"(see DESIGN.md); run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import g2hip as g2
+    g2.init(0)
+    name, cus = g2.device_name()
+    cfg = g2.preset(args.config)
+    f16 = not args.fp32
+    wdtype = g2.F16 if f16 else g2.F32
+    t0 = time.perf_counter()
+    m = g2.Model.synth(cfg, SEED, wdtype, g2.PATH_FUSED)
+    log(f"{args.config} model on {name} ({cus} CUs) in {time.perf_counter() - t0:.1f}s, "
+        f"{m.weight_bytes() / 2**20:.0f} MiB of weights")
+    prompt = np.random.default_rng(SEED).integers(0, cfg.vocab_size, PROMPT_LEN).astype(np.int32)
+    P = PROMPT_LEN
+    n_dec = 1023 - P
+
+    # prefill: prompt -> first token (device-selected), timed by HIP events
+    ids, _ = m.generate(prompt, 2)  # warm-up, builds the decode graph
+    prefill_ms = []
+    for _ in range(3):
+        ids, (pf_ms, _) = m.generate(prompt, 1)
+        prefill_ms.append(pf_ms)
+    first_tok = int(ids[0])
+    prefill_tok_s = P / (min(prefill_ms) * 1e-3)
+
+    # decode: W untimed steps, then K timed steps of 511 forwards each
+    for _ in range(args.warmup):
+        ref_ids, _ = m.decode_run(first_tok, P, n_dec)
+    g2.sync()
+    ev_ms = []
+    t_start = time.perf_counter()
+    for _ in range(args.steps):
+        out, ms = m.decode_run(first_tok, P, n_dec)
+        ev_ms.append(ms)
+        if not np.array_equal(out, ref_ids):
+            raise SystemExit("bench.py: decode steps disagree with each other (non-deterministic output)")
+    g2.sync()
+    wall = time.perf_counter() - t_start
+    tok_s = args.steps * n_dec / wall
+    step_ms_events = float(np.mean(ev_ms))
+    bytes_step = step_bytes(cfg, 2 if f16 else 4, 4, range(P, P + n_dec))
+    achieved = bytes_step / (step_ms_events * 1e-3) / 1e9
+
+    result = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": f"GPT-2 {args.config.upper()} {'fp16' if f16 else 'fp32'}-weight batch-1 greedy "
+                               f"decode: {P}-token random prompt, {n_dec} decode forwards (positions {P}..{P + n_dec - 1})",
+                   "weights": "f16" if f16 else "f32", "kv_cache": "f32", "accumulate": "f32",
+                   "decode_graph_replay": bool(m.uses_graph() == 1)},
+        "prefill_tok_s": round(prefill_tok_s, 1),
+        "prefill_ms": round(min(prefill_ms), 3),
+        "decode_ms_per_token": round(step_ms_events / n_dec, 4),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "decode step (one replayed graph per token)",
+                     "bytes_per_launch": round(bytes_step / n_dec)},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(g2, m, cfg, first_tok)
+    print(json.dumps(result), flush=True)
+    m.free()
+
+
+if __name__ == "__main__":
+    main()

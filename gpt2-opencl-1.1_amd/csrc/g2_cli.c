@@ -108,6 +108,7 @@ int main(int argc, char **argv)
     printf("Generated:");
     for (int i = 0; i < n; ++i) printf(" %d", out[i]);
     printf("\n");
+    printf("Decode graph replay: %d\n", g2_model_uses_graph(m));
     fprintf(stderr,
             "Timing:\n"
             "  prefill+first : %9.3f ms (%d prompt tokens, %.1f tok/s)\n"

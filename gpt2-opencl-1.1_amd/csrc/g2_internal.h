@@ -15,6 +15,16 @@
 #include "g2hip.h"
 #include "g2_kargs.h"
 
+/* Packed-matvec kernels of one epilogue: f32/f16 twins of the three lane
+ * shapes (64 lanes x 4 chunks, 256 x 4, 256 x 8), see g2i_rows_kernel. */
+#define G2_ROWS_LIST(X, E, s)                                                 \
+    X(ROWS_##E##_F32_64, "g2k_rows_" s "_f32_64")                             \
+    X(ROWS_##E##_F16_64, "g2k_rows_" s "_f16_64")                             \
+    X(ROWS_##E##_F32_256, "g2k_rows_" s "_f32_256")                           \
+    X(ROWS_##E##_F16_256, "g2k_rows_" s "_f16_256")                           \
+    X(ROWS_##E##_F32_256X8, "g2k_rows_" s "_f32_256x8")                       \
+    X(ROWS_##E##_F16_256X8, "g2k_rows_" s "_f16_256x8")
+
 /* Kernel table: index -> symbol name in the gfx950 code object. */
 #define G2_KERNEL_LIST(X)                                                     \
     X(MVKN_F32, "g2k_mvkn_f32") X(MVKN_F32_S, "g2k_mvkn_f32_s")               \
@@ -25,19 +35,11 @@
     X(EMBED_F32, "g2k_embed_f32") X(EMBED_F16, "g2k_embed_f16")               \
     X(SPLIT_KV, "g2k_split_kv") X(ATTN_SCORES, "g2k_attn_scores")             \
     X(ATTN_SOFTMAX, "g2k_attn_softmax") X(ATTN_OUT, "g2k_attn_out")           \
-    X(ATTN_1Q, "g2k_attn_1q")                                                 \
-    X(ROWS_F32_STORE, "g2k_rows_f32_store")                                   \
-    X(ROWS_F16_STORE, "g2k_rows_f16_store")                                   \
-    X(ROWS_F32_LN_STORE, "g2k_rows_f32_ln_store")                             \
-    X(ROWS_F16_LN_STORE, "g2k_rows_f16_ln_store")                             \
-    X(ROWS_F32_LN_QKV, "g2k_rows_f32_ln_qkv")                                 \
-    X(ROWS_F16_LN_QKV, "g2k_rows_f16_ln_qkv")                                 \
-    X(ROWS_F32_RESID, "g2k_rows_f32_resid")                                   \
-    X(ROWS_F16_RESID, "g2k_rows_f16_resid")                                   \
-    X(ROWS_F32_LN_GELU, "g2k_rows_f32_ln_gelu")                               \
-    X(ROWS_F16_LN_GELU, "g2k_rows_f16_ln_gelu")                               \
-    X(ROWS_F32_LN_ARGMAX, "g2k_rows_f32_ln_argmax")                           \
-    X(ROWS_F16_LN_ARGMAX, "g2k_rows_f16_ln_argmax")                           \
+    X(ATTN_PART, "g2k_attn_part") X(ATTN_PART_S, "g2k_attn_part_s")           \
+    X(ATTN_MERGE, "g2k_attn_merge") X(ARGMAX_MERGE, "g2k_argmax_merge")       \
+    G2_ROWS_LIST(X, STORE, "store") G2_ROWS_LIST(X, LN_QKV, "ln_qkv")         \
+    G2_ROWS_LIST(X, RESID, "resid") G2_ROWS_LIST(X, LN_GELU, "ln_gelu")       \
+    G2_ROWS_LIST(X, LN_ARGMAX, "ln_argmax")                                   \
     X(GEMM_KN_F32, "g2k_gemm_kn_f32") X(GEMM_KN_F16, "g2k_gemm_kn_f16")       \
     X(GEMM_NK_F32_STORE, "g2k_gemm_nk_f32_store")                             \
     X(GEMM_NK_F16_STORE, "g2k_gemm_nk_f16_store")                             \
@@ -53,10 +55,10 @@
 enum { G2_KERNEL_LIST(G2_ENUM_ENTRY) G2F_COUNT };
 #undef G2_ENUM_ENTRY
 
-/* Rows per work-group of the packed matvec kernels (4 waves x 2 rows). */
-#define G2_ROWS_PER_WG 8
-/* Largest K the packed matvec accepts (its LDS input vector). */
+/* Largest K of the fused model's packed matvecs (GPT-2 XL ffn). */
 #define G2_ROWS_MAXK 6400
+/* Cap on packed-matvec work-groups (8 per CU); longer matrices grid-stride. */
+#define G2_ROWS_MAX_GRID 2048
 /* Key chunk of the single-query attention kernel and chunks per head. */
 #define G2_ATTN_CHUNK 64
 #define G2_ATTN_MAX_CHUNKS (G2_KV_MAX_SEQ / G2_ATTN_CHUNK)
@@ -70,6 +72,13 @@ int g2i_ready(void);
 hipStream_t g2i_stream(void);
 int g2i_launch(int fid, unsigned gx, unsigned gy, unsigned bx, void *args);
 int g2i_device_alloc(void **p, size_t bytes);
+/* Launch a packed-matvec kernel: fid_f32_64 is the epilogue's first table
+ * entry (f32, 64-lane shape); the lane shape and grid follow from K. */
+int g2i_rows_launch(int fid_f32_64, int f16, g2_rows_args *a);
+/* Work-groups g2i_rows_launch uses for N rows of K (0 if K is invalid). */
+unsigned g2i_rows_grid(int N, int K, int f16);
+/* Single-query attention: partials over `chunks` key chunks, then merge. */
+int g2i_attn_launch(g2_attn1q_args *a, unsigned chunks);
 
 /* host helpers (g2_host.c) */
 void g2i_f32_to_f16(uint16_t *dst, const float *src, size_t n);

@@ -123,9 +123,9 @@ typedef struct {
     int T, D, DH, out_base;
 } g2_attnout_args;
 
-/* Single-query attention, head dim 64, split over key chunks with an
- * in-kernel merge.  T = T_fixed if > 0, else state[G2S_POS] + 1.
- * part: [NH][max_chunks][2 + 64] floats; counter: [NH] (zero between uses). */
+/* Single-query attention, head dim 64, split over 64-position key chunks
+ * (partials kernel) and merged by a second kernel.  T = T_fixed if > 0,
+ * else state[G2S_POS] + 1.  part: [NH][max_chunks][2 + 64] floats. */
 typedef struct {
     const float *q;
     const float *k_cache;
@@ -133,7 +133,6 @@ typedef struct {
     float *out;
     const int *state;
     float *part;
-    unsigned *counter;
     int T_fixed, D, NH, S, max_chunks;
     float scale;
 } g2_attn1q_args;
@@ -143,9 +142,8 @@ typedef struct {
  * ln_g/ln_b when the LN variant is used.  Epilogue by kernel variant:
  * store y = acc + bias; gelu; resid y = y + (acc + bias);
  * qkv (q_out / k_cache / v_cache at state[G2S_POS]);
- * argmax: y = acc (logits), first-max argmax with EOS masked while
- * state[G2S_NGEN] < state[G2S_MIN_NEW], merged by the last work-group, which
- * then appends the id to state[G2S_IDS + NGEN], sets TOK, POS+1 and NGEN+1. */
+ * argmax: y = acc (logits) and each work-group's first-max (value, index)
+ * to part[2b], with EOS masked while state[G2S_NGEN] < state[G2S_MIN_NEW]. */
 typedef struct {
     const void *W;
     const float *x;
@@ -158,10 +156,15 @@ typedef struct {
     float *v_cache;
     int *state;
     float *part;
-    unsigned *counter;
     int N, K, E, S;
-    int advance;          /* argmax: 1 = update POS/TOK/NGEN, 0 = only IDS/TOK */
 } g2_rows_args;
+
+/* Greedy pick over the lm_head work-groups' (value, index) partials. */
+typedef struct {
+    const float *part;
+    int *state;
+    int n_parts, N, advance;
+} g2_amerge_args;
 
 /* Causal attention over a prompt block: rows i < P of q[P,E]; keys/values
  * j <= i from the transposed K cache and the V cache; head dim 64. */

@@ -338,308 +338,6 @@ extern "C" __global__ __launch_bounds__(1024) void g2k_attn_out(const g2_attnout
 }
 
 /* ======================================================================
- * Single-query attention, head dim 64 (fused scores -> softmax -> PV)
- *
- * grid (NH, max_chunks), 256 threads.  Work-group (h, c) takes positions
- * [64c, 64c+64) of head h: scores with lanes over positions (transposed K,
- * 256-byte rows), a chunk-local softmax, the weighted V sum with lanes over
- * the 64 dims, then writes (max, sum, o[64]) to part.  The last work-group
- * of a head to finish (agent-scope counter) merges the chunk partials in
- * chunk order with the usual max-rescaling and writes out[h*64 .. +64].
- * ==================================================================== */
-G2K void g2k_attn_1q(const g2_attn1q_args a)
-{
-    __shared__ float qs[64];
-    __shared__ float pr[64];
-    __shared__ float red[4][64];
-    __shared__ float stat[2];
-    __shared__ int is_last;
-    const int h = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
-    const int T = clampi(a.T_fixed > 0 ? a.T_fixed : a.state[G2S_POS] + 1, 1, a.S);
-    const int nch = (T + 63) >> 6;
-    if (h >= a.NH || c >= nch || nch > a.max_chunks) return;
-    const int j0 = c * 64;
-    if (tid < 64) qs[tid] = a.q[h * 64 + tid];
-    __syncthreads();
-    {
-        const int jj = tid & 63, dg = tid >> 6, j = j0 + jj;
-        float s = 0.f;
-        if (j < T) {
-            const float *kp = a.k_cache + (size_t)(h * 64 + dg * 16) * a.S + j;
-#pragma unroll
-            for (int d = 0; d < 16; ++d) s = fmaf(qs[dg * 16 + d], kp[(size_t)d * a.S], s);
-        }
-        red[dg][jj] = s;
-    }
-    __syncthreads();
-    if (tid < 64) {
-        const bool ok = j0 + tid < T;
-        const float s = (((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid]) * a.scale;
-        const float m = wave_max(ok ? s : -INFINITY);
-        const float p = ok ? expf(s - m) : 0.f;
-        const float l = wave_sum(p);
-        pr[tid] = p;
-        if (tid == 0) { stat[0] = m; stat[1] = l; }
-    }
-    __syncthreads();
-    {
-        const int d = tid & 63, jg = tid >> 6;
-        float o = 0.f;
-#pragma unroll 4
-        for (int i = 0; i < 16; ++i) {
-            const int jj = jg + 4 * i, j = j0 + jj;
-            if (j < T) o = fmaf(pr[jj], a.v_cache[(size_t)j * a.D + h * 64 + d], o);
-        }
-        red[jg][d] = o;
-    }
-    __syncthreads();
-    const float o = tid < 64 ? ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid] : 0.f;
-    if (nch == 1) {
-        if (tid < 64) a.out[h * 64 + tid] = o / stat[1];
-        return;
-    }
-    float *pp = a.part + ((size_t)h * a.max_chunks + c) * 66;
-    if (tid < 64) {
-        st_agent(pp + 2 + tid, o);
-        if (tid == 0) { st_agent(pp, stat[0]); st_agent(pp + 1, stat[1]); }
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned old = atomicAdd(&a.counter[h], 1u);
-        is_last = (old == (unsigned)(nch - 1));
-    }
-    __syncthreads();
-    if (!is_last) return;
-    __threadfence();
-    if (tid < 64) {
-        const float *hp = a.part + (size_t)h * a.max_chunks * 66;
-        float M = -INFINITY;
-        for (int cc = 0; cc < nch; ++cc) M = fmaxf(M, ld_agent(hp + (size_t)cc * 66));
-        float L = 0.f, acc = 0.f;
-        for (int cc = 0; cc < nch; ++cc) {
-            const float w = expf(ld_agent(hp + (size_t)cc * 66) - M);
-            L = fmaf(ld_agent(hp + (size_t)cc * 66 + 1), w, L);
-            acc = fmaf(ld_agent(hp + (size_t)cc * 66 + 2 + tid), w, acc);
-        }
-        a.out[h * 64 + tid] = acc / L;
-    }
-    if (tid == 0) a.counter[h] = 0u;
-}
-
-/* ======================================================================
- * Fused row-major matvec over packed weights W[N,K] (decode hot path)
- *
- * 256 threads; wave w of work-group b takes R consecutive rows starting at
- * (b*4 + w)*R and strides by gridDim.x*4*R.  Lanes stream 16-byte chunks of
- * each row (4 fp32 or 8 fp16 weights), U chunks per row in flight, and
- * multiply them with the input vector held in LDS; a butterfly over the wave
- * gives the row sum.  The input vector is x, or LayerNorm(x) computed by
- * every work-group in its prologue.
- * ==================================================================== */
-enum { EPI_STORE = 0, EPI_GELU = 1, EPI_RESID = 2, EPI_QKV = 3, EPI_ARGMAX = 4 };
-
-template <typename WT> struct chunk_t;
-template <> struct chunk_t<float> { typedef f32x4 T; static constexpr int V = 4; };
-template <> struct chunk_t<_Float16> { typedef f16x8 T; static constexpr int V = 8; };
-
-template <typename WT>
-__device__ __forceinline__ float chunk_dot(const typename chunk_t<WT>::T &w, const float *xs)
-{
-    if constexpr (sizeof(WT) == 4) {
-        const f32x4 x = *(const f32x4 *)xs;
-        float s = w.x * x.x;
-        s = fmaf(w.y, x.y, s);
-        s = fmaf(w.z, x.z, s);
-        return fmaf(w.w, x.w, s);
-    } else {
-        const f32x4 x0 = *(const f32x4 *)xs;
-        const f32x4 x1 = *(const f32x4 *)(xs + 4);
-        float s = (float)w[0] * x0.x;
-        s = fmaf((float)w[1], x0.y, s);
-        s = fmaf((float)w[2], x0.z, s);
-        s = fmaf((float)w[3], x0.w, s);
-        s = fmaf((float)w[4], x1.x, s);
-        s = fmaf((float)w[5], x1.y, s);
-        s = fmaf((float)w[6], x1.z, s);
-        return fmaf((float)w[7], x1.w, s);
-    }
-}
-
-/* Better (value, index) under first-max: larger value, then lower index. */
-__device__ __forceinline__ bool am_better(float v1, int i1, float v2, int i2)
-{
-    return v1 > v2 || (v1 == v2 && i1 < i2);
-}
-
-template <typename WT, int EPI, bool LN, int R, int U>
-__device__ void rows_impl(const g2_rows_args &a)
-{
-    typedef typename chunk_t<WT>::T CT;
-    constexpr int V = chunk_t<WT>::V;
-    __shared__ __attribute__((aligned(16))) float xs[G2_MAXK];
-    __shared__ float red4[4];
-    __shared__ float amv[256];
-    __shared__ int ami[256];
-    __shared__ int is_last;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int K = a.K, N = a.N, C = K / V;
-
-    /* prologue: input vector (optionally LayerNorm'd) into LDS */
-    if (LN) {
-        float s = 0.f;
-        for (int k = tid; k < K; k += 256) {
-            const float v = a.x[k];
-            xs[k] = v;
-            s += v;
-        }
-        const float mean = block_sum(s, red4) / (float)K;
-        float q = 0.f;
-        for (int k = tid; k < K; k += 256) {
-            const float d = xs[k] - mean;
-            q = fmaf(d, d, q);
-        }
-        const float inv = 1.0f / sqrtf(block_sum(q, red4) / (float)K + 1e-5f);
-        for (int k = tid; k < K; k += 256)
-            xs[k] = fmaf((xs[k] - mean) * inv, a.ln_g[k], a.ln_b[k]);
-    } else {
-        for (int k = tid; k < K; k += 256) xs[k] = a.x[k];
-    }
-    __syncthreads();
-
-    int pos = 0;
-    if (EPI == EPI_QKV) pos = clampi(a.state[G2S_POS], 0, a.S - 1);
-    float best_v = -INFINITY;
-    int best_i = 0x7fffffff;
-    int masked = -1;
-    if (EPI == EPI_ARGMAX)
-        masked = a.state[G2S_NGEN] < a.state[G2S_MIN_NEW] ? G2_EOS_ID : -1;
-
-    const CT *W = (const CT *)a.W;
-    for (int row0 = (blockIdx.x * 4 + wave) * R; row0 < N; row0 += gridDim.x * 4 * R) {
-        float acc[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = 0.f;
-        for (int c0 = lane; c0 < C; c0 += 64 * U) {
-            CT w[R][U];
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const int c = c0 + 64 * u;
-                    if (c < C && row0 + r < N) w[r][u] = W[(size_t)(row0 + r) * C + c];
-                }
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const int c = c0 + 64 * u;
-                    if (c < C && row0 + r < N) acc[r] += chunk_dot<WT>(w[r][u], xs + c * V);
-                }
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = wave_sum(acc[r]);
-        float v = acc[0];
-#pragma unroll
-        for (int r = 1; r < R; ++r)
-            if (lane == r) v = acc[r];
-        const int n = row0 + lane;
-        if (lane < R && n < N) {
-            if (EPI == EPI_STORE) {
-                if (a.bias) v += a.bias[n];
-                a.y[n] = v;
-            } else if (EPI == EPI_GELU) {
-                if (a.bias) v += a.bias[n];
-                a.y[n] = gelu_f(v);
-            } else if (EPI == EPI_RESID) {
-                if (a.bias) v += a.bias[n];
-                a.y[n] = v + a.y[n];
-            } else if (EPI == EPI_QKV) {
-                if (a.bias) v += a.bias[n];
-                const int E = a.E;
-                if (n < E) a.q_out[n] = v;
-                else if (n < 2 * E) a.k_cache[(size_t)(n - E) * a.S + pos] = v;
-                else a.v_cache[(size_t)pos * E + (n - 2 * E)] = v;
-            } else {
-                a.y[n] = v;
-                const float mv = (n == masked) ? -1e30f : v;
-                if (am_better(mv, n, best_v, best_i)) { best_v = mv; best_i = n; }
-            }
-        }
-    }
-
-    if (EPI == EPI_ARGMAX) {
-        amv[tid] = best_v;
-        ami[tid] = best_i;
-        __syncthreads();
-        for (int s = 128; s > 0; s >>= 1) {
-            if (tid < s && am_better(amv[tid + s], ami[tid + s], amv[tid], ami[tid])) {
-                amv[tid] = amv[tid + s];
-                ami[tid] = ami[tid + s];
-            }
-            __syncthreads();
-        }
-        if (tid == 0) {
-            st_agent(a.part + 2 * blockIdx.x, amv[0]);
-            st_agent(a.part + 2 * blockIdx.x + 1, __int_as_float(ami[0]));
-        }
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) {
-            const unsigned old = atomicAdd(a.counter, 1u);
-            is_last = (old == gridDim.x - 1);
-        }
-        __syncthreads();
-        if (!is_last) return;
-        __threadfence();
-        float bv = -INFINITY;
-        int bi = 0x7fffffff;
-        for (int b = tid; b < (int)gridDim.x; b += 256) {
-            const float v = ld_agent(a.part + 2 * b);
-            const int i = __float_as_int(ld_agent(a.part + 2 * b + 1));
-            if (am_better(v, i, bv, bi)) { bv = v; bi = i; }
-        }
-        amv[tid] = bv;
-        ami[tid] = bi;
-        __syncthreads();
-        for (int s = 128; s > 0; s >>= 1) {
-            if (tid < s && am_better(amv[tid + s], ami[tid + s], amv[tid], ami[tid])) {
-                amv[tid] = amv[tid + s];
-                ami[tid] = ami[tid + s];
-            }
-            __syncthreads();
-        }
-        if (tid == 0) {
-            const int tok = (ami[0] >= 0 && ami[0] < N) ? ami[0] : 0;
-            const int ng = clampi(a.state[G2S_NGEN], 0, G2S_WORDS - G2S_IDS - 1);
-            a.state[G2S_IDS + ng] = tok;
-            a.state[G2S_TOK] = tok;
-            if (a.advance) {
-                a.state[G2S_NGEN] = ng + 1;
-                a.state[G2S_POS] = a.state[G2S_POS] + 1;
-            }
-            *a.counter = 0u;
-        }
-    }
-}
-
-#define G2_ROWS(name, WT, EPI, LN, R, U) \
-    G2K void name(const g2_rows_args a) { rows_impl<WT, EPI, LN, R, U>(a); }
-
-G2_ROWS(g2k_rows_f32_store, float, EPI_STORE, false, 2, 4)
-G2_ROWS(g2k_rows_f16_store, _Float16, EPI_STORE, false, 2, 4)
-G2_ROWS(g2k_rows_f32_ln_store, float, EPI_STORE, true, 2, 4)
-G2_ROWS(g2k_rows_f16_ln_store, _Float16, EPI_STORE, true, 2, 4)
-G2_ROWS(g2k_rows_f32_ln_qkv, float, EPI_QKV, true, 2, 4)
-G2_ROWS(g2k_rows_f16_ln_qkv, _Float16, EPI_QKV, true, 2, 4)
-G2_ROWS(g2k_rows_f32_resid, float, EPI_RESID, false, 2, 4)
-G2_ROWS(g2k_rows_f16_resid, _Float16, EPI_RESID, false, 2, 4)
-G2_ROWS(g2k_rows_f32_ln_gelu, float, EPI_GELU, true, 2, 4)
-G2_ROWS(g2k_rows_f16_ln_gelu, _Float16, EPI_GELU, true, 2, 4)
-G2_ROWS(g2k_rows_f32_ln_argmax, float, EPI_ARGMAX, true, 2, 4)
-G2_ROWS(g2k_rows_f16_ln_argmax, _Float16, EPI_ARGMAX, true, 2, 4)
-
-/* ======================================================================
  * MFMA GEMM (prefill and the reference matmul)
  *
  * Tile 64x64x16, 256 threads = 2x2 waves of 32x32, each wave a 2x2 grid of
@@ -854,3 +552,6 @@ G2K void g2k_attn_prefill(const g2_attnp_args a)
         for (int d = 0; d < 16; ++d) a.out[(size_t)i * a.E + h * 64 + g * 16 + d] = o[d] * inv;
     }
 }
+
+/* Fused decode kernels (packed matvecs, single-query attention). */
+#include "g2_decode.hip"

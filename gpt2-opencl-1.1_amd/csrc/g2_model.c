@@ -49,7 +49,6 @@ struct g2_model {
     /* fused path */
     int *state;
     float *att_part, *am_part;
-    unsigned *att_cnt, *am_cnt;
     hipGraphExec_t step_exec;
     int graph_state; /* 0 not built, 1 ready, -1 capture unsupported */
     hipEvent_t ev[3];
@@ -163,8 +162,8 @@ static int alloc_workspaces(g2_model *m)
     A(m->logits, V * 4); A(m->ids_dev, S * 4); A(m->partial, 8 * V * 4);
     A(m->scores, NH * S * 4); A(m->q, S * E * 4);
     A(m->state, G2S_WORDS * 4);
-    A(m->att_part, NH * G2_ATTN_MAX_CHUNKS * 66 * 4); A(m->att_cnt, NH * 4);
-    A(m->am_part, 2 * 8192 * 4); A(m->am_cnt, 64);
+    A(m->att_part, NH * G2_ATTN_MAX_CHUNKS * 66 * 4);
+    A(m->am_part, 2 * 8192 * 4);
     for (int l = 0; l < m->cfg.n_layer && !rc; ++l) {
         A(m->L[l].k_cache, E * S * 4);
         A(m->L[l].v_cache, S * E * 4);
@@ -172,8 +171,6 @@ static int alloc_workspaces(g2_model *m)
         if (!rc) rc = g2i_hip(hipMemsetAsync(m->L[l].v_cache, 0, E * S * 4, g2i_stream()), "kv clear");
     }
 #undef A
-    if (!rc) rc = g2i_hip(hipMemsetAsync(m->att_cnt, 0, NH * 4, g2i_stream()), "counter clear");
-    if (!rc) rc = g2i_hip(hipMemsetAsync(m->am_cnt, 0, 64, g2i_stream()), "counter clear");
     if (!rc) rc = g2i_hip(hipMemsetAsync(m->state, 0, G2S_WORDS * 4, g2i_stream()), "state clear");
     if (!rc) rc = g2i_hip(hipStreamSynchronize(g2i_stream()), "workspace sync");
     if (!rc) {
@@ -214,7 +211,7 @@ int g2_model_free(g2_model *m)
     void *bufs[] = { m->wte, m->wpe, m->lnf_w, m->lnf_b, m->lm_head, m->hidden, m->ln_out,
                      m->attn, m->attn_proj, m->ffn1, m->ffn2, m->qkv_new, m->qkv_full,
                      m->last_hidden, m->logits, m->partial, m->scores, m->q, m->ids_dev,
-                     m->state, m->att_part, m->am_part, m->att_cnt, m->am_cnt };
+                     m->state, m->att_part, m->am_part };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; ++i)
         if (bufs[i]) hipFree(bufs[i]);
     for (int l = 0; l < m->cfg.n_layer; ++l) {
@@ -485,6 +482,12 @@ int g2_model_set_kslice(g2_model *m, int kslice)
 
 size_t g2_model_weight_bytes(const g2_model *m) { return m ? m->weight_bytes : 0; }
 
+int g2_model_uses_graph(const g2_model *m)
+{
+    if (!m) return g2i_err(G2_E_ARG, "NULL model");
+    return m->graph_state == 1 ? 1 : (m->graph_state == -1 ? 0 : -1);
+}
+
 /* ------------------------------------------------ reference path (main.c) */
 
 /* launch_matvec_splitk, main.c:1578-1618 with the pinned slice count. */
@@ -559,23 +562,9 @@ static int ref_decode(g2_model *m, int pos)
 
 static unsigned cdivu(long a, long b) { return (unsigned)((a + b - 1) / b); }
 
-/* Work-groups for a packed matvec of N rows: 8 rows each, at most 1024. */
-static unsigned rows_grid(int N)
+static int launch_rows(g2_model *m, int fid_f32_64, g2_rows_args *a)
 {
-    unsigned g = cdivu(N, G2_ROWS_PER_WG);
-    return g > 1024 ? 1024 : g;
-}
-
-static int fid_rows(g2_model *m, int f32_id)
-{
-    /* f16 variants directly follow their f32 twin in the kernel table */
-    return m->dtype == G2_F16 ? f32_id + 1 : f32_id;
-}
-
-static int launch_rows(g2_model *m, int f32_fid, g2_rows_args *a)
-{
-    const int fid = fid_rows(m, f32_fid);
-    return g2i_launch(fid, rows_grid(a->N), 1, 256, a);
+    return g2i_rows_launch(fid_f32_64, m->dtype == G2_F16, a);
 }
 
 /* LayerNorm(ln_f) of row x, logits over the tied wte [V,E], argmax. */
@@ -584,10 +573,13 @@ static int fused_lm_head(g2_model *m, const float *x, int advance)
     g2_rows_args a;
     memset(&a, 0, sizeof a);
     a.W = m->lm_w; a.x = x; a.ln_g = m->lnf_w; a.ln_b = m->lnf_b; a.y = m->logits;
-    a.state = m->state; a.part = m->am_part; a.counter = m->am_cnt;
+    a.state = m->state; a.part = m->am_part;
     a.N = m->cfg.vocab_size; a.K = m->cfg.n_embd; a.E = m->cfg.n_embd; a.S = G2_KV_MAX_SEQ;
-    a.advance = advance;
-    return launch_rows(m, G2F_ROWS_F32_LN_ARGMAX, &a);
+    int rc = launch_rows(m, G2F_ROWS_LN_ARGMAX_F32_64, &a);
+    g2_amerge_args g = { m->am_part, m->state, (int)g2i_rows_grid(a.N, a.K, m->dtype == G2_F16),
+                         m->cfg.vocab_size, advance };
+    if (!rc) rc = g2i_launch(G2F_ARGMAX_MERGE, 1, 1, 256, &g);
+    return rc;
 }
 
 /* One decode forward at state[POS] with token state[TOK] (launches only). */
@@ -603,30 +595,30 @@ static int fused_step_launches(g2_model *m)
         a.W = y->qkv_w; a.x = m->hidden; a.ln_g = y->ln1_w; a.ln_b = y->ln1_b; a.bias = y->qkv_b;
         a.q_out = m->q; a.k_cache = y->k_cache; a.v_cache = y->v_cache; a.state = m->state;
         a.N = 3 * E; a.K = E; a.E = E; a.S = G2_KV_MAX_SEQ;
-        rc = launch_rows(m, G2F_ROWS_F32_LN_QKV, &a);
+        rc = launch_rows(m, G2F_ROWS_LN_QKV_F32_64, &a);
         if (rc) break;
         g2_attn1q_args t;
         memset(&t, 0, sizeof t);
         t.q = m->q; t.k_cache = y->k_cache; t.v_cache = y->v_cache; t.out = m->attn;
-        t.state = m->state; t.part = m->att_part; t.counter = m->att_cnt;
+        t.state = m->state; t.part = m->att_part;
         t.T_fixed = 0; t.D = E; t.NH = NH; t.S = G2_KV_MAX_SEQ; t.max_chunks = G2_ATTN_MAX_CHUNKS;
         t.scale = 1.0f / sqrtf(64.0f);
-        rc = g2i_launch(G2F_ATTN_1Q, (unsigned)NH, G2_ATTN_MAX_CHUNKS, 256, &t);
+        rc = g2i_attn_launch(&t, G2_ATTN_MAX_CHUNKS); /* chunks past the position exit at once */
         if (rc) break;
         memset(&a, 0, sizeof a);
         a.W = y->proj_w; a.x = m->attn; a.bias = y->proj_b; a.y = m->hidden;
         a.N = E; a.K = E;
-        rc = launch_rows(m, G2F_ROWS_F32_RESID, &a);
+        rc = launch_rows(m, G2F_ROWS_RESID_F32_64, &a);
         if (rc) break;
         memset(&a, 0, sizeof a);
         a.W = y->fc_w; a.x = m->hidden; a.ln_g = y->ln2_w; a.ln_b = y->ln2_b; a.bias = y->fc_b;
         a.y = m->ffn1; a.N = F; a.K = E;
-        rc = launch_rows(m, G2F_ROWS_F32_LN_GELU, &a);
+        rc = launch_rows(m, G2F_ROWS_LN_GELU_F32_64, &a);
         if (rc) break;
         memset(&a, 0, sizeof a);
         a.W = y->fc2_w; a.x = m->ffn1; a.bias = y->fc2_b; a.y = m->hidden;
         a.N = E; a.K = F;
-        rc = launch_rows(m, G2F_ROWS_F32_RESID, &a);
+        rc = launch_rows(m, G2F_ROWS_RESID_F32_64, &a);
     }
     if (!rc) rc = fused_lm_head(m, m->hidden, 1);
     return rc;
@@ -635,6 +627,10 @@ static int fused_step_launches(g2_model *m)
 /* Run one decode step, replaying the captured graph (captured on first use). */
 static int fused_step(g2_model *m)
 {
+    if (m->graph_state == 0) {
+        const char *env = getenv("G2_NO_GRAPH");
+        if (env && env[0] && env[0] != '0') m->graph_state = -1;
+    }
     if (m->graph_state == 0) {
         hipGraph_t g = NULL;
         int ok = hipStreamBeginCapture(g2i_stream(), hipStreamCaptureModeThreadLocal) == hipSuccess;
@@ -731,6 +727,17 @@ int g2_read_logits(g2_model *m, float *host, int n)
     int rc = g2i_hip(hipMemcpyAsync(host, m->logits, (size_t)n * sizeof(float),
                                     hipMemcpyDeviceToHost, g2i_stream()), "read logits");
     return rc ? rc : g2i_hip(hipStreamSynchronize(g2i_stream()), "read logits sync");
+}
+
+int g2_read_kv(g2_model *m, int layer, float *k_host, float *v_host)
+{
+    if (!m) return g2i_err(G2_E_ARG, "NULL model");
+    if (layer < 0 || layer >= m->cfg.n_layer) return g2i_err(G2_E_ARG, "layer %d out of range", layer);
+    const size_t bytes = (size_t)m->cfg.n_embd * G2_KV_MAX_SEQ * sizeof(float);
+    int rc = 0;
+    if (k_host) rc = g2i_hip(hipMemcpyAsync(k_host, m->L[layer].k_cache, bytes, hipMemcpyDeviceToHost, g2i_stream()), "read k");
+    if (!rc && v_host) rc = g2i_hip(hipMemcpyAsync(v_host, m->L[layer].v_cache, bytes, hipMemcpyDeviceToHost, g2i_stream()), "read v");
+    return rc ? rc : g2i_hip(hipStreamSynchronize(g2i_stream()), "read kv sync");
 }
 
 /* sample_next_token, greedy branch (main.c:1872-1904). */

@@ -38,7 +38,6 @@ static struct {
     hipFunction_t fn[G2F_COUNT];
     float *scratch;
     float *attn_part;
-    unsigned *attn_cnt;
 } G;
 
 static char g_errbuf[512] = "no error";
@@ -82,6 +81,42 @@ int g2i_device_alloc(void **p, size_t bytes)
 
 #define NEED_READY() do { if (!G.ready) return g2i_err(G2_E_STATE, "g2_init has not been called"); } while (0)
 
+/* Lane shape of the packed matvec for K: a row of C = K/V 16-byte chunks is
+ * owned by 64 lanes (C <= 256, two rows at a time) or by the 256-thread
+ * work-group (C <= 1024, or C <= 2048 with 8 chunks a lane), so each lane
+ * holds at most 4 (8) chunks of a row.  Returns the shape index 0..2 and
+ * the rows one work-group takes at a time, or -1 if K is not supported. */
+static int rows_shape(int K, int f16, int *rows_per_wg)
+{
+    const int V = f16 ? 8 : 4;
+    if (K <= 0 || K % V) return -1;
+    const int C = K / V;
+    if (C <= 256) { *rows_per_wg = 8; return 0; }
+    *rows_per_wg = 1;
+    if (C <= 1024) return 1;
+    if (C <= 2048) return 2;
+    return -1;
+}
+
+unsigned g2i_rows_grid(int N, int K, int f16)
+{
+    int per;
+    if (rows_shape(K, f16, &per) < 0 || N <= 0) return 0;
+    const unsigned per_wg = (unsigned)per;
+    unsigned g = ((unsigned)N + per_wg - 1) / per_wg;
+    return g > G2_ROWS_MAX_GRID ? G2_ROWS_MAX_GRID : g;
+}
+
+int g2i_rows_launch(int fid_f32_64, int f16, g2_rows_args *a)
+{
+    int per;
+    const int shape = rows_shape(a->K, f16, &per);
+    if (shape < 0 || a->N <= 0)
+        return g2i_err(G2_E_ARG, "packed matvec: K=%d must be a multiple of %d and at most %d",
+                       a->K, f16 ? 8 : 4, (f16 ? 8 : 4) * 2048);
+    return g2i_launch(fid_f32_64 + 2 * shape + (f16 ? 1 : 0), g2i_rows_grid(a->N, a->K, f16), 1, 256, a);
+}
+
 /* ------------------------------------------------------------------ runtime */
 
 int g2_init(int device)
@@ -115,10 +150,8 @@ int g2_init(int device)
     }
     rc = g2i_hip(hipMalloc((void **)&G.scratch, G2_SCRATCH_FLOATS * sizeof(float)), "scratch");
     if (!rc) rc = g2i_hip(hipMalloc((void **)&G.attn_part, G2_ATTN_PART_FLOATS * sizeof(float)), "attn scratch");
-    if (!rc) rc = g2i_hip(hipMalloc((void **)&G.attn_cnt, 64 * sizeof(unsigned)), "attn counters");
-    if (!rc) rc = g2i_hip(hipMemset(G.attn_cnt, 0, 64 * sizeof(unsigned)), "attn counters");
     if (rc) {
-        hipFree(G.scratch); hipFree(G.attn_part); hipFree(G.attn_cnt);
+        hipFree(G.scratch); hipFree(G.attn_part);
         hipStreamDestroy(G.stream); hipModuleUnload(G.module);
         memset(&G, 0, sizeof G);
         return rc;
@@ -135,7 +168,6 @@ int g2_shutdown(void)
     hipStreamSynchronize(G.stream);
     hipFree(G.scratch);
     hipFree(G.attn_part);
-    hipFree(G.attn_cnt);
     hipStreamDestroy(G.stream);
     hipModuleUnload(G.module);
     memset(&G, 0, sizeof G);
@@ -422,8 +454,32 @@ int g2_attn_1q(const float *qkv, const float *k_cache, const float *v_cache, flo
     g2_attn1q_args a;
     memset(&a, 0, sizeof a);
     a.q = qkv + q_base; a.k_cache = k_cache; a.v_cache = v_cache; a.out = out + out_base;
-    a.part = G.attn_part; a.counter = G.attn_cnt;
+    a.part = G.attn_part;
     a.T_fixed = T_kv; a.D = D; a.NH = NH; a.S = max_seq; a.max_chunks = G2_ATTN_MAX_CHUNKS;
     a.scale = scale;
-    return g2i_launch(G2F_ATTN_1Q, (unsigned)NH, cdiv(T_kv, G2_ATTN_CHUNK), 256, &a);
+    return g2i_attn_launch(&a, cdiv(T_kv, G2_ATTN_CHUNK));
+}
+
+int g2i_attn_launch(g2_attn1q_args *a, unsigned chunks)
+{
+    const int vec = a->S % 4 == 0 && a->D % 4 == 0 && aligned(a->k_cache, 16) && aligned(a->v_cache, 16);
+    int rc = g2i_launch(vec ? G2F_ATTN_PART : G2F_ATTN_PART_S, (unsigned)a->NH, chunks, 256, a);
+    if (!rc) rc = g2i_launch(G2F_ATTN_MERGE, (unsigned)a->NH, 1, 64, a);
+    return rc;
+}
+
+int g2_matvec_rows(const float *x, const void *W, int w_dtype, const float *bias,
+                   const float *residual, float *y, int N, int K, int apply_gelu)
+{
+    NEED_READY();
+    if (!x || !W || !y) return g2i_err(G2_E_ARG, "g2_matvec_rows: NULL buffer");
+    if (w_dtype != G2_F32 && w_dtype != G2_F16) return g2i_err(G2_E_ARG, "g2_matvec_rows: bad dtype");
+    if (N <= 0) return g2i_err(G2_E_ARG, "g2_matvec_rows: N must be positive");
+    if (!aligned(x, 16) || !aligned(W, 16)) return g2i_err(G2_E_ARG, "g2_matvec_rows: x and W must be 16-byte aligned");
+    if (apply_gelu) return g2i_err(G2_E_ARG, "g2_matvec_rows: GELU exists only fused with LayerNorm (model path)");
+    if (residual && residual != y) return g2i_err(G2_E_ARG, "g2_matvec_rows: the residual must alias y");
+    g2_rows_args a;
+    memset(&a, 0, sizeof a);
+    a.W = W; a.x = x; a.bias = bias; a.y = y; a.N = N; a.K = K;
+    return g2i_rows_launch(residual ? G2F_ROWS_RESID_F32_64 : G2F_ROWS_STORE_F32_64, w_dtype == G2_F16, &a);
 }

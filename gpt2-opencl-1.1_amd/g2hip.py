@@ -91,6 +91,8 @@ for _n, _a in {
     "g2_attn_scores_1q": [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f],
     "g2_attn_softmax_1q": [_vp, _i, _i], "g2_attn_out_1q": [_vp, _vp, _vp, _i, _i, _i, _i],
     "g2_attn_1q": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f],
+    "g2_matvec_rows": [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i],
+    "g2_model_uses_graph": [_vp], "g2_read_kv": [_vp, _i, _vp, _vp],
     "g2_config_load": [C.c_char_p, C.POINTER(Config)], "g2_config_parse": [C.c_char_p, C.POINTER(Config)],
     "g2_model_load": [C.c_char_p, _i, _i, C.POINTER(_vp)],
     "g2_model_synth": [C.POINTER(Config), C.c_uint64, _i, _i, C.POINTER(_vp)],
@@ -218,6 +220,11 @@ def matvec(A, B, bias, residual, Cb, N, K, apply_gelu=0, f16=False):
 def matvec_sk(A, B, partial, N, K, kslice, f16=False):
     fn = _lib.g2_matvec_sk_f16 if f16 else _lib.g2_matvec_sk
     check(fn(_p(A), _p(B), _p(partial), N, K, kslice))
+
+
+def matvec_rows(x, W, w_dtype, bias, residual, y, N, K, apply_gelu=0):
+    """Packed (output-major W[N,K]) matvec of the fused model."""
+    check(_lib.g2_matvec_rows(_p(x), _p(W), w_dtype, _p(bias), _p(residual), _p(y), N, K, int(apply_gelu)))
 
 
 def reduce_partial(partial, bias, residual, Cb, N, kslice, apply_gelu=0):
@@ -376,6 +383,9 @@ class Model:
     def weight_bytes(self):
         return _lib.g2_model_weight_bytes(self.h)
 
+    def uses_graph(self):
+        return _lib.g2_model_uses_graph(self.h)
+
     def prefill(self, ids):
         ids = np.ascontiguousarray(ids, dtype=np.int32)
         check(_lib.g2_prefill(self.h, ids.ctypes.data, len(ids)))
@@ -388,6 +398,14 @@ class Model:
         out = np.empty(n, dtype=np.float32)
         check(_lib.g2_read_logits(self.h, out.ctypes.data, n))
         return out
+
+    def read_kv(self, layer):
+        """(K [E,1024] transposed, V [1024,E]) of one layer."""
+        E = self.cfg.n_embd
+        k = np.empty((E, MAX_SEQ), np.float32)
+        v = np.empty((MAX_SEQ, E), np.float32)
+        check(_lib.g2_read_kv(self.h, layer, k.ctypes.data, v.ctypes.data))
+        return k, v
 
     def sample_greedy(self, ctx, forbid_eos=False, rep_penalty=1.0):
         ctx = np.ascontiguousarray(ctx, dtype=np.int32)

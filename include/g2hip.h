@@ -135,6 +135,15 @@ int g2_attn_1q(const float *qkv, const float *k_cache, const float *v_cache,
                float *out, int q_base, int T_kv, int D, int NH, int max_seq,
                int out_base, float scale);
 
+/* launch_matvec over the output-major weight layout the fused model uses:
+ * y[n] = sum_k W[n*K + k] x[k] (+ bias[n]) (+ y[n] when residual == y);
+ * W is [N,K] row-major fp32 or fp16 (w_dtype), i.e. the transpose of the
+ * reference's B[K,N].  K must be a multiple of 4 (fp32) or 8 (fp16), at
+ * most 8192 (fp32) / 16384 (fp16); x and W 16-byte aligned. apply_gelu must
+ * be 0 (the GELU epilogue exists only fused with LayerNorm in the model). */
+int g2_matvec_rows(const float *x, const void *W, int w_dtype, const float *bias,
+                   const float *residual, float *y, int N, int K, int apply_gelu);
+
 /* ---- configuration, weights, model (main.c:272-331, 1137-1512, 1739-1904) -- */
 
 typedef struct {
@@ -193,6 +202,10 @@ int g2_model_config(const g2_model *m, g2_config *cfg);
 int g2_model_set_kslice(g2_model *m, int kslice);
 /* Device bytes held by the model's weights (cf. "Model VRAM", main.c:1416). */
 size_t g2_model_weight_bytes(const g2_model *m);
+/* Fused path: 1 if decode steps replay a captured HIP graph, 0 if their
+ * kernels are launched one by one (capture unavailable, or the environment
+ * sets G2_NO_GRAPH=1, e.g. under a profiler), -1 before the first step. */
+int g2_model_uses_graph(const g2_model *m);
 
 /* prefill, main.c:1739-1790: ids[0..n) at positions 0..n-1, 1 <= n <= 1023;
  * leaves the last row's logits on the device. */
@@ -201,6 +214,10 @@ int g2_prefill(g2_model *m, const int *ids, int n);
 int g2_decode(g2_model *m, int token, int pos);
 /* Blocking read of the first n logits of the last forward (main.c:1878). */
 int g2_read_logits(g2_model *m, float *host, int n);
+/* Blocking read of layer `layer`'s KV cache in the reference layout
+ * (main.c:1481-1486): k_host [n_embd, 1024] (transposed), v_host
+ * [1024, n_embd]; either pointer may be NULL. */
+int g2_read_kv(g2_model *m, int layer, float *k_host, float *v_host);
 /* sample_next_token greedy branch, main.c:1872-1904 (temperature 0): EOS
  * mask when forbid_eos, repetition penalty over the distinct context ids
  * when rep_penalty > 1, first-max argmax. Returns the token id (>= 0) or a

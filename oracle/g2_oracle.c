@@ -470,6 +470,22 @@ void or_decode(or_model *m, int tok, int pos)
 
 const float *or_logits(const or_model *m) { return m->logits; }
 
+/* Overwrite layer l's caches (K transposed [E,1024], V [1024,E]); lets a
+ * timing sample start decoding at a late position without a CPU prefill. */
+void or_set_kv(or_model *m, int l, const float *k_cache, const float *v_cache)
+{
+    const size_t n = (size_t)m->n_embd * OR_MAX_SEQ;
+    memcpy(m->k_cache[l], k_cache, n * sizeof(float));
+    memcpy(m->v_cache[l], v_cache, n * sizeof(float));
+}
+
+#ifdef _OPENMP
+#include <omp.h>
+int or_num_threads(void) { return omp_get_max_threads(); }
+#else
+int or_num_threads(void) { return 1; }
+#endif
+
 /* main.c:1872-1904, greedy branch (temperature <= 0).  Works on a copy of
  * the first `vocab` logits: EOS mask, repetition penalty over distinct
  * context ids, then first-max argmax (lowest index wins ties). */

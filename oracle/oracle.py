@@ -50,10 +50,17 @@ for _n, _a, _r in [
     ("or_greedy", [_vp, _i, _vp, _i, _i, _f, _vp], _i),
     ("or_generate", [_vp, _vp, _i, _i, _i, _f, _vp, _vp, _vp, _i], _i),
     ("or_teacher_forced", [_vp, _vp, _i, _vp, _i, _vp], None),
+    ("or_set_kv", [_vp, _i, _vp, _vp], None),
+    ("or_num_threads", [], _i),
 ]:
     fn = getattr(_lib, _n)
     fn.argtypes = _a
     fn.restype = _r
+
+
+def num_threads():
+    """OpenMP threads the oracle runs with (OMP_NUM_THREADS or all cores)."""
+    return _lib.or_num_threads()
 
 
 def _a32(x):
@@ -199,6 +206,11 @@ class Model:
 
     def decode(self, token, pos):
         _lib.or_decode(self.h, int(token), int(pos))
+
+    def set_kv(self, layer, k_cache, v_cache):
+        k, v = _a32(k_cache), _a32(v_cache)
+        assert k.size == v.size == self.cfg.n_embd * 1024
+        _lib.or_set_kv(self.h, layer, _ptr(k), _ptr(v))
 
     def logits(self):
         p = _lib.or_logits(self.h)

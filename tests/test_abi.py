@@ -1,0 +1,220 @@
+"""C-ABI and host-logic tests that need no GPU.
+
+- libg2hip.so loads and exports every function include/g2hip.h declares;
+- host-only entry points: config.json parsing with the reference's defaults
+  and ceilings (main.c:294-331), the synthetic weight generator, fp16
+  rounding, the safetensors reader's error paths (main.c:1141-1232);
+- every device entry point fails with an error code (never a crash) when the
+  runtime is not initialised.
+"""
+import ctypes as C
+import json
+import os
+import struct
+import subprocess
+
+import numpy as np
+import pytest
+
+import g2hip
+
+
+def test_library_exports_every_declared_symbol():
+    declared = g2hip.exported_symbols()
+    assert len(declared) >= 40
+    out = subprocess.run(["nm", "-D", "--defined-only", g2hip.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = [s for s in declared if s not in exported]
+    assert not missing, f"declared in g2hip.h but not exported: {missing}"
+    lib = C.CDLL(g2hip.LIB_PATH)
+    for s in declared:
+        getattr(lib, s)
+
+
+def test_code_object_is_embedded_for_gfx950():
+    out = subprocess.run(["nm", "-D", "--defined-only", g2hip.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    assert "g2_hsaco_begin" in out
+    blob = open(g2hip.LIB_PATH, "rb").read()
+    assert b"amdgcn-amd-amdhsa--gfx950" in blob
+    for k in ("g2k_rows_ln_qkv_f16_64", "g2k_attn_part", "g2k_attn_merge", "g2k_argmax_merge",
+              "g2k_gemm_nk_f16_qkv", "g2k_mvsk_f32"):
+        assert k.encode() in blob
+
+
+def test_calls_without_init_return_state_error():
+    lib = C.CDLL(g2hip.LIB_PATH)
+    lib.g2_matvec.argtypes = [C.c_void_p] * 5 + [C.c_int] * 3
+    assert lib.g2_matvec(None, None, None, None, None, 4, 4, 0) == g2hip.G2_E_STATE
+    lib.g2_sync.argtypes = []
+    assert lib.g2_sync() == g2hip.G2_E_STATE
+    assert "g2_init" in g2hip.last_error()
+
+
+def test_config_parse_defaults_and_keys():
+    c = g2hip.config_parse('{"n_layer": 24, "n_embd": 1024, "n_head": 16, "vocab_size": 50257}')
+    assert (c.n_layer, c.n_embd, c.n_head, c.ffn_dim, c.n_ctx) == (24, 1024, 16, 4096, 1024)
+    c = g2hip.config_parse('{"n_layer":2,"n_embd":64,"n_head":1,"n_inner":100,"n_ctx":512}')
+    assert (c.ffn_dim, c.n_ctx) == (100, 512)
+    c = g2hip.config_parse("{}")  # every key defaults to GPT-2 small
+    assert (c.n_layer, c.n_embd, c.n_head, c.vocab_size, c.ffn_dim) == (12, 768, 12, 50257, 3072)
+    xl = g2hip.config_parse(json.dumps({"n_layer": 48, "n_embd": 1600, "n_head": 25}))
+    assert xl.ffn_dim == 6400
+
+
+@pytest.mark.parametrize("cfg", [{"n_layer": 49}, {"n_embd": 1664, "n_head": 26}, {"n_head": 32, "n_embd": 2048},
+                                 {"vocab_size": 60000}, {"n_inner": 8192}, {"n_positions": 2048}])
+def test_config_ceilings(cfg):
+    with pytest.raises(g2hip.G2Error) as e:
+        g2hip.config_parse(json.dumps(cfg))
+    assert e.value.code == g2hip.G2_E_LIMIT
+
+
+def test_config_missing_file_means_small(tmp_path):
+    c = g2hip.config_load(str(tmp_path))
+    assert (c.n_layer, c.n_embd, c.n_head) == (12, 768, 12)
+
+
+def test_synth_deterministic_and_normal():
+    a = g2hip.synth_normal(1_000_001, 42, 7)
+    b = g2hip.synth_normal(1_000_001, 42, 7)
+    np.testing.assert_array_equal(a, b)
+    assert not np.array_equal(a, g2hip.synth_normal(1_000_001, 42, 8))
+    assert not np.array_equal(a, g2hip.synth_normal(1_000_001, 43, 7))
+    assert abs(a.mean()) < 1e-4 and abs(a.std() - 0.02) < 1e-4
+    # prefix property: element i does not depend on n
+    np.testing.assert_array_equal(g2hip.synth_normal(1001, 42, 7), a[:1001])
+    # standardised 4th moment of a normal is 3
+    z = a / 0.02
+    assert abs((z ** 4).mean() - 3.0) < 0.05
+
+
+def test_synth_tensor_ids():
+    assert g2hip.synth_tensor_id(-1, 1) == 1 and g2hip.synth_tensor_id(-1, 2) == 2
+    ids = {g2hip.synth_tensor_id(l, w) for l in range(48) for w in range(4)}
+    assert len(ids) == 192 and min(ids) == 16
+
+
+def test_convert_f16_matches_ieee_rne():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32) * 10.0 ** rng.integers(-9, 6, 200000),
+        np.array([0.0, -0.0, 65504, 65519.99, 65520, -65520, 1e9, np.inf, -np.inf, 2 ** -24, 2 ** -25,
+                  2 ** -25 * 1.0000001, 3 * 2 ** -26, 2 ** -14, 2 ** -14 - 2 ** -25, 1 + 2 ** -11,
+                  1 + 3 * 2 ** -11, 6e-8, 5.9604645e-08], np.float32),
+    ]).astype(np.float32)
+    got = g2hip.convert_f16(x)
+    with np.errstate(over="ignore"):
+        exp = x.astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(got, exp)
+    nan = g2hip.convert_f16(np.array([np.nan], np.float32))[0]
+    assert (nan & 0x7C00) == 0x7C00 and (nan & 0x3FF) != 0
+
+
+def _write_st(path, tensors, header_extra=None, raw_header=None):
+    """Write a safetensors file; tensors: name -> (dtype str, shape, bytes)."""
+    hdr, blobs, off = {}, [], 0
+    for name, (dt, shape, data) in tensors.items():
+        hdr[name] = {"dtype": dt, "shape": list(shape), "data_offsets": [off, off + len(data)]}
+        blobs.append(data)
+        off += len(data)
+    if header_extra:
+        hdr.update(header_extra)
+    h = raw_header if raw_header is not None else json.dumps(hdr).encode()
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(h)))
+        f.write(h)
+        for b in blobs:
+            f.write(b)
+
+
+def _model_dir(tmp_path, dtype="F32", linear=False, drop=None):
+    E, V, L = 64, 100, 1
+    (tmp_path / "config.json").write_text(json.dumps({"n_layer": L, "n_embd": E, "n_head": 1, "vocab_size": V}))
+    rng = np.random.default_rng(1)
+    t = {}
+
+    def add(name, shape):
+        a = rng.standard_normal(shape).astype(np.float32)
+        if dtype == "F16":
+            t[name] = ("F16", shape, a.astype(np.float16).tobytes())
+        else:
+            t[name] = (dtype, shape, a.tobytes() if dtype == "F32" else a.astype(np.float64).tobytes())
+
+    add("wte.weight", (V, E))
+    add("wpe.weight", (1024, E))
+    for n, s in [("ln_1.weight", (E,)), ("ln_1.bias", (E,)), ("attn.c_attn.bias", (3 * E,)),
+                 ("attn.c_proj.bias", (E,)), ("ln_2.weight", (E,)), ("ln_2.bias", (E,)),
+                 ("mlp.c_fc.bias", (4 * E,)), ("mlp.c_proj.bias", (E,))]:
+        add(f"h.0.{n}", s)
+    for n, (i, o) in [("attn.c_attn.weight", (E, 3 * E)), ("attn.c_proj.weight", (E, E)),
+                      ("mlp.c_fc.weight", (E, 4 * E)), ("mlp.c_proj.weight", (4 * E, E))]:
+        add(f"h.0.{n}", (o, i) if linear else (i, o))
+    add("ln_f.weight", (E,))
+    add("ln_f.bias", (E,))
+    if drop:
+        t.pop(drop)
+    _write_st(tmp_path / "model.safetensors", t)
+    return str(tmp_path)
+
+
+def _load_rc(d, dtype=g2hip.F32, path=g2hip.PATH_FUSED):
+    h = C.c_void_p()
+    rc = g2hip._lib.g2_model_load(d.encode(), dtype, path, C.byref(h))
+    return rc, g2hip.last_error()
+
+
+def test_loader_structure_ok_reaches_device_check(tmp_path):
+    """A well-formed directory passes every host check and stops only at the
+    missing runtime (no GPU here): F32 Conv1D, F16, and Linear layouts."""
+    for kw in ({}, {"dtype": "F16"}, {"linear": True}):
+        d = tmp_path / str(len(os.listdir(tmp_path)))
+        d.mkdir()
+        rc, msg = _load_rc(_model_dir(d, **kw))
+        assert rc == g2hip.G2_E_STATE, msg
+
+
+def test_loader_errors(tmp_path):
+    rc, msg = _load_rc(str(tmp_path / "nowhere"))
+    assert rc == g2hip.G2_E_IO and "model.safetensors" in msg
+    d1 = tmp_path / "f64"
+    d1.mkdir()
+    rc, msg = _load_rc(_model_dir(d1, dtype="F64"))
+    assert rc == g2hip.G2_E_FORMAT and "F64" in msg
+    d2 = tmp_path / "noattn"
+    d2.mkdir()
+    rc, msg = _load_rc(_model_dir(d2, drop="h.0.attn.c_attn.weight"))
+    assert rc == g2hip.G2_E_FORMAT and "c_attn" in msg
+    d3 = tmp_path / "badjson"
+    d3.mkdir()
+    (d3 / "config.json").write_text("{}")
+    _write_st(d3 / "model.safetensors", {}, raw_header=b'{"a": {"dtype": "F32", "shape": [2], "data_offsets": [0')
+    rc, msg = _load_rc(str(d3))
+    assert rc == g2hip.G2_E_FORMAT
+    d4 = tmp_path / "short"
+    d4.mkdir()
+    (d4 / "model.safetensors").write_bytes(b"\x10\x00")
+    rc, msg = _load_rc(str(d4))
+    assert rc == g2hip.G2_E_IO
+    d5 = tmp_path / "inconsistent"
+    d5.mkdir()
+    _write_st(d5 / "model.safetensors", {"x": ("F32", (3, 3), b"\0" * 12)})
+    rc, msg = _load_rc(str(d5))
+    assert rc == g2hip.G2_E_FORMAT and "inconsistent" in msg
+
+
+def test_reference_path_rejects_fp16_and_bad_shapes(tmp_path):
+    d = _model_dir(tmp_path)
+    rc, msg = _load_rc(d, dtype=g2hip.F16, path=g2hip.PATH_REFERENCE)
+    assert rc == g2hip.G2_E_ARG
+    (tmp_path / "config.json").write_text(json.dumps({"n_layer": 1, "n_embd": 96, "n_head": 1}))
+    rc, msg = _load_rc(d)  # fused path needs head dim 64
+    assert rc == g2hip.G2_E_ARG and "64" in msg
+
+
+def test_init_without_gpu_is_an_error_not_a_crash():
+    if os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU driver is present")
+    rc = g2hip._lib.g2_init(0)
+    assert rc < 0

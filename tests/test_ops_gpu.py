@@ -44,6 +44,42 @@ def test_matvec_sweep(g2, N, K, f16):
     assert_close_bound(got, ref, dot_bound(np.abs(A), np.abs(B), K), what=f"matvec {N}x{K}")
 
 
+ROWS_SHAPES = MV_SHAPES + [(4800, 1600), (1600, 1600), (1600, 6400), (5, 8), (3, 1024), (77, 2048),
+                           (1000, 4096), (64, 8192), (33, 5120), (50257, 1280)]
+
+
+@pytest.mark.parametrize("f16", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("N,K", ROWS_SHAPES)
+def test_matvec_rows(g2, N, K, f16):
+    """The fused model's packed matvec: W = B^T stored [N,K], every lane
+    shape (64 x 4, 256 x 4, 256 x 8 chunks) and the grid-stride path."""
+    A, B, bias, res = rnd(K, 1), rnd((K, N), 2), rnd(N, 3), rnd(N, 4)
+    if f16:
+        B = f16_round(B)
+    Wt = np.ascontiguousarray(B.T)
+    dW = g2.to_device(g2.convert_f16(Wt) if f16 else Wt)
+    dA, dbias = g2.to_device(A), g2.to_device(bias)
+    dC = g2.DevBuf(N * 4)
+    g2.matvec_rows(dA, dW, g2.F16 if f16 else g2.F32, dbias, None, dC, N, K)
+    ref = oracle.matvec(A, B, bias, None, N, K) if N % 4 == 0 else oracle.matvec_scalar(A, B, bias, None, N, K)
+    bound = dot_bound(np.abs(A), np.abs(B), K)
+    assert_close_bound(dC.download(np.float32, N), ref, bound, what=f"rows {N}x{K}")
+    dR = g2.to_device(res)
+    g2.matvec_rows(dA, dW, g2.F16 if f16 else g2.F32, dbias, dR, dR, N, K)
+    ref = oracle.matvec(A, B, bias, res, N, K) if N % 4 == 0 else oracle.matvec_scalar(A, B, bias, res, N, K)
+    assert_close_bound(dR.download(np.float32, N), ref, bound, slack=2e-6, what=f"rows resid {N}x{K}")
+
+
+def test_matvec_rows_rejects(g2):
+    buf = g2.DevBuf(1 << 16)
+    with pytest.raises(g2.G2Error):
+        g2.matvec_rows(buf, buf, g2.F16, None, None, buf, 4, 12)  # K % 8
+    with pytest.raises(g2.G2Error):
+        g2.matvec_rows(buf, buf, g2.F32, None, None, buf, 4, 8196)  # K above 8192
+    with pytest.raises(g2.G2Error):
+        g2.matvec_rows(buf, buf, g2.F32, None, None, buf, 4, 8, apply_gelu=1)
+
+
 @pytest.mark.parametrize("N,K", [(768, 768), (3072, 768), (7, 5), (13, 1000), (4, 1), (1, 33)])
 @pytest.mark.parametrize("gelu", [0, 1])
 def test_matvec_epilogues(g2, N, K, gelu):

@@ -37,6 +37,20 @@ def hf_model(cfg, w):
     return m
 
 
+def eos_dominant(w, E):
+    """Weights whose EOS logit wins every step: ln_f beta = 10 e_0 and the
+    EOS row of wte = 10 e_0 add 100 to the EOS logit, while the normalised
+    hidden state moves it by at most 10*|h_0| and other logits stay O(1).
+    The prompt never holds EOS, so the embedding lookup is unaffected."""
+    w2 = dict(w)
+    w2["wte"] = w["wte"].copy()
+    w2["wte"][50256] = 0.0
+    w2["wte"][50256, 0] = 10.0
+    w2["lnf_b"] = np.zeros(E, np.float32)
+    w2["lnf_b"][0] = 10.0
+    return w2
+
+
 def hf_logits(m, ids):
     with torch.no_grad():
         return m(torch.tensor(np.asarray(ids, np.int64)[None])).logits[0].numpy()
@@ -101,9 +115,7 @@ def test_greedy_first_max_and_eos_mask():
     om.prefill(np.array([1, 2, 3], np.int32))
     lg = om.logits()
     assert om.greedy([1, 2, 3]) == int(np.argmax(lg))  # np.argmax is first-max too
-    w2 = dict(w)
-    w2["wte"] = w["wte"].copy()
-    w2["wte"][50256] *= 50
+    w2 = eos_dominant(w, cfg.n_embd)
     om2 = oracle.Model(cfg, w2)
     om2.prefill(np.array([1, 2, 3], np.int32))
     assert om2.greedy([1, 2, 3]) == 50256
