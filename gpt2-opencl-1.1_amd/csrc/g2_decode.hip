@@ -390,16 +390,22 @@ G2K void g2k_argmax_merge(const g2_amerge_args a)
     }
 }
 
-/* Instantiations: per epilogue, the f32 and f16 twins of each lane shape
- * (64 lanes x 4 chunks x 2 rows, 256 x 4 x 1, 256 x 8 x 1), in the order
- * g2_internal.h lists them. */
-#define G2_ROWS_SET(ename, EPI, LN)                                                                            \
-    G2K void g2k_rows_##ename##_f32_64(const g2_rows_args a) { rows_impl<float, EPI, LN, 64, 4, 2>(a); }      \
-    G2K void g2k_rows_##ename##_f16_64(const g2_rows_args a) { rows_impl<_Float16, EPI, LN, 64, 4, 2>(a); }   \
-    G2K void g2k_rows_##ename##_f32_256(const g2_rows_args a) { rows_impl<float, EPI, LN, 256, 4, 1>(a); }    \
-    G2K void g2k_rows_##ename##_f16_256(const g2_rows_args a) { rows_impl<_Float16, EPI, LN, 256, 4, 1>(a); } \
-    G2K void g2k_rows_##ename##_f32_256x8(const g2_rows_args a) { rows_impl<float, EPI, LN, 256, 8, 1>(a); }  \
-    G2K void g2k_rows_##ename##_f16_256x8(const g2_rows_args a) { rows_impl<_Float16, EPI, LN, 256, 8, 1>(a); }
+/* Instantiations: per epilogue, the f32 and f16 twins of each lane shape, in
+ * the order g2_internal.h lists them (SG lanes x CPT chunks x R rows):
+ *   s64    64 x 4 x 1   rows of <= 256 chunks, short matrices (proj)
+ *   s256r  256 x 1 x 2  rows of <= 256 chunks, long matrices (qkv, fc)
+ *   s256   256 x 4 x 2  rows of <= 1024 chunks (fc2 of GPT-2 XL)
+ *   s256x8 256 x 8 x 1  rows of <= 2048 chunks (fp32 ffn of large models)
+ * chosen by measurement on the GPT-2 XL decode matrices. */
+#define G2_ROWS_SET(ename, EPI, LN)                                                                                \
+    G2K void g2k_rows_##ename##_f32_s64(const g2_rows_args a) { rows_impl<float, EPI, LN, 64, 4, 1>(a); }         \
+    G2K void g2k_rows_##ename##_f16_s64(const g2_rows_args a) { rows_impl<_Float16, EPI, LN, 64, 4, 1>(a); }      \
+    G2K void g2k_rows_##ename##_f32_s256r(const g2_rows_args a) { rows_impl<float, EPI, LN, 256, 1, 2>(a); }      \
+    G2K void g2k_rows_##ename##_f16_s256r(const g2_rows_args a) { rows_impl<_Float16, EPI, LN, 256, 1, 2>(a); }   \
+    G2K void g2k_rows_##ename##_f32_s256(const g2_rows_args a) { rows_impl<float, EPI, LN, 256, 4, 2>(a); }       \
+    G2K void g2k_rows_##ename##_f16_s256(const g2_rows_args a) { rows_impl<_Float16, EPI, LN, 256, 4, 2>(a); }    \
+    G2K void g2k_rows_##ename##_f32_s256x8(const g2_rows_args a) { rows_impl<float, EPI, LN, 256, 8, 1>(a); }     \
+    G2K void g2k_rows_##ename##_f16_s256x8(const g2_rows_args a) { rows_impl<_Float16, EPI, LN, 256, 8, 1>(a); }
 
 G2_ROWS_SET(store, EPI_STORE, false)
 G2_ROWS_SET(ln_qkv, EPI_QKV, true)

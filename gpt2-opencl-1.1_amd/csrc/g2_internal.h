@@ -15,15 +15,17 @@
 #include "g2hip.h"
 #include "g2_kargs.h"
 
-/* Packed-matvec kernels of one epilogue: f32/f16 twins of the three lane
- * shapes (64 lanes x 4 chunks, 256 x 4, 256 x 8), see g2i_rows_kernel. */
+/* Packed-matvec kernels of one epilogue: f32/f16 twins of the four lane
+ * shapes (see g2_decode.hip and rows_shape in g2_shim.c). */
 #define G2_ROWS_LIST(X, E, s)                                                 \
-    X(ROWS_##E##_F32_64, "g2k_rows_" s "_f32_64")                             \
-    X(ROWS_##E##_F16_64, "g2k_rows_" s "_f16_64")                             \
-    X(ROWS_##E##_F32_256, "g2k_rows_" s "_f32_256")                           \
-    X(ROWS_##E##_F16_256, "g2k_rows_" s "_f16_256")                           \
-    X(ROWS_##E##_F32_256X8, "g2k_rows_" s "_f32_256x8")                       \
-    X(ROWS_##E##_F16_256X8, "g2k_rows_" s "_f16_256x8")
+    X(ROWS_##E##_F32_64, "g2k_rows_" s "_f32_s64")                            \
+    X(ROWS_##E##_F16_64, "g2k_rows_" s "_f16_s64")                            \
+    X(ROWS_##E##_F32_256R, "g2k_rows_" s "_f32_s256r")                        \
+    X(ROWS_##E##_F16_256R, "g2k_rows_" s "_f16_s256r")                        \
+    X(ROWS_##E##_F32_256, "g2k_rows_" s "_f32_s256")                          \
+    X(ROWS_##E##_F16_256, "g2k_rows_" s "_f16_s256")                          \
+    X(ROWS_##E##_F32_256X8, "g2k_rows_" s "_f32_s256x8")                      \
+    X(ROWS_##E##_F16_256X8, "g2k_rows_" s "_f16_s256x8")
 
 /* Kernel table: index -> symbol name in the gfx950 code object. */
 #define G2_KERNEL_LIST(X)                                                     \
@@ -57,8 +59,8 @@ enum { G2_KERNEL_LIST(G2_ENUM_ENTRY) G2F_COUNT };
 
 /* Largest K of the fused model's packed matvecs (GPT-2 XL ffn). */
 #define G2_ROWS_MAXK 6400
-/* Cap on packed-matvec work-groups (8 per CU); longer matrices grid-stride. */
-#define G2_ROWS_MAX_GRID 2048
+/* Cap on packed-matvec work-groups (4 per CU); longer matrices grid-stride. */
+#define G2_ROWS_MAX_GRID 1024
 /* Key chunk of the single-query attention kernel and chunks per head. */
 #define G2_ATTN_CHUNK 64
 #define G2_ATTN_MAX_CHUNKS (G2_KV_MAX_SEQ / G2_ATTN_CHUNK)

@@ -81,27 +81,30 @@ int g2i_device_alloc(void **p, size_t bytes)
 
 #define NEED_READY() do { if (!G.ready) return g2i_err(G2_E_STATE, "g2_init has not been called"); } while (0)
 
-/* Lane shape of the packed matvec for K: a row of C = K/V 16-byte chunks is
- * owned by 64 lanes (C <= 256, two rows at a time) or by the 256-thread
- * work-group (C <= 1024, or C <= 2048 with 8 chunks a lane), so each lane
- * holds at most 4 (8) chunks of a row.  Returns the shape index 0..2 and
- * the rows one work-group takes at a time, or -1 if K is not supported. */
-static int rows_shape(int K, int f16, int *rows_per_wg)
+/* Lane shape of the packed matvec for N rows of C = K/V 16-byte chunks
+ * (measured on the GPT-2 XL decode matrices):
+ *   0: 64 lanes x 4 chunks, 4 rows per work-group -- C <= 256, N <= 2048
+ *   1: 256 lanes x 1 chunk x 2 rows                -- C <= 256, longer N
+ *   2: 256 lanes x 4 chunks x 2 rows               -- C <= 1024
+ *   3: 256 lanes x 8 chunks x 1 row                -- C <= 2048
+ * Returns the shape and the rows a work-group takes at a time, or -1 if K
+ * is not supported. */
+static int rows_shape(int N, int K, int f16, int *rows_per_wg)
 {
     const int V = f16 ? 8 : 4;
     if (K <= 0 || K % V) return -1;
     const int C = K / V;
-    if (C <= 256) { *rows_per_wg = 8; return 0; }
-    *rows_per_wg = 1;
-    if (C <= 1024) return 1;
-    if (C <= 2048) return 2;
+    if (C <= 256 && N <= 2048) { *rows_per_wg = 4; return 0; }
+    if (C <= 256) { *rows_per_wg = 2; return 1; }
+    if (C <= 1024) { *rows_per_wg = 2; return 2; }
+    if (C <= 2048) { *rows_per_wg = 1; return 3; }
     return -1;
 }
 
 unsigned g2i_rows_grid(int N, int K, int f16)
 {
     int per;
-    if (rows_shape(K, f16, &per) < 0 || N <= 0) return 0;
+    if (rows_shape(N, K, f16, &per) < 0 || N <= 0) return 0;
     const unsigned per_wg = (unsigned)per;
     unsigned g = ((unsigned)N + per_wg - 1) / per_wg;
     return g > G2_ROWS_MAX_GRID ? G2_ROWS_MAX_GRID : g;
@@ -110,7 +113,7 @@ unsigned g2i_rows_grid(int N, int K, int f16)
 int g2i_rows_launch(int fid_f32_64, int f16, g2_rows_args *a)
 {
     int per;
-    const int shape = rows_shape(a->K, f16, &per);
+    const int shape = rows_shape(a->N, a->K, f16, &per);
     if (shape < 0 || a->N <= 0)
         return g2i_err(G2_E_ARG, "packed matvec: K=%d must be a multiple of %d and at most %d",
                        a->K, f16 ? 8 : 4, (f16 ? 8 : 4) * 2048);

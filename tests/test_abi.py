@@ -38,7 +38,7 @@ def test_code_object_is_embedded_for_gfx950():
     assert "g2_hsaco_begin" in out
     blob = open(g2hip.LIB_PATH, "rb").read()
     assert b"amdgcn-amd-amdhsa--gfx950" in blob
-    for k in ("g2k_rows_ln_qkv_f16_64", "g2k_attn_part", "g2k_attn_merge", "g2k_argmax_merge",
+    for k in ("g2k_rows_ln_qkv_f16_s256r", "g2k_attn_part", "g2k_attn_merge", "g2k_argmax_merge",
               "g2k_gemm_nk_f16_qkv", "g2k_mvsk_f32"):
         assert k.encode() in blob
 
