@@ -12,9 +12,11 @@ to the next, replayed from the same prefilled KV cache every step.  The
 timed region covers K steps; `value` is decode tokens per second over it.
 Prefill throughput (prompt tokens / prefill time) is reported beside it.
 
-roofline: the dominant kernel is the decode step itself (one replayed graph
-per token); achieved = algorithmic bytes per step / the step's mean duration
-from HIP events on the library stream, bytes per token from the formula
+roofline: the dominant kernel is the persistent decode-step kernel
+g2k_step_f16 (one cooperative launch per token running all 48 layers, the
+lm_head and the greedy pick); achieved = algorithmic bytes per launch / the
+mean launch duration from HIP events on the library stream around the 511
+launches, bytes per token from the formula
   w*(L*(3E^2 + E^2 + 2EF) + E*V) + kvb*2*L*E*T + 4*(13*L*E + 2E) + w*2E + kvb*2*L*E
 (weights, K/V reads over T = pos+1 positions, biases and LayerNorm
 parameters, embedding rows, K/V writes), against MI355X's 8 TB/s HBM peak.
@@ -123,6 +125,7 @@ def main():
     prefill_tok_s = P / (min(prefill_ms) * 1e-3)
 
     # decode: W untimed steps, then K timed steps of 511 forwards each
+    ref_ids = None
     for _ in range(args.warmup):
         ref_ids, _ = m.decode_run(first_tok, P, n_dec)
     g2.sync()
@@ -131,7 +134,9 @@ def main():
     for _ in range(args.steps):
         out, ms = m.decode_run(first_tok, P, n_dec)
         ev_ms.append(ms)
-        if not np.array_equal(out, ref_ids):
+        if ref_ids is None:
+            ref_ids = out
+        elif not np.array_equal(out, ref_ids):
             raise SystemExit("bench.py: decode steps disagree with each other (non-deterministic output)")
     g2.sync()
     wall = time.perf_counter() - t_start
@@ -148,13 +153,15 @@ def main():
         "config": {"workload": f"GPT-2 {args.config.upper()} {'fp16' if f16 else 'fp32'}-weight batch-1 greedy "
                                f"decode: {P}-token random prompt, {n_dec} decode forwards (positions {P}..{P + n_dec - 1})",
                    "weights": "f16" if f16 else "f32", "kv_cache": "f32", "accumulate": "f32",
-                   "decode_graph_replay": bool(m.uses_graph() == 1)},
+                   "decode_engine": "persistent step kernel" if m.uses_step() else
+                   ("per-operator kernels, graph replay" if m.uses_graph() == 1 else "per-operator kernels")},
         "prefill_tok_s": round(prefill_tok_s, 1),
         "prefill_ms": round(min(prefill_ms), 3),
         "decode_ms_per_token": round(step_ms_events / n_dec, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode step (one replayed graph per token)",
+                     "kernel": (f"g2k_step_{'f16' if f16 else 'f32'} (one launch per decode token)" if m.uses_step()
+                                else "decode step (per-operator kernels)"),
                      "bytes_per_launch": round(bytes_step / n_dec)},
     }
     if not args.no_cpu_baseline:

@@ -51,7 +51,8 @@
     X(GEMM_NK_F16_RESID, "g2k_gemm_nk_f16_resid")                             \
     X(GEMM_NK_F32_QKV, "g2k_gemm_nk_f32_qkv")                                 \
     X(GEMM_NK_F16_QKV, "g2k_gemm_nk_f16_qkv")                                 \
-    X(ATTN_PREFILL, "g2k_attn_prefill")
+    X(ATTN_PREFILL, "g2k_attn_prefill")                                       \
+    X(STEP_F32, "g2k_step_f32") X(STEP_F16, "g2k_step_f16")
 
 #define G2_ENUM_ENTRY(id, name) G2F_##id,
 enum { G2_KERNEL_LIST(G2_ENUM_ENTRY) G2F_COUNT };
@@ -73,6 +74,10 @@ int g2i_hip(hipError_t e, const char *what);
 int g2i_ready(void);
 hipStream_t g2i_stream(void);
 int g2i_launch(int fid, unsigned gx, unsigned gy, unsigned bx, void *args);
+/* Cooperative launch (all gx work-groups co-resident) of a 1-D grid. */
+int g2i_coop_launch(int fid, unsigned gx, unsigned bx, void *args);
+/* Work-groups of the persistent step kernel's grid (0: not supported). */
+int g2i_step_wgs(void);
 int g2i_device_alloc(void **p, size_t bytes);
 /* Launch a packed-matvec kernel: fid_f32_64 is the epilogue's first table
  * entry (f32, 64-lane shape); the lane shape and grid follow from K. */

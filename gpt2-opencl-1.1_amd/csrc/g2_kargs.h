@@ -23,9 +23,13 @@ enum {
     G2S_MIN_NEW = 2,  /* EOS is masked while G2S_NGEN < G2S_MIN_NEW          */
     G2S_NGEN = 3,     /* tokens selected so far in this generation           */
     G2S_ERR = 4,      /* sticky error bits set by kernels (bounds clamps)    */
+    G2S_SEQ = 5,      /* decode steps run by the persistent step kernel      */
     G2S_IDS = 16,     /* ids selected, G2S_IDS + k for the k-th selection    */
     G2S_WORDS = 16 + 1024
 };
+
+/* G2S_ERR bits */
+#define G2_ERR_STEP_TIMEOUT 4 /* a step-kernel exchange wait ran out of time */
 
 /* GEMM: C[M,N] = A[M,K] * op(B) with an epilogue.
  * B layout G2_BKN: [K,N] row-major (the reference's device layout);
@@ -165,6 +169,60 @@ typedef struct {
     int *state;
     int n_parts, N, advance;
 } g2_amerge_args;
+
+/* Persistent decode step (one cooperative launch per token, 512 threads per
+ * work-group, one work-group per CU).  Per-layer weights come from a device
+ * array of g2_step_layer.  Work-groups hand vectors to each other through
+ * the exchange area `xbuf` of 64-bit words (value in the low half, the
+ * step's tag in the high half); its layout is fixed by the G2X_* offsets
+ * below and sized with G2X_TOTAL_WORDS. */
+typedef struct {
+    const float *ln1_w, *ln1_b, *qkv_b, *proj_b, *ln2_w, *ln2_b, *fc_b, *fc2_b;
+    const void *qkv_w, *proj_w, *fc_w, *fc2_w;
+    float *k_cache, *v_cache;
+} g2_step_layer;
+
+typedef struct {
+    const g2_step_layer *layers;
+    const void *wte;
+    const void *wpe;
+    const void *lm_w;
+    const float *lnf_w;
+    const float *lnf_b;
+    float *logits;
+    int *state;
+    unsigned long long *xbuf;
+    /* optional phase timestamps (100 MHz clock): work-group w writes
+     * trace[w * G2_TRACE_STRIDE(L) + 16*l + k] for phase boundary k of layer
+     * l, and 16*L + k for the lm_head and the pick; NULL: off */
+    unsigned long long *trace;
+    int L, E, F, NH, V, S;
+    int xlayer; /* words per layer region */
+    float scale;
+} g2_step_args;
+
+#define G2_TRACE_STRIDE(L) (16 * (L) + 4)
+
+#define G2_STEP_THREADS 512
+#define G2_STEP_MAXE 1600   /* largest n_embd the step kernel holds in LDS */
+#define G2_STEP_MAXF 6400   /* largest ffn width */
+#define G2_STEP_MAXUNITS 512 /* (row, segment) units per work-group and phase */
+#define G2_STEP_MAXCH 16    /* 64-position key chunks per head */
+#define G2X_HEAD 64         /* words before the first layer region (word 0: abort) */
+
+/* Word offsets inside one layer region (E = n_embd, NH heads, F = ffn):
+ * QKV outputs [3E], attention chunk partials [NH][G2_STEP_MAXCH][66],
+ * merged attention O [E], X1 = x + proj [E], H = gelu(fc) [F],
+ * X2 = X1 + fc2 [E]; regions are padded to 32 words. */
+#define G2X_ATT(E) (3 * (E))
+#define G2X_O(E, NH) (3 * (E) + (NH) * G2_STEP_MAXCH * 66)
+#define G2X_X1(E, NH) (G2X_O(E, NH) + (E))
+#define G2X_H(E, NH) (G2X_X1(E, NH) + (E))
+#define G2X_X2(E, NH, F) (G2X_H(E, NH) + (F))
+#define G2X_LAYER_WORDS(E, NH, F) ((G2X_X2(E, NH, F) + (E) + 31) & ~31)
+/* Total words: header, L layer regions, 2 argmax words per work-group. */
+#define G2X_TOTAL_WORDS(L, E, NH, F, nwg) \
+    ((long)G2X_HEAD + (long)(L) * G2X_LAYER_WORDS(E, NH, F) + 2L * (nwg) + 32)
 
 /* Causal attention over a prompt block: rows i < P of q[P,E]; keys/values
  * j <= i from the transposed K cache and the V cache; head dim 64. */

@@ -555,3 +555,6 @@ G2K void g2k_attn_prefill(const g2_attnp_args a)
 
 /* Fused decode kernels (packed matvecs, single-query attention). */
 #include "g2_decode.hip"
+
+/* The persistent decode step (one cooperative launch per token). */
+#include "g2_step.hip"

@@ -49,6 +49,16 @@ struct g2_model {
     /* fused path */
     int *state;
     float *att_part, *am_part;
+    /* persistent step kernel: per-layer pointer table, exchange area */
+    g2_step_layer *step_layers;
+    unsigned long long *xbuf;
+    size_t xbuf_bytes;
+    int step_wgs;  /* grid of the step kernel, 0 if this model cannot use it */
+    int step_on;   /* decode steps run the step kernel */
+    int step_ran;  /* a step kernel ran since the last error check */
+    const char *step_why; /* why the step kernel cannot run this model */
+    unsigned long long *trace; /* phase timestamps, when G2_STEP_TRACE names a file */
+    size_t trace_words;
     hipGraphExec_t step_exec;
     int graph_state; /* 0 not built, 1 ready, -1 capture unsupported */
     hipEvent_t ev[3];
@@ -150,6 +160,72 @@ static int check_model_config(const g2_config *c, int dtype, int path)
     return G2_OK;
 }
 
+/* (row, segment) units one work-group of the step kernel takes for an
+ * N x K packed matrix: rows split evenly, each row in 1, 2, 4 or 8
+ * segments of at most 256 16-byte chunks (more is not supported). */
+static int step_units(int N, int K, int elems_per_chunk, int nwg)
+{
+    const int C = K / elems_per_chunk, need = (C + 255) / 256;
+    if (need > 8) return 1 << 30;
+    const int nseg = need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : 8));
+    return ((N + nwg - 1) / nwg) * nseg;
+}
+
+/* Whether the persistent step kernel can run this model: fused path, a
+ * device grid, the kernel's LDS ceilings (n_embd <= G2_STEP_MAXE, ffn <=
+ * G2_STEP_MAXF) and at most G2_STEP_MAXUNITS units per work-group in every
+ * matrix.  On refusal `why` names the reason. */
+static int step_supported(const g2_model *m, int nwg, const char **why)
+{
+    const g2_config *c = &m->cfg;
+    const int ve = m->dtype == G2_F16 ? 8 : 4;
+    const int E = c->n_embd, F = c->ffn_dim, V = c->vocab_size;
+    if (m->path != G2_PATH_FUSED) { *why = "not the fused path"; return 0; }
+    if (nwg <= 0 || nwg > G2_STEP_THREADS) { *why = "the device has no cooperative step grid"; return 0; }
+    if (E > G2_STEP_MAXE || F > G2_STEP_MAXF) { *why = "n_embd or ffn above the step kernel's ceilings"; return 0; }
+    if (E % ve || F % ve || E != 64 * c->n_head) { *why = "sizes not multiples of the weight chunk or head dim not 64"; return 0; }
+    const int dims[5][2] = { { 3 * E, E }, { E, E }, { F, E }, { E, F }, { V, E } };
+    for (int i = 0; i < 5; ++i)
+        if (step_units(dims[i][0], dims[i][1], ve, nwg) > G2_STEP_MAXUNITS) { *why = "a matrix exceeds the units per work-group"; return 0; }
+    *why = NULL;
+    return 1;
+}
+
+/* Device tables of the step kernel (after the weights are uploaded). */
+static int step_setup(g2_model *m)
+{
+    const int nwg = g2i_step_wgs();
+    if (!step_supported(m, nwg, &m->step_why)) return G2_OK;
+    const g2_config *c = &m->cfg;
+    const int L = c->n_layer;
+    g2_step_layer *t = calloc((size_t)L, sizeof *t);
+    if (!t) return g2i_err(G2_E_NOMEM, "step layer table");
+    for (int l = 0; l < L; ++l) {
+        const g2_layer *y = &m->L[l];
+        t[l].ln1_w = y->ln1_w; t[l].ln1_b = y->ln1_b; t[l].qkv_b = y->qkv_b; t[l].proj_b = y->proj_b;
+        t[l].ln2_w = y->ln2_w; t[l].ln2_b = y->ln2_b; t[l].fc_b = y->fc_b; t[l].fc2_b = y->fc2_b;
+        t[l].qkv_w = y->qkv_w; t[l].proj_w = y->proj_w; t[l].fc_w = y->fc_w; t[l].fc2_w = y->fc2_w;
+        t[l].k_cache = y->k_cache; t[l].v_cache = y->v_cache;
+    }
+    int rc = dev_alloc(m, (void **)&m->step_layers, (size_t)L * sizeof *t, 0);
+    if (!rc) rc = up(m->step_layers, t, (size_t)L * sizeof *t);
+    free(t);
+    m->xbuf_bytes = (size_t)G2X_TOTAL_WORDS(L, c->n_embd, c->n_head, c->ffn_dim, nwg) * 8;
+    if (!rc) rc = dev_alloc(m, (void **)&m->xbuf, m->xbuf_bytes, 0);
+    if (!rc) rc = g2i_hip(hipMemsetAsync(m->xbuf, 0, m->xbuf_bytes, g2i_stream()), "exchange clear");
+    if (rc) return rc;
+    m->step_wgs = nwg;
+    const char *env = getenv("G2_STEP");
+    m->step_on = !(env && env[0] == '0');
+    const char *tr = getenv("G2_STEP_TRACE");
+    if (tr && tr[0]) {
+        m->trace_words = (size_t)nwg * G2_TRACE_STRIDE(L);
+        rc = dev_alloc(m, (void **)&m->trace, m->trace_words * 8, 0);
+        if (!rc) rc = g2i_hip(hipMemsetAsync(m->trace, 0, m->trace_words * 8, g2i_stream()), "trace clear");
+    }
+    return rc;
+}
+
 static int alloc_workspaces(g2_model *m)
 {
     const size_t E = (size_t)m->cfg.n_embd, F = (size_t)m->cfg.ffn_dim, T = 3 * E;
@@ -172,6 +248,7 @@ static int alloc_workspaces(g2_model *m)
     }
 #undef A
     if (!rc) rc = g2i_hip(hipMemsetAsync(m->state, 0, G2S_WORDS * 4, g2i_stream()), "state clear");
+    if (!rc) rc = step_setup(m);
     if (!rc) rc = g2i_hip(hipStreamSynchronize(g2i_stream()), "workspace sync");
     if (!rc) {
         m->host_logits = malloc(V * sizeof(float));
@@ -211,7 +288,7 @@ int g2_model_free(g2_model *m)
     void *bufs[] = { m->wte, m->wpe, m->lnf_w, m->lnf_b, m->lm_head, m->hidden, m->ln_out,
                      m->attn, m->attn_proj, m->ffn1, m->ffn2, m->qkv_new, m->qkv_full,
                      m->last_hidden, m->logits, m->partial, m->scores, m->q, m->ids_dev,
-                     m->state, m->att_part, m->am_part };
+                     m->state, m->att_part, m->am_part, m->step_layers, m->xbuf, m->trace };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; ++i)
         if (bufs[i]) hipFree(bufs[i]);
     for (int l = 0; l < m->cfg.n_layer; ++l) {
@@ -482,6 +559,22 @@ int g2_model_set_kslice(g2_model *m, int kslice)
 
 size_t g2_model_weight_bytes(const g2_model *m) { return m ? m->weight_bytes : 0; }
 
+int g2_model_set_step(g2_model *m, int on)
+{
+    if (!m) return g2i_err(G2_E_ARG, "NULL model");
+    if (on && !m->step_wgs)
+        return g2i_err(G2_E_ARG, "the persistent step kernel cannot run this model: %s (grid %d)",
+                       m->step_why ? m->step_why : "not set up", g2i_step_wgs());
+    m->step_on = on ? 1 : 0;
+    return G2_OK;
+}
+
+int g2_model_uses_step(const g2_model *m)
+{
+    if (!m) return g2i_err(G2_E_ARG, "NULL model");
+    return m->step_on;
+}
+
 int g2_model_uses_graph(const g2_model *m)
 {
     if (!m) return g2i_err(G2_E_ARG, "NULL model");
@@ -624,9 +717,76 @@ static int fused_step_launches(g2_model *m)
     return rc;
 }
 
-/* Run one decode step, replaying the captured graph (captured on first use). */
+/* One decode forward at state[POS] as one cooperative launch of the
+ * persistent step kernel. */
+static int step_launch(g2_model *m)
+{
+    const g2_config *c = &m->cfg;
+    g2_step_args a;
+    memset(&a, 0, sizeof a);
+    a.layers = m->step_layers; a.wte = m->wte; a.wpe = m->wpe; a.lm_w = m->lm_w;
+    a.lnf_w = m->lnf_w; a.lnf_b = m->lnf_b; a.logits = m->logits; a.state = m->state;
+    a.xbuf = m->xbuf;
+    a.trace = m->trace;
+    a.L = c->n_layer; a.E = c->n_embd; a.F = c->ffn_dim; a.NH = c->n_head; a.V = c->vocab_size;
+    a.S = G2_KV_MAX_SEQ;
+    a.xlayer = G2X_LAYER_WORDS(c->n_embd, c->n_head, c->ffn_dim);
+    a.scale = 1.0f / sqrtf(64.0f);
+    m->step_ran = 1;
+    return g2i_coop_launch(m->dtype == G2_F16 ? G2F_STEP_F16 : G2F_STEP_F32, (unsigned)m->step_wgs,
+                           G2_STEP_THREADS, &a);
+}
+
+/* After step kernels ran: fail if one of them abandoned a hand-off (its
+ * outputs are then invalid) and clear the exchange area for the next run. */
+static int step_check(g2_model *m, const int *state_words)
+{
+    if (!m->step_ran) return G2_OK;
+    m->step_ran = 0;
+    int err = 0, rc = G2_OK;
+    if (state_words) err = state_words[G2S_ERR];
+    else {
+        rc = g2i_hip(hipMemcpyAsync(&err, m->state + G2S_ERR, sizeof err, hipMemcpyDeviceToHost,
+                                    g2i_stream()), "step check");
+        if (!rc) rc = g2i_hip(hipStreamSynchronize(g2i_stream()), "step check sync");
+        if (rc) return rc;
+    }
+    if (!(err & G2_ERR_STEP_TIMEOUT)) return G2_OK;
+    const int zero = 0;
+    rc = g2i_hip(hipMemsetAsync(m->xbuf, 0, m->xbuf_bytes, g2i_stream()), "exchange clear");
+    if (!rc) rc = up(m->state + G2S_ERR, &zero, sizeof zero);
+    if (rc) return rc;
+    return g2i_err(G2_E_HIP, "decode step kernel: a hand-off between work-groups timed out; "
+                             "the step's outputs are invalid");
+}
+
+/* With G2_STEP_TRACE=<file>: write the phase timestamps of the last step
+ * (header: work-groups, layers, words per work-group; then the words). */
+static int step_trace_dump(g2_model *m)
+{
+    if (!m->trace) return G2_OK;
+    unsigned long long *h = malloc((m->trace_words + 3) * 8);
+    if (!h) return g2i_err(G2_E_NOMEM, "trace staging");
+    h[0] = (unsigned long long)m->step_wgs;
+    h[1] = (unsigned long long)m->cfg.n_layer;
+    h[2] = (unsigned long long)G2_TRACE_STRIDE(m->cfg.n_layer);
+    int rc = g2i_hip(hipMemcpy(h + 3, m->trace, m->trace_words * 8, hipMemcpyDeviceToHost), "trace read");
+    if (!rc) {
+        FILE *f = fopen(getenv("G2_STEP_TRACE"), "wb");
+        if (f) {
+            fwrite(h, 8, m->trace_words + 3, f);
+            fclose(f);
+        }
+    }
+    free(h);
+    return rc;
+}
+
+/* Run one decode step: the persistent step kernel, or the per-operator
+ * kernels replaying the captured graph (captured on first use). */
 static int fused_step(g2_model *m)
 {
+    if (m->step_on) return step_launch(m);
     if (m->graph_state == 0) {
         const char *env = getenv("G2_NO_GRAPH");
         if (env && env[0] && env[0] != '0') m->graph_state = -1;
@@ -717,7 +877,8 @@ int g2_decode(g2_model *m, int token, int pos)
         return rc ? rc : ref_decode(m, pos);
     }
     int rc = set_state(m, pos, token, 0, 0);
-    return rc ? rc : fused_step(m);
+    if (!rc) rc = fused_step(m);
+    return rc ? rc : step_check(m, NULL);
 }
 
 int g2_read_logits(g2_model *m, float *host, int n)
@@ -828,6 +989,7 @@ int g2_generate(g2_model *m, const int *prompt, int n_prompt, int max_new, int m
     rc = g2i_hip(hipMemcpyAsync(st, m->state, (size_t)G2S_WORDS * sizeof(int), hipMemcpyDeviceToHost,
                                 g2i_stream()), "state readback");
     if (!rc) rc = g2i_hip(hipStreamSynchronize(g2i_stream()), "state sync");
+    if (!rc) rc = step_check(m, st);
     int gen = 0;
     if (!rc) {
         const int total = 1 + n_dec;
@@ -855,6 +1017,8 @@ int g2_decode_run(g2_model *m, int token, int start_pos, int n_steps, int forbid
     for (int s = 0; s < n_steps && !rc; ++s) rc = fused_step(m);
     if (m->events_ok) hipEventRecord(m->ev[1], g2i_stream());
     if (!rc) rc = g2i_hip(hipStreamSynchronize(g2i_stream()), "decode run sync");
+    if (!rc) rc = step_check(m, NULL);
+    if (!rc) rc = step_trace_dump(m);
     if (rc) return rc;
     if (elapsed_ms) *elapsed_ms = ev_ms(m, 0, 1);
     if (out_ids) {

@@ -32,6 +32,7 @@ static const char *const g2_kernel_names[G2F_COUNT] = { G2_KERNEL_LIST(G2_NAME_E
 
 static struct {
     int ready, device, cus;
+    int step_wgs; /* work-groups of a cooperative step launch (0: unsupported) */
     char name[256];
     hipModule_t module;
     hipStream_t stream;
@@ -71,6 +72,15 @@ int g2i_launch(int fid, unsigned gx, unsigned gy, unsigned bx, void *args)
                                          G.stream, params, NULL),
                    g2_kernel_names[fid]);
 }
+
+int g2i_coop_launch(int fid, unsigned gx, unsigned bx, void *args)
+{
+    void *params[1] = { args };
+    return g2i_hip(hipModuleLaunchCooperativeKernel(G.fn[fid], gx, 1, 1, bx, 1, 1, 0, G.stream, params),
+                   g2_kernel_names[fid]);
+}
+
+int g2i_step_wgs(void) { return G.step_wgs; }
 
 int g2i_device_alloc(void **p, size_t bytes)
 {
@@ -158,6 +168,32 @@ int g2_init(int device)
         hipStreamDestroy(G.stream); hipModuleUnload(G.module);
         memset(&G, 0, sizeof G);
         return rc;
+    }
+    /* The persistent step kernel runs one work-group per CU and needs all of
+     * them co-resident: require cooperative launch support and an occupancy
+     * of at least one work-group per CU for both weight types. */
+    {
+        int coop = 0, nb[2] = { -1, -1 };
+        hipError_t ea = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device);
+        hipError_t eo[2] = { hipSuccess, hipSuccess };
+        const int fids[2] = { G2F_STEP_F32, G2F_STEP_F16 };
+        for (int i = 0; i < 2; ++i)
+            eo[i] = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb[i], G.fn[fids[i]], G2_STEP_THREADS, 0);
+        const int ok = ea == hipSuccess && coop && eo[0] == hipSuccess && eo[1] == hipSuccess && nb[0] >= 1 && nb[1] >= 1;
+        G.step_wgs = ok ? prop.multiProcessorCount : 0;
+        if (!ok) {
+            int rtv = 0;
+            hipFuncAttributes fa;
+            memset(&fa, 0, sizeof fa);
+            (void)hipRuntimeGetVersion(&rtv);
+            (void)hipFuncGetAttributes(&fa, (const void *)G.fn[G2F_STEP_F16]);
+            fprintf(stderr, "g2hip: persistent step kernel unavailable (HIP runtime %d, cooperative launch %d, "
+                            "err %d; work-groups per CU %d/%d, err %d/%d; kernel regs %d lds %zu max threads %d); "
+                            "decode uses per-operator kernels\n",
+                    rtv, coop, (int)ea, nb[0], nb[1], (int)eo[0], (int)eo[1], fa.numRegs, fa.sharedSizeBytes,
+                    fa.maxThreadsPerBlock);
+        }
+        (void)hipGetLastError();
     }
     G.device = device;
     G.ready = 1;

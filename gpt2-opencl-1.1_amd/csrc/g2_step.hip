@@ -1,0 +1,800 @@
+/*
+ * g2_step.hip -- one GPT-2 decode forward as a single persistent cooperative
+ * kernel (included by g2_kernels.hip, which provides the shared helpers).
+ *
+ * Why one kernel: on gfx950 every kernel boundary costs several
+ * microseconds (wave start-up, drain, the end-of-kernel L2 write-back of the
+ * 8 XCDs), and the multi-kernel decode crosses five of them per layer.  Here
+ * one launch runs every layer: each work-group (one per CU) owns fixed rows
+ * of every matrix, and work-groups hand the activation vectors to each other
+ * through an exchange area of tagged 64-bit words.
+ *
+ * Exchange protocol: a producer stores (tag << 32 | float bits) with a
+ * relaxed agent-scope atomic store; a consumer loads the words with relaxed
+ * agent-scope atomic loads (coherent across XCDs) until every tag equals
+ * this step's tag.  Each word carries its own validity, so no fence is
+ * needed (an agent-scope release/acquire writes back or invalidates the XCD
+ * L2 and costs microseconds).  Every word is written at most once per
+ * launch; the tag is state[G2S_SEQ] + 1 and work-group 0 advances G2S_SEQ
+ * at the end of the step, so words left by earlier steps never match.  The
+ * KV cache entries of the current position reach the attention through the
+ * exchange area; the cache itself is read only at earlier positions, which
+ * earlier launches wrote.
+ *
+ * Memory-level parallelism: a work-group's weight rows of a matrix are
+ * loaded into registers as soon as the previous matrix held by the same
+ * register set has been used (one set for qkv -> fc -> fc2 -> next qkv, a
+ * small one for proj), so the weight stream runs while the work-group waits
+ * for its next input vector.
+ *
+ * Phases per layer (input -> output, each a hand-off between work-groups):
+ *   QKV   x (X2 of the layer before, or the embedding) -> LayerNorm ->
+ *         qkv rows; writes q/k/v to the exchange and k/v to the KV cache
+ *   ATTN  (head, 64-position chunk) units -> (max, sum, o[64]) partials
+ *   MERGE one work-group per head -> O
+ *   PROJ  O -> proj rows + bias + x -> X1
+ *   FC    X1 -> LayerNorm -> fc rows + bias -> GELU -> H
+ *   FC2   H -> fc2 rows + bias + X1 -> X2
+ * then LM (LayerNorm + logits over the tied head + per-work-group first-max)
+ * and the greedy pick by work-group 0, which advances the device state.
+ *
+ * Every wait is bounded in time: a wait that runs out (100 ms) sets
+ * G2_ERR_STEP_TIMEOUT in the state and raises the abort word, after which
+ * every wait of every work-group returns at once, so the grid always
+ * drains.  The launch is cooperative (all work-groups co-resident), so no
+ * wait depends on a work-group that has not started.
+ */
+
+namespace g2step {
+
+constexpr int NT = G2_STEP_THREADS;                     /* 512 threads    */
+constexpr int NW = NT / 64;                             /* 8 waves        */
+constexpr int UMAX = 4;                                 /* units per wave, main set */
+constexpr int UPROJ = 1;                                /* units per wave, proj set */
+constexpr int SEGC = 256;                               /* chunks per unit: 64 lanes x 4 */
+constexpr int PMAX = (G2_STEP_MAXF + NT - 1) / NT;      /* exchange words per thread */
+constexpr unsigned long long WAIT_LIMIT = 10000000ull;  /* 100 ms of the 100 MHz clock */
+constexpr unsigned long long ABORT_CHECK_AFTER = 200000ull; /* 2 ms */
+
+typedef unsigned long long u64;
+
+/* Pointers read from the per-layer table are generic; device memory
+ * accessed through them must be addressed as global so the compiler emits
+ * global (not flat) loads: flat loads also count against the LDS counter,
+ * which would make every LDS access and barrier wait for the weight stream. */
+#define G2_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ const G2_GLOBAL T *gl(const T *p) { return (const G2_GLOBAL T *)p; }
+template <typename T>
+__device__ __forceinline__ G2_GLOBAL T *glw(T *p) { return (G2_GLOBAL T *)p; }
+/* LDS flags likewise: through a generic pointer they become flat accesses,
+ * which wait for every outstanding global load. */
+#define G2_LDS __attribute__((address_space(3)))
+/* The per-layer table is read-only for the whole launch: reading it through
+ * the constant address space lets the compiler use scalar loads, so weight
+ * addresses are a scalar base plus a lane offset (no vector-loaded pointer
+ * whose wait would be merged into every weight load). */
+#define G2_CONST __attribute__((address_space(4)))
+typedef G2_LDS volatile int lds_flag;
+
+__device__ __forceinline__ void ll_put(u64 *p, float v, unsigned tag)
+{
+    __hip_atomic_store(p, ((u64)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ u64 ll_get(const u64 *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned ll_tag(u64 w) { return (unsigned)(w >> 32); }
+__device__ __forceinline__ float ll_val(u64 w) { return __uint_as_float((unsigned)w); }
+
+/* Wave-wide sum / max through DPP lane moves (no LDS traffic): butterfly
+ * within quads, rotations within 16-lane rows, then the four row results
+ * combined in row order.  Every lane gets the result. */
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_lane(float v, int lane)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ float wsum(float v)
+{
+    v += dpp<0xB1>(v);  /* quad_perm [1,0,3,2] */
+    v += dpp<0x4E>(v);  /* quad_perm [2,3,0,1] */
+    v += dpp<0x124>(v); /* row_ror:4 */
+    v += dpp<0x128>(v); /* row_ror:8 */
+    return ((row_lane(v, 0) + row_lane(v, 16)) + row_lane(v, 32)) + row_lane(v, 48);
+}
+__device__ __forceinline__ float wmax(float v)
+{
+    v = fmaxf(v, dpp<0xB1>(v));
+    v = fmaxf(v, dpp<0x4E>(v));
+    v = fmaxf(v, dpp<0x124>(v));
+    v = fmaxf(v, dpp<0x128>(v));
+    return fmaxf(fmaxf(row_lane(v, 0), row_lane(v, 16)), fmaxf(row_lane(v, 32), row_lane(v, 48)));
+}
+
+struct ctx {
+    unsigned tag;
+    u64 *abort_w;
+    int *state;
+    lds_flag *dead; /* this work-group stopped waiting */
+};
+
+/* A wait ran out of time: record it and release every work-group. */
+__device__ __noinline__ void give_up(const ctx &c)
+{
+    atomicOr(c.state + G2S_ERR, G2_ERR_STEP_TIMEOUT);
+    ll_put(c.abort_w, 0.f, c.tag);
+    *c.dead = 1;
+}
+
+/* Bounded wait on a list of words already loaded into v[]: reload the ones
+ * whose tag is stale (with a short back-off) until all match, the abort
+ * word is raised or time runs out.  idx(i) < 0 marks an unused slot. */
+template <int NP, typename IDX>
+__device__ __forceinline__ void settle(const ctx &c, const u64 *src, u64 (&v)[NP], IDX idx)
+{
+    unsigned bad = 0;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) bad |= (unsigned)(ll_tag(v[i]) != c.tag);
+    if (!bad || *c.dead) return;
+    const u64 t0 = wall_clock64();
+    for (;;) {
+        __builtin_amdgcn_s_sleep(4);
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const int w = idx(i);
+            if (w >= 0 && ll_tag(v[i]) != c.tag) v[i] = ll_get(src + w);
+        }
+        bad = 0;
+#pragma unroll
+        for (int i = 0; i < NP; ++i) bad |= (unsigned)(ll_tag(v[i]) != c.tag);
+        if (!bad || *c.dead) return;
+        /* the abort word is consulted only by waits that already took long
+         * (every waiting thread reading one word would be a hot spot) */
+        const u64 el = wall_clock64() - t0;
+        if (el > ABORT_CHECK_AFTER) {
+            if (ll_tag(ll_get(c.abort_w)) == c.tag) { *c.dead = 1; return; }
+            if (el > WAIT_LIMIT) { give_up(c); return; }
+        }
+    }
+}
+
+/* All threads: dst[w] = value of src[w] for w < n <= NP*NT once it carries
+ * the tag (thread tid takes w = tid + NT*i).
+ *
+ * Waiting must not flood the memory system: if every thread of every
+ * work-group re-read all of its words each round trip, a 6400-word vector
+ * would cost ~13 MB of coherent reads per round, competing with the weight
+ * stream.  So after one speculative read of everything, a work-group that
+ * found stale words waits on nsent sentinel words only (word n*k/nsent for
+ * k < nsent: the first word of each producer when n is split evenly over
+ * nsent producers), then re-reads just its stale words.  Ends with a
+ * barrier; `flag` is an LDS word of the caller. */
+template <int NP>
+__device__ __forceinline__ void fetch(int tid, const ctx &c, const u64 *src, int n, int nsent,
+                                      float *dst, lds_flag *flag)
+{
+    const u64 filler = (u64)c.tag << 32;
+    u64 v[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const int w = tid + NT * i;
+        v[i] = w < n ? ll_get(src + w) : filler;
+    }
+    if (tid == 0) *flag = 0;
+    __syncthreads();
+    unsigned bad = 0;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) bad |= (unsigned)(ll_tag(v[i]) != c.tag);
+    if (bad) *flag = 1;
+    __syncthreads();
+    if (*flag && !*c.dead) {
+        if (tid < nsent) {
+            const int w = (int)(((long)n * tid) / nsent);
+            u64 sv[1] = {ll_get(src + w)};
+            settle(c, src, sv, [&](int) { return w; });
+        }
+        __syncthreads();
+        settle(c, src, v, [&](int i) { const int w = tid + NT * i; return w < n ? w : -1; });
+    }
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+        const int w = tid + NT * i;
+        if (w < n) dst[w] = ll_val(v[i]);
+    }
+    __syncthreads();
+}
+
+/* Sum over the 512-thread work-group, wave totals added in wave order.
+ * `red` must not be rewritten before every thread has read it (callers
+ * alternate buffers). */
+__device__ __forceinline__ float blk_sum(int tid, float v, float *red)
+{
+    v = wsum(v);
+    if ((tid & 63) == 0) red[tid >> 6] = v;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) t += red[w];
+    return t;
+}
+
+/* LayerNorm parameters of the thread's entries i = tid + NT*k, loaded at
+ * the start of a phase so their latency overlaps the input wait. */
+template <int NE>
+struct ln_params {
+    float g[NE], b[NE];
+};
+
+template <int NE>
+__device__ __forceinline__ ln_params<NE> ln_load(int tid, const G2_GLOBAL float *g, const G2_GLOBAL float *b, int E)
+{
+    ln_params<NE> p;
+#pragma unroll
+    for (int k = 0; k < NE; ++k) {
+        const int i = tid + NT * k;
+        p.g[k] = i < E ? g[i] : 0.f;
+        p.b[k] = i < E ? b[i] : 0.f;
+    }
+    return p;
+}
+
+/* xin = LayerNorm(x) over E entries (both in LDS): mean, then biased
+ * variance of (x - mean), eps 1e-5, (x - mean) * inv_std * g + b
+ * (layernorm, math.cl:283-311).  Ends with a barrier. */
+template <int NE>
+__device__ __forceinline__ void layernorm(int tid, const float *x, float *xin, const ln_params<NE> &lp,
+                                          int E, float *red)
+{
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < NE; ++k) {
+        const int i = tid + NT * k;
+        if (i < E) s += x[i];
+    }
+    const float mean = blk_sum(tid, s, red) / (float)E;
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < NE; ++k) {
+        const int i = tid + NT * k;
+        if (i < E) {
+            const float d = x[i] - mean;
+            q = fmaf(d, d, q);
+        }
+    }
+    const float inv = 1.0f / sqrtf(blk_sum(tid, q, red + NW) / (float)E + 1e-5f);
+#pragma unroll
+    for (int k = 0; k < NE; ++k) {
+        const int i = tid + NT * k;
+        if (i < E) xin[i] = fmaf((x[i] - mean) * inv, lp.g[k], lp.b[k]);
+    }
+    __syncthreads();
+}
+
+/* A work-group's share of one packed matrix W[N,K] (output-major): rows
+ * [r0, r0+nrows), each split into nseg (1, 2, 4 or 8: a divisor of the wave
+ * count, so every unit of a wave has the segment wave % nseg) segments of
+ * SL <= 256 16-byte chunks; a (row, segment) unit is one wave's job (64
+ * lanes x up to 4 chunks).  With
+ * a register set of UM units per wave, unit u belongs to wave u % NW, slot
+ * (u / NW) % UM, batch u / (NW * UM). */
+struct plan {
+    const u32x4 *W;
+    int C, nseg, SL, r0, nrows, nunits;
+};
+
+template <typename WT>
+__device__ __forceinline__ plan make_plan(const void *W, int N, int K)
+{
+    constexpr int VE = chunk_t<WT>::V;
+    plan p;
+    p.W = (const u32x4 *)W;
+    p.C = K / VE;
+    const int need = (p.C + SEGC - 1) / SEGC;
+    p.nseg = need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : 8));
+    p.SL = (p.C + p.nseg - 1) / p.nseg;
+    const long nwg = gridDim.x, wg = blockIdx.x;
+    p.r0 = (int)(((long)N * wg) / nwg);
+    p.nrows = (int)(((long)N * (wg + 1)) / nwg) - p.r0;
+    p.nunits = p.nrows * p.nseg;
+    return p;
+}
+
+/* Issue the loads of one batch (NW*UM units) into a register set. */
+template <int UM>
+__device__ __forceinline__ void load_set(int tid, u32x4 (&w)[UM][4], const plan &p, int batch)
+{
+    const int wave = tid >> 6, lane = tid & 63;
+#pragma unroll
+    for (int j = 0; j < UM; ++j) {
+        const int u = batch * NW * UM + wave + NW * j;
+        const bool uv = u < p.nunits;
+        const int row = p.r0 + (uv ? u / p.nseg : 0);
+        const int c0 = (uv ? u % p.nseg : 0) * p.SL;
+        const int c1 = min(p.C, c0 + p.SL);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int cc = c0 + lane + 64 * i;
+            w[j][i] = (u32x4){0u, 0u, 0u, 0u};
+            if (uv && cc < c1) w[j][i] = __builtin_nontemporal_load(gl(p.W) + (size_t)row * p.C + cc);
+        }
+    }
+}
+
+/* Dot products of a loaded batch with xin (LDS); unit sums to part[u].
+ * Every unit of the wave covers the same chunks of x, so they are read from
+ * LDS once. */
+template <typename WT, int UM>
+__device__ __forceinline__ void dot_set(int tid, const u32x4 (&w)[UM][4], const plan &p, int batch,
+                                        const float *xin, float *part)
+{
+    constexpr int VE = chunk_t<WT>::V;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int c0 = (wave % p.nseg) * p.SL;
+    const int c1 = min(p.C, c0 + p.SL);
+    if (batch * NW * UM + wave >= p.nunits) return; /* wave-uniform */
+    float xv[4][VE];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int cc = c0 + lane + 64 * i;
+#pragma unroll
+        for (int e = 0; e < VE; e += 4) {
+            f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
+            if (cc < c1) v = *(const f32x4 *)(xin + cc * VE + e);
+            xv[i][e] = v.x; xv[i][e + 1] = v.y; xv[i][e + 2] = v.z; xv[i][e + 3] = v.w;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < UM; ++j) {
+        const int u = batch * NW * UM + wave + NW * j;
+        if (u >= p.nunits) break; /* wave-uniform */
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc += chunk_dot<WT>(w[j][i], xv[i]);
+        acc = wsum(acc);
+        if (lane == 0) part[u] = acc;
+    }
+}
+
+/* The whole matrix share: batch 0 from the preloaded set, later batches
+ * loaded on demand into the same set.  Ends with a barrier. */
+template <typename WT, int UM>
+__device__ __forceinline__ void matvec(int tid, u32x4 (&w)[UM][4], const plan &p, const float *xin,
+                                       float *part)
+{
+    dot_set<WT, UM>(tid, w, p, 0, xin, part);
+    for (int b = 1; b * NW * UM < p.nunits; ++b) {
+        load_set<UM>(tid, w, p, b);
+        dot_set<WT, UM>(tid, w, p, b, xin, part);
+    }
+    __syncthreads();
+}
+
+/* Row t's dot product from its segment sums (in segment order). */
+__device__ __forceinline__ float row_sum(const plan &p, const float *part, int t)
+{
+    float v = part[t * p.nseg];
+    for (int s = 1; s < p.nseg; ++s) v += part[t * p.nseg + s];
+    return v;
+}
+
+/* Per-half LDS of the attention phase. */
+struct att_lds {
+    float q[64], kn[64], vn[64];
+    float red[16][65];
+    float pr[64];
+    float stat[2];
+};
+
+/* Cached keys and values of one 64-position chunk, loaded into registers
+ * ahead of the attention (they do not depend on this position's q).
+ * Scores: thread (pq = t%16, dg = t/16) of a half takes positions
+ * j0+4pq..+3 and dims 4dg..+3 (four 16-byte loads of the transposed K
+ * cache); weighted sum: thread (d4 = t%16, jg = t/16) takes dims 4d4..+3
+ * and positions j0+4jg..+3 (four 16-byte loads of the V cache).  The
+ * current position is not read from the cache. */
+struct att_regs {
+    f32x4 kv[4], vv[4];
+};
+
+__device__ __forceinline__ void attn_load(int tid, const g2_step_layer &y, att_regs &r, bool on, int h,
+                                          int ch, int pos, int T, int E, int S)
+{
+    const int t = tid & 255;
+    const int j0 = ch * 64;
+    const int pq = t & 15, dg = t >> 4, jk = j0 + 4 * pq;
+    const int d4 = t & 15, jg = t >> 4;
+    if (on && jk < T) {
+        const G2_GLOBAL f32x4 *kb = gl((const f32x4 *)(y.k_cache + (size_t)(h * 64 + 4 * dg) * S + jk));
+#pragma unroll
+        for (int d = 0; d < 4; ++d) r.kv[d] = kb[(size_t)d * (S / 4)];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int j = j0 + 4 * jg + e;
+        if (on && j < T && j != pos) r.vv[e] = *gl((const f32x4 *)(y.v_cache + (size_t)j * E + h * 64 + 4 * d4));
+    }
+}
+
+/* One 64-position chunk c of single-query attention for head h by the 256
+ * threads of one half of the work-group (t = thread in the half): the
+ * computation of g2k_attn_part, with the current position's key and value
+ * taken from the exchange.  `on` is false for a half without a unit; it
+ * still takes part in the barriers. */
+__device__ __forceinline__ void attn_chunk(int tid, const ctx &c, const g2_step_args &a, const u64 *R,
+                                           att_lds &L, att_regs &r, bool on, int h, int ch, int pos,
+                                           int T)
+{
+    const int t = tid & 255;
+    const int E = a.E;
+    const int j0 = ch * 64;
+    const int pq = t & 15, dg = t >> 4, jk = j0 + 4 * pq;
+    const int d4 = t & 15, jg = t >> 4;
+    /* q, k and v of head h at this position */
+    if (on && t < 192) {
+        const int part = t >> 6, d = t & 63;
+        const int w = part * E + h * 64 + d;
+        u64 v[1] = {ll_get(R + w)};
+        settle(c, R, v, [&](int) { return w; });
+        float *dst = part == 0 ? L.q : (part == 1 ? L.kn : L.vn);
+        dst[d] = ll_val(v[0]);
+    }
+    __syncthreads();
+    if (on) {
+        float s[4] = {0.f, 0.f, 0.f, 0.f};
+        if (jk < T) {
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                f32x4 kv = r.kv[d];
+                if (pos >= jk && pos < jk + 4) kv[pos - jk] = L.kn[4 * dg + d];
+                const float qv = L.q[4 * dg + d];
+                s[0] = fmaf(qv, kv.x, s[0]);
+                s[1] = fmaf(qv, kv.y, s[1]);
+                s[2] = fmaf(qv, kv.z, s[2]);
+                s[3] = fmaf(qv, kv.w, s[3]);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) L.red[dg][4 * pq + e] = s[e];
+    }
+    __syncthreads();
+    if (on && t < 64) {
+        const bool ok = j0 + t < T;
+        float s = 0.f;
+#pragma unroll
+        for (int g = 0; g < 16; ++g) s += L.red[g][t];
+        s *= a.scale;
+        const float m = wmax(ok ? s : -INFINITY);
+        const float p = ok ? expf(s - m) : 0.f;
+        const float l = wsum(p);
+        L.pr[t] = p;
+        if (t == 0) { L.stat[0] = m; L.stat[1] = l; }
+    }
+    __syncthreads();
+    if (on) {
+        float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int jj = 4 * jg + e, j = j0 + jj;
+            if (j < T) {
+                const float p = L.pr[jj];
+                f32x4 v = r.vv[e];
+                if (j == pos) v = (f32x4){L.vn[4 * d4], L.vn[4 * d4 + 1], L.vn[4 * d4 + 2], L.vn[4 * d4 + 3]};
+                o[0] = fmaf(p, v.x, o[0]);
+                o[1] = fmaf(p, v.y, o[1]);
+                o[2] = fmaf(p, v.z, o[2]);
+                o[3] = fmaf(p, v.w, o[3]);
+            }
+        }
+#pragma unroll
+        for (int f = 0; f < 4; ++f) L.red[jg][4 * d4 + f] = o[f];
+    }
+    __syncthreads();
+    if (on && t < 64) {
+        float o = 0.f;
+#pragma unroll
+        for (int g = 0; g < 16; ++g) o += L.red[g][t];
+        u64 *pp = (u64 *)R + G2X_ATT(E) + ((size_t)h * G2_STEP_MAXCH + ch) * 66;
+        ll_put(pp + 2 + t, o, c.tag);
+        if (t == 0) {
+            ll_put(pp, L.stat[0], c.tag);
+            ll_put(pp + 1, L.stat[1], c.tag);
+        }
+    }
+}
+
+__device__ __forceinline__ bool am_better2(float v1, int i1, float v2, int i2)
+{
+    return v1 > v2 || (v1 == v2 && i1 < i2);
+}
+
+/* First-max over the work-group's (bv, bi); result in amv[0], ami[0]. */
+__device__ __forceinline__ void blk_argmax(int tid, float bv, int bi, float *amv, int *ami)
+{
+    amv[tid] = bv;
+    ami[tid] = bi;
+    __syncthreads();
+    for (int s = NT / 2; s > 0; s >>= 1) {
+        if (tid < s && am_better2(amv[tid + s], ami[tid + s], amv[tid], ami[tid])) {
+            amv[tid] = amv[tid + s];
+            ami[tid] = ami[tid + s];
+        }
+        __syncthreads();
+    }
+}
+
+/* Phase timestamps (only when the caller passed a trace buffer). */
+#define TRACE(k)                                                                       \
+    do {                                                                               \
+        if (a.trace && tid == 0)                                                       \
+            a.trace[(size_t)wg * G2_TRACE_STRIDE(a.L) + 16 * l + (k)] = wall_clock64(); \
+    } while (0)
+
+/* The thread index as a value the compiler cannot prove loop-invariant:
+ * taken fresh in every phase, it keeps per-phase lane arithmetic from being
+ * hoisted out of the layer loop (which would hold it in registers across
+ * all 48 layers). */
+__device__ __forceinline__ int fresh_tid()
+{
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
+template <typename WT>
+__device__ __forceinline__ void step_impl(const g2_step_args &a)
+{
+    /* 16-byte alignment: the dot products read 16-byte chunks of these */
+    __shared__ __attribute__((aligned(16))) float xin[G2_STEP_MAXF];
+    __shared__ __attribute__((aligned(16))) float xres[G2_STEP_MAXE];
+    __shared__ float part[G2_STEP_MAXUNITS];
+    __shared__ float red[2 * NW];
+    __shared__ att_lds att[2];
+    __shared__ float cw[G2_STEP_MAXCH];
+    __shared__ float amv[NT];
+    __shared__ int ami[NT];
+    __shared__ volatile int dead;
+    __shared__ volatile int flag;
+
+    constexpr int NPE = (G2_STEP_MAXE + NT - 1) / NT;              /* words of an E vector */
+    constexpr int NPM = (G2_STEP_MAXCH * 66 + NT - 1) / NT;        /* a head's partials    */
+    const int wg = blockIdx.x, nwg = gridDim.x;
+    const int E = a.E, F = a.F, NH = a.NH, S = a.S, V = a.V;
+    const int pos = clampi(a.state[G2S_POS], 0, S - 1);
+    const int tok = clampi(a.state[G2S_TOK], 0, V - 1);
+    const int ngen = a.state[G2S_NGEN], min_new = a.state[G2S_MIN_NEW];
+    const unsigned seq = (unsigned)a.state[G2S_SEQ];
+    ctx c;
+    c.tag = seq + 1u;
+    c.abort_w = a.xbuf;
+    c.state = a.state;
+    c.dead = (lds_flag *)&dead;
+    const int T = pos + 1, nch = (T + 63) >> 6;
+    u64 *X = a.xbuf + G2X_HEAD;
+    att_regs ar[1];
+
+    /* register sets: wa carries qkv -> fc -> fc2 -> next qkv (each loaded as
+     * soon as the previous matrix is consumed), wp the proj rows */
+    u32x4 wa[UMAX][4], wp[UPROJ][4];
+    {
+        const G2_CONST g2_step_layer *LT0 = (const G2_CONST g2_step_layer *)a.layers;
+        const int tid = fresh_tid();
+        if (tid == 0) dead = 0;
+        load_set<UMAX>(tid, wa, make_plan<WT>(LT0->qkv_w, 3 * E, E), 0);
+        load_set<UPROJ>(tid, wp, make_plan<WT>(LT0->proj_w, E, E), 0);
+        /* embedding of the token at its position (embed, math.cl:333-350) */
+        for (int d = tid; d < E; d += NT)
+            xres[d] = ldw((const WT *)a.wte, (size_t)tok * E + d) + ldw((const WT *)a.wpe, (size_t)pos * E + d);
+        __syncthreads();
+    }
+
+    const G2_CONST g2_step_layer *LT = (const G2_CONST g2_step_layer *)a.layers;
+    for (int l = 0; l < a.L; ++l) {
+        const g2_step_layer y = LT[l];
+        u64 *R = X + (size_t)l * a.xlayer;
+
+        /* ---- QKV: LayerNorm(x) . Wqkv + b -> q, k, v (+ KV cache) */
+        {
+            const int tid = fresh_tid();
+            TRACE(0);
+            const plan p = make_plan<WT>(y.qkv_w, 3 * E, E);
+            const ln_params<NPE> lp = ln_load<NPE>(tid, gl(y.ln1_w), gl(y.ln1_b), E);
+            const float bias = tid < p.nrows && y.qkv_b ? gl(y.qkv_b)[p.r0 + tid] : 0.f;
+            if (l > 0) {
+                fetch<NPE>(tid, c, X + (size_t)(l - 1) * a.xlayer + G2X_X2(E, NH, F), E, nwg, xres, (lds_flag *)&flag);
+            }
+            TRACE(1);
+            layernorm(tid, xres, xin, lp, E, red);
+            TRACE(11);
+            matvec<WT, UMAX>(tid, wa, p, xin, part);
+            TRACE(12);
+            if (tid < p.nrows) {
+                const int r = p.r0 + tid;
+                float v = row_sum(p, part, tid);
+                v += bias;
+                ll_put(R + r, v, c.tag);
+                if (r >= 2 * E) glw(y.v_cache)[(size_t)pos * E + (r - 2 * E)] = v;
+                else if (r >= E) glw(y.k_cache)[(size_t)(r - E) * S + pos] = v;
+            }
+            TRACE(2);
+        }
+
+        /* ---- ATTN: unit u = h * nch + chunk, work-group u % nwg, half */
+        {
+            const int tid = fresh_tid();
+            const int nunits = NH * nch;
+            const int rounds = (nunits + 2 * nwg - 1) / (2 * nwg);
+            const int hf = tid >> 8;
+            for (int rd = 0; rd < rounds; ++rd) {
+                const int u = wg + nwg * (2 * rd + hf);
+                const bool on = u < nunits;
+                const int h = on ? u / nch : 0, ch = on ? u % nch : 0;
+                attn_load(tid, y, ar[0], on, h, ch, pos, T, E, S);
+                attn_chunk(tid, c, a, R, att[hf], ar[0], on, h, ch, pos, T);
+                __syncthreads();
+            }
+            TRACE(3);
+            /* the fc rows stream from here on; a work-group that merges a head
+             * issues them after its merge, so its merge waits behind nothing */
+            if (wg >= NH) load_set<UMAX>(tid, wa, make_plan<WT>(y.fc_w, F, E), 0);
+        }
+
+        /* ---- MERGE: head h by work-group h (g2k_attn_merge) */
+        for (int h = wg; h < NH; h += nwg) {
+            const int tid = fresh_tid();
+            const u64 *hp = R + G2X_ATT(E) + (size_t)h * G2_STEP_MAXCH * 66;
+            fetch<NPM>(tid, c, hp, nch * 66, nch, xin, (lds_flag *)&flag);
+            float Ls = 0.f;
+            if (tid < 64) {
+                const float mc = tid < nch ? xin[tid * 66] : -INFINITY;
+                const float lc = tid < nch ? xin[tid * 66 + 1] : 0.f;
+                const float M = wmax(mc);
+                const float w = tid < nch ? expf(mc - M) : 0.f;
+                Ls = wsum(lc * w);
+                if (tid < nch) cw[tid] = w;
+            }
+            __syncthreads();
+            if (tid < 64) {
+                float acc = 0.f;
+                for (int ch = 0; ch < nch; ++ch) acc = fmaf(xin[ch * 66 + 2 + tid], cw[ch], acc);
+                ll_put(R + G2X_O(E, NH) + h * 64 + tid, acc / Ls, c.tag);
+            }
+            __syncthreads();
+        }
+        {
+            const int tid = fresh_tid();
+            if (wg < NH) load_set<UMAX>(tid, wa, make_plan<WT>(y.fc_w, F, E), 0);
+            TRACE(4);
+        }
+
+        /* ---- PROJ: X1 = x + (O . Wp + b) */
+        {
+            const int tid = fresh_tid();
+            const plan p = make_plan<WT>(y.proj_w, E, E);
+            const float bias = tid < p.nrows && y.proj_b ? gl(y.proj_b)[p.r0 + tid] : 0.f;
+            fetch<NPE>(tid, c, R + G2X_O(E, NH), E, NH, xin, (lds_flag *)&flag);
+            TRACE(5);
+            matvec<WT, UPROJ>(tid, wp, p, xin, part);
+            if (tid < p.nrows) {
+                const int r = p.r0 + tid;
+                float v = row_sum(p, part, tid);
+                v += bias;
+                ll_put(R + G2X_X1(E, NH) + r, v + xres[r], c.tag);
+            }
+            TRACE(6);
+            if (l + 1 < a.L) load_set<UPROJ>(tid, wp, make_plan<WT>(LT[l + 1].proj_w, E, E), 0);
+            __syncthreads();
+        }
+
+        /* ---- FC: H = gelu(LayerNorm(X1) . Wfc + b) */
+        {
+            const int tid = fresh_tid();
+            const plan p = make_plan<WT>(y.fc_w, F, E);
+            const ln_params<NPE> lp = ln_load<NPE>(tid, gl(y.ln2_w), gl(y.ln2_b), E);
+            const float bias = tid < p.nrows && y.fc_b ? gl(y.fc_b)[p.r0 + tid] : 0.f;
+            fetch<NPE>(tid, c, R + G2X_X1(E, NH), E, nwg, xres, (lds_flag *)&flag);
+            TRACE(7);
+            layernorm(tid, xres, xin, lp, E, red);
+            TRACE(13);
+            matvec<WT, UMAX>(tid, wa, p, xin, part);
+            TRACE(14);
+            if (tid < p.nrows) {
+                const int r = p.r0 + tid;
+                float v = row_sum(p, part, tid);
+                v += bias;
+                ll_put(R + G2X_H(E, NH) + r, gelu_f(v), c.tag);
+            }
+            TRACE(8);
+            load_set<UMAX>(tid, wa, make_plan<WT>(y.fc2_w, E, F), 0);
+            __syncthreads();
+        }
+
+        /* ---- FC2: X2 = X1 + (H . Wfc2 + b) */
+        {
+            const int tid = fresh_tid();
+            const plan p = make_plan<WT>(y.fc2_w, E, F);
+            const float bias = tid < p.nrows && y.fc2_b ? gl(y.fc2_b)[p.r0 + tid] : 0.f;
+            fetch<PMAX>(tid, c, R + G2X_H(E, NH), F, nwg, xin, (lds_flag *)&flag);
+            TRACE(9);
+            matvec<WT, UMAX>(tid, wa, p, xin, part);
+            TRACE(15);
+            if (tid < p.nrows) {
+                const int r = p.r0 + tid;
+                float v = row_sum(p, part, tid);
+                v += bias;
+                ll_put(R + G2X_X2(E, NH, F) + r, v + xres[r], c.tag);
+            }
+            TRACE(10);
+            if (l + 1 < a.L) load_set<UMAX>(tid, wa, make_plan<WT>(LT[l + 1].qkv_w, 3 * E, E), 0);
+            else load_set<UMAX>(tid, wa, make_plan<WT>(a.lm_w, V, E), 0);
+            __syncthreads();
+        }
+    }
+
+    /* ---- LM: logits over the head rows, work-group first-max */
+    const int tid = fresh_tid();
+    const int l = a.L;
+    const ln_params<NPE> lpf = ln_load<NPE>(tid, gl(a.lnf_w), gl(a.lnf_b), E);
+    fetch<NPE>(tid, c, X + (size_t)(a.L - 1) * a.xlayer + G2X_X2(E, NH, F), E, nwg, xres, (lds_flag *)&flag);
+    TRACE(0);
+    layernorm(tid, xres, xin, lpf, E, red);
+    const plan p = make_plan<WT>(a.lm_w, V, E);
+    matvec<WT, UMAX>(tid, wa, p, xin, part);
+    const int masked = ngen < min_new ? G2_EOS_ID : -1;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    if (tid < p.nrows) {
+        const int r = p.r0 + tid;
+        const float v = row_sum(p, part, tid);
+        glw(a.logits)[r] = v;
+        bv = r == masked ? -1e30f : v;
+        bi = r;
+    }
+    blk_argmax(tid, bv, bi, amv, ami);
+    u64 *AM = X + (size_t)a.L * a.xlayer;
+    if (tid == 0) {
+        ll_put(AM + 2 * wg, amv[0], c.tag);
+        ll_put(AM + 2 * wg + 1, __int_as_float(ami[0]), c.tag);
+    }
+    TRACE(1);
+    if (wg != 0) return;
+
+    /* ---- greedy pick (g2k_argmax_merge with advance) */
+    __syncthreads();
+    fetch<2>(tid, c, AM, 2 * nwg, nwg, xin, (lds_flag *)&flag);
+    bv = -INFINITY;
+    bi = 0x7fffffff;
+    for (int b = tid; b < nwg; b += NT) {
+        const float v = xin[2 * b];
+        const int i = __float_as_int(xin[2 * b + 1]);
+        if (am_better2(v, i, bv, bi)) { bv = v; bi = i; }
+    }
+    blk_argmax(tid, bv, bi, amv, ami);
+    if (tid == 0) {
+        const int tk = (ami[0] >= 0 && ami[0] < V) ? ami[0] : 0;
+        const int ng = clampi(ngen, 0, G2S_WORDS - G2S_IDS - 1);
+        a.state[G2S_IDS + ng] = tk;
+        a.state[G2S_TOK] = tk;
+        a.state[G2S_NGEN] = ng + 1;
+        a.state[G2S_POS] = pos + 1;
+        a.state[G2S_SEQ] = (int)(seq + 1u);
+    }
+    TRACE(2);
+}
+
+} /* namespace g2step */
+
+extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f32(const g2_step_args a)
+{
+    g2step::step_impl<float>(a);
+}
+extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f16(const g2_step_args a)
+{
+    g2step::step_impl<_Float16>(a);
+}

@@ -98,7 +98,7 @@ for _n, _a in {
     "g2_model_synth": [C.POINTER(Config), C.c_uint64, _i, _i, C.POINTER(_vp)],
     "g2_model_from_host": [C.POINTER(Config), _vp, _vp, _vp, _vp, C.POINTER(_vp), _i, _i, C.POINTER(_vp)],
     "g2_model_free": [_vp], "g2_model_config": [_vp, C.POINTER(Config)],
-    "g2_model_set_kslice": [_vp, _i],
+    "g2_model_set_kslice": [_vp, _i], "g2_model_set_step": [_vp, _i], "g2_model_uses_step": [_vp],
     "g2_prefill": [_vp, _vp, _i], "g2_decode": [_vp, _i, _i], "g2_read_logits": [_vp, _vp, _i],
     "g2_sample_greedy": [_vp, _vp, _i, _i, _f],
     "g2_generate": [_vp, _vp, _i, _i, _i, _vp, C.POINTER(C.c_double)],
@@ -385,6 +385,13 @@ class Model:
 
     def uses_graph(self):
         return _lib.g2_model_uses_graph(self.h)
+
+    def set_step(self, on):
+        """Decode with the persistent step kernel (True) or per-operator kernels."""
+        check(_lib.g2_model_set_step(self.h, 1 if on else 0))
+
+    def uses_step(self):
+        return _lib.g2_model_uses_step(self.h) == 1
 
     def prefill(self, ids):
         ids = np.ascontiguousarray(ids, dtype=np.int32)

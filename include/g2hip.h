@@ -206,6 +206,16 @@ size_t g2_model_weight_bytes(const g2_model *m);
  * kernels are launched one by one (capture unavailable, or the environment
  * sets G2_NO_GRAPH=1, e.g. under a profiler), -1 before the first step. */
 int g2_model_uses_graph(const g2_model *m);
+/* Fused path decode engine.  By default (when the device supports
+ * cooperative launch and the model fits the kernel: n_embd <= 1600, ffn <=
+ * 6400) every decode forward is ONE launch of a persistent kernel that runs
+ * all layers, the lm_head and the greedy pick; the environment variable
+ * G2_STEP=0 or g2_model_set_step(m, 0) selects the per-operator kernels
+ * instead.  Replaces the reference's per-op enqueue loop of decode()
+ * (main.c:1792-1833) with no counterpart there.  set_step returns G2_E_ARG
+ * if on=1 and the model cannot use the kernel; uses_step returns 1 or 0. */
+int g2_model_set_step(g2_model *m, int on);
+int g2_model_uses_step(const g2_model *m);
 
 /* prefill, main.c:1739-1790: ids[0..n) at positions 0..n-1, 1 <= n <= 1023;
  * leaves the last row's logits on the device. */

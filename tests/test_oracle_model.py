@@ -9,20 +9,29 @@ first-max greedy semantics and the EOS mask.
 """
 import numpy as np
 import pytest
-import torch
 
 import g2hip
 from oracle import oracle
 from parity import random_prompt
 
-transformers = pytest.importorskip("transformers")
 
 NAMES = ["ln_1.weight", "ln_1.bias", "attn.c_attn.weight", "attn.c_attn.bias", "attn.c_proj.weight",
          "attn.c_proj.bias", "ln_2.weight", "ln_2.bias", "mlp.c_fc.weight", "mlp.c_fc.bias",
          "mlp.c_proj.weight", "mlp.c_proj.bias"]
 
 
+
+def _torch():
+    """torch, imported only inside the CPU tests that use it: a GPU test
+    session then never loads torch's bundled HIP runtime beside the one
+    libg2hip is linked against (two HIP runtimes in one process)."""
+    import torch
+
+    return torch
+
 def hf_model(cfg, w):
+    transformers = pytest.importorskip("transformers")
+    torch = _torch()
     hc = transformers.GPT2Config(vocab_size=cfg.vocab_size, n_positions=1024, n_embd=cfg.n_embd,
                                  n_layer=cfg.n_layer, n_head=cfg.n_head, n_inner=cfg.ffn_dim,
                                  activation_function="gelu_new", resid_pdrop=0.0, embd_pdrop=0.0,
@@ -52,6 +61,7 @@ def eos_dominant(w, E):
 
 
 def hf_logits(m, ids):
+    torch = _torch()
     with torch.no_grad():
         return m(torch.tensor(np.asarray(ids, np.int64)[None])).logits[0].numpy()
 

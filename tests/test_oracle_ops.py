@@ -15,11 +15,19 @@ import math
 
 import numpy as np
 import pytest
-import torch
 
 from oracle import oracle
 from parity import EPS32, assert_close_bound, dot_bound
 
+
+
+def _torch():
+    """torch, imported only inside the CPU tests that use it: a GPU test
+    session then never loads torch's bundled HIP runtime beside the one
+    libg2hip is linked against (two HIP runtimes in one process)."""
+    import torch
+
+    return torch
 
 def rnd(shape, seed):
     return np.random.default_rng(seed).standard_normal(shape).astype(np.float32)
@@ -36,6 +44,7 @@ def fma32(a, b, c):
 
 
 def gelu64(x):
+    torch = _torch()
     x = torch.tensor(np.asarray(x, np.float64))
     return torch.nn.functional.gelu(x, approximate="tanh").numpy()
 
@@ -155,6 +164,7 @@ def test_splitk_slice_is_strided_not_contiguous():
 
 @pytest.mark.parametrize("E,rows", [(768, 3), (1600, 1), (7, 2)])
 def test_layernorm_vs_torch(E, rows):
+    torch = _torch()
     x = rnd((rows, E), 24) * 2 + 0.3
     g, b = rnd(E, 25), rnd(E, 26)
     got = oracle.layernorm(x, g, b, E, rows)
@@ -209,6 +219,7 @@ def test_split_kv_layout():
 
 @pytest.mark.parametrize("T", [1, 5, 64, 300, 1024])
 def test_attention_chain_vs_float64(T):
+    torch = _torch()
     NH, DH, S = 3, 64, 1024
     D = NH * DH
     qkv, kc, vc = rnd(3 * D, 34), rnd(D * S, 35), rnd(S * D, 36)

@@ -1,0 +1,121 @@
+"""GPU parity of the persistent decode-step kernel (one cooperative launch
+per token running every layer, the lm_head and the greedy pick).
+
+The fused path decodes with it by default; these tests pin it against the
+CPU oracle (greedy ids, teacher-forced per-step logits within 2e-3 fp32 /
+5e-2 fp16-weight, as for the other paths), against the per-operator decode
+kernels of the same model, at GPT-2 XL width (n_embd 1600, 25 heads, ffn
+6400, vocab 50257) up to the last cache position, and for run-to-run
+determinism (every reduction has a fixed order).
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle
+from parity import greedy_agree, random_prompt
+
+pytestmark = pytest.mark.gpu
+
+SEED = 0x67707432
+
+
+def _check(got, ref, f16):
+    tol = 5e-2 if f16 else 2e-3
+    np.testing.assert_allclose(got, ref, rtol=tol if f16 else 1e-3, atol=tol)
+
+
+def test_step_kernel_is_default(g2):
+    for cfg in (g2.make_config(2, 128, 2, vocab_size=256), g2.preset("small")):
+        m = g2.Model.synth(cfg, SEED, g2.F16, g2.PATH_FUSED)
+        if not m.uses_step():
+            m.set_step(True)  # raises with the reason
+        assert m.uses_step(), f"E{cfg.n_embd}: the fused path should decode with the step kernel"
+        m.free()
+    m = g2.Model.synth(g2.make_config(2, 128, 2, vocab_size=256), SEED, g2.F32, g2.PATH_REFERENCE)
+    assert not m.uses_step()
+    with pytest.raises(g2.G2Error):
+        m.set_step(True)
+    m.free()
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_step_matches_operator_kernels(g2, dtype):
+    """Same model, same prompt: the step kernel and the per-operator decode
+    kernels give the same greedy ids and logits within the parity bound."""
+    cfg = g2.preset("small")
+    dt = g2.F16 if dtype == "f16" else g2.F32
+    m = g2.Model.synth(cfg, SEED, dt, g2.PATH_FUSED)
+    prompt = random_prompt(48, cfg.vocab_size, 11)
+    print(f"[step] small {dtype}: step kernel vs operator kernels", flush=True)
+    m.set_step(True)
+    ids_s, _ = m.generate(prompt, 20)
+    lg_s = m.logits()
+    m.set_step(False)
+    ids_k, _ = m.generate(prompt, 20)
+    lg_k = m.logits()
+    n = min(len(ids_s), len(ids_k))
+    agree = int(np.argmax(ids_s[:n] != ids_k[:n])) if (ids_s[:n] != ids_k[:n]).any() else n
+    if agree == n:
+        _check(lg_s, lg_k, dtype == "f16")
+    # the two may part only where the oracle sees a near tie
+    w = g2.synth_weights(cfg, SEED, f16_round=dtype == "f16")
+    om = oracle.Model(cfg, w)
+    ref_ids, top2, _ = om.generate(prompt, 20)
+    om.close()
+    tie = 1e-2 if dtype == "f16" else 1e-4
+    greedy_agree(ids_s, ref_ids, top2, tie)
+    greedy_agree(ids_k, ref_ids, top2, tie)
+    m.free()
+
+
+def test_step_xl_width_to_end_of_context(g2):
+    """Two layers at GPT-2 XL width (n_embd 1600, 25 heads, ffn 6400, vocab
+    50257, fp16 weights): teacher-forced decode logits at positions
+    1000..1022 (16 key chunks per head) against the oracle."""
+    cfg = g2.make_config(2, 1600, 25, vocab_size=50257)
+    assert cfg.ffn_dim == 6400
+    w = g2.synth_weights(cfg, SEED, f16_round=True)
+    om = oracle.Model(cfg, w, kslice=4)
+    m = g2.Model.from_host(cfg, w, g2.F16, g2.PATH_FUSED)
+    assert m.uses_step()
+    P = 1000
+    prompt = random_prompt(P, cfg.vocab_size, 77)
+    print(f"[step] XL width L2, prompt {P}", flush=True)
+    om.prefill(prompt)
+    m.prefill(prompt)
+    _check(m.logits(), om.logits(), True)
+    tok = om.greedy(prompt, False, 1.0)
+    for k in range(1023 - P):
+        pos = P + k
+        om.decode(tok, pos)
+        m.decode(tok, pos)
+        _check(m.logits(), om.logits(), True)
+        tok = om.greedy([tok], False, 1.0)
+    m.free()
+    om.close()
+
+
+def test_step_deterministic(g2):
+    """Two identical runs produce bit-identical ids and logits."""
+    cfg = g2.preset("small")
+    m = g2.Model.synth(cfg, SEED, g2.F16, g2.PATH_FUSED)
+    prompt = random_prompt(100, cfg.vocab_size, 5)
+    outs = []
+    for _ in range(2):
+        ids, _ = m.generate(prompt, 64)
+        outs.append((ids.copy(), m.logits().copy()))
+    np.testing.assert_array_equal(outs[0][0], outs[1][0])
+    np.testing.assert_array_equal(outs[0][1], outs[1][1])
+    m.free()
+
+
+def test_step_decode_run_matches_generate(g2):
+    """decode_run (the bench's loop) continues a prefilled cache exactly as
+    generate does."""
+    cfg = g2.make_config(3, 256, 4, vocab_size=1000)
+    m = g2.Model.synth(cfg, SEED, g2.F16, g2.PATH_FUSED)
+    prompt = random_prompt(200, cfg.vocab_size, 8)
+    ids, _ = m.generate(prompt, 40, min_new=40)
+    run, _ = m.decode_run(int(ids[0]), len(prompt), 39)
+    np.testing.assert_array_equal(run, ids[1:40])
+    m.free()
