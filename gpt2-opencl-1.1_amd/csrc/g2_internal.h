@@ -52,7 +52,9 @@
     X(GEMM_NK_F32_QKV, "g2k_gemm_nk_f32_qkv")                                 \
     X(GEMM_NK_F16_QKV, "g2k_gemm_nk_f16_qkv")                                 \
     X(ATTN_PREFILL, "g2k_attn_prefill")                                       \
-    X(STEP_F32, "g2k_step_f32") X(STEP_F16, "g2k_step_f16")
+    X(STEP_F32, "g2k_step_f32") X(STEP_F16, "g2k_step_f16")                   \
+    X(STEPX_F32, "g2k_stepx_f32") X(STEPX_F16, "g2k_stepx_f16")               \
+    X(XCC_PROBE, "g2k_xcc_probe")
 
 #define G2_ENUM_ENTRY(id, name) G2F_##id,
 enum { G2_KERNEL_LIST(G2_ENUM_ENTRY) G2F_COUNT };
@@ -78,6 +80,9 @@ int g2i_launch(int fid, unsigned gx, unsigned gy, unsigned bx, void *args);
 int g2i_coop_launch(int fid, unsigned gx, unsigned bx, void *args);
 /* Work-groups of the persistent step kernel's grid (0: not supported). */
 int g2i_step_wgs(void);
+/* 1 if the XCD-parallel step kernel may run: its occupancy fits and a probe
+ * launch found work-group w on XCD w % G2_NXCD for every w of the grid. */
+int g2i_stepx_ok(void);
 int g2i_device_alloc(void **p, size_t bytes);
 /* Launch a packed-matvec kernel: fid_f32_64 is the epilogue's first table
  * entry (f32, 64-lane shape); the lane shape and grid follow from K. */

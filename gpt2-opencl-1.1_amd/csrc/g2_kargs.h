@@ -193,15 +193,15 @@ typedef struct {
     int *state;
     unsigned long long *xbuf;
     /* optional phase timestamps (100 MHz clock): work-group w writes
-     * trace[w * G2_TRACE_STRIDE(L) + 16*l + k] for phase boundary k of layer
-     * l, and 16*L + k for the lm_head and the pick; NULL: off */
+     * trace[w * G2_TRACE_STRIDE(L) + 24*l + k] for phase boundary k of layer
+     * l, and 24*L + k for the lm_head and the pick; NULL: off */
     unsigned long long *trace;
     int L, E, F, NH, V, S;
     int xlayer; /* words per layer region */
     float scale;
 } g2_step_args;
 
-#define G2_TRACE_STRIDE(L) (16 * (L) + 4)
+#define G2_TRACE_STRIDE(L) (24 * (L) + 8)
 
 #define G2_STEP_THREADS 512
 #define G2_STEP_MAXE 1600   /* largest n_embd the step kernel holds in LDS */
@@ -223,6 +223,28 @@ typedef struct {
 /* Total words: header, L layer regions, 2 argmax words per work-group. */
 #define G2X_TOTAL_WORDS(L, E, NH, F, nwg) \
     ((long)G2X_HEAD + (long)(L) * G2X_LAYER_WORDS(E, NH, F) + 2L * (nwg) + 32)
+
+/* XCD-parallel decode step (same arguments as g2_step_args; layout below).
+ * A work-group reads its XCD from the hardware; its rank within the XCD is
+ * w / G2_NXCD (distinct under the dispatcher's round-robin).  XCD x
+ * owns heads [NH*x/8, NH*(x+1)/8) and ffn rows [F*x/8, F*(x+1)/8); proj and
+ * fc2 are computed as per-XCD partial products over those K-slices and
+ * summed across XCDs.  Hand-offs inside an XCD go through its L2; only the
+ * two partial sums per layer cross XCDs.
+ * Exchange words per layer: G2_NXCD local regions of G2XL_WORDS each
+ * (qkv of the XCD's heads, attention partials, merged o, X1, H slice, X2),
+ * then two global regions of G2_NXCD*E partial sums (proj, fc2). */
+#define G2_NXCD 8
+#define G2XL_QKV 0
+#define G2XL_ATT(HX) (192 * (HX))
+#define G2XL_O(HX) (G2XL_ATT(HX) + (HX) * G2_STEP_MAXCH * 66)
+#define G2XL_X1(HX) (G2XL_O(HX) + 64 * (HX))
+#define G2XL_H(HX, E) (G2XL_X1(HX) + (E))
+#define G2XL_X2(HX, E, FX) (G2XL_H(HX, E) + (FX))
+#define G2XL_WORDS(HX, E, FX) ((G2XL_X2(HX, E, FX) + (E) + 63) & ~63)
+#define G2XX_LAYER_WORDS(HX, E, FX) (G2_NXCD * G2XL_WORDS(HX, E, FX) + 2 * G2_NXCD * (E))
+#define G2XX_TOTAL_WORDS(L, HX, E, FX, nwg) \
+    ((long)G2X_HEAD + (long)(L) * G2XX_LAYER_WORDS(HX, E, FX) + 2L * (nwg) + 32)
 
 /* Causal attention over a prompt block: rows i < P of q[P,E]; keys/values
  * j <= i from the transposed K cache and the V cache; head dim 64. */

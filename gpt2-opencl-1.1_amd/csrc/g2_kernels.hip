@@ -558,3 +558,4 @@ G2K void g2k_attn_prefill(const g2_attnp_args a)
 
 /* The persistent decode step (one cooperative launch per token). */
 #include "g2_step.hip"
+#include "g2_stepx.hip"

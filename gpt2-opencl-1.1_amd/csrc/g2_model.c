@@ -55,6 +55,7 @@ struct g2_model {
     size_t xbuf_bytes;
     int step_wgs;  /* grid of the step kernel, 0 if this model cannot use it */
     int step_on;   /* decode steps run the step kernel */
+    int stepx;     /* ... in its XCD-parallel form */
     int step_ran;  /* a step kernel ran since the last error check */
     const char *step_why; /* why the step kernel cannot run this model */
     unsigned long long *trace; /* phase timestamps, when G2_STEP_TRACE names a file */
@@ -191,6 +192,38 @@ static int step_supported(const g2_model *m, int nwg, const char **why)
     return 1;
 }
 
+static int step_nseg(int C)
+{
+    const int cpl = C <= 64 ? 1 : (C <= 128 ? 2 : 4);
+    const int need = (C + 64 * cpl - 1) / (64 * cpl);
+    return need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : (need <= 8 ? 8 : 1 << 20)));
+}
+
+/* Whether the XCD-parallel step kernel can run this model on a grid of nwg
+ * work-groups (G2_NXCD XCDs of nwg/G2_NXCD): the ffn slice of an XCD must
+ * start on a 16-byte chunk, every work-group's share of every matrix must
+ * fit its units and threads, and the reduce-scatter of E rows over the
+ * ranks of an XCD must fit one read per thread. */
+static int stepx_supported(const g2_model *m, int nwg)
+{
+    const g2_config *c = &m->cfg;
+    const int ve = m->dtype == G2_F16 ? 8 : 4;
+    const int E = c->n_embd, F = c->ffn_dim, V = c->vocab_size, NH = c->n_head;
+    if (nwg <= 0 || nwg % G2_NXCD) return 0;
+    const int G = nwg / G2_NXCD;
+    const int HX = (NH + G2_NXCD - 1) / G2_NXCD, FX = (F + G2_NXCD - 1) / G2_NXCD;
+    if (F % G2_NXCD || (F / G2_NXCD) % ve) return 0;
+    if (G2_NXCD * ((E + G - 1) / G) > G2_STEP_THREADS) return 0;
+    const int rows[5] = { (192 * HX + G - 1) / G, (FX + G - 1) / G, (E + G - 1) / G, (E + G - 1) / G,
+                          (V + nwg - 1) / nwg };
+    const int chunks[5] = { E / ve, E / ve, 64 * HX / ve, FX / ve, E / ve };
+    for (int i = 0; i < 5; ++i) {
+        if (rows[i] > G2_STEP_THREADS) return 0;
+        if ((long)rows[i] * step_nseg(chunks[i]) > G2_STEP_MAXUNITS) return 0;
+    }
+    return 1;
+}
+
 /* Device tables of the step kernel (after the weights are uploaded). */
 static int step_setup(g2_model *m)
 {
@@ -210,7 +243,12 @@ static int step_setup(g2_model *m)
     int rc = dev_alloc(m, (void **)&m->step_layers, (size_t)L * sizeof *t, 0);
     if (!rc) rc = up(m->step_layers, t, (size_t)L * sizeof *t);
     free(t);
-    m->xbuf_bytes = (size_t)G2X_TOTAL_WORDS(L, c->n_embd, c->n_head, c->ffn_dim, nwg) * 8;
+    const char *envx = getenv("G2_STEPX");
+    m->stepx = envx && envx[0] == '1' && g2i_stepx_ok() && stepx_supported(m, nwg);
+    const long w1 = G2X_TOTAL_WORDS(L, c->n_embd, c->n_head, c->ffn_dim, nwg);
+    const int HX = (c->n_head + G2_NXCD - 1) / G2_NXCD, FX = (c->ffn_dim + G2_NXCD - 1) / G2_NXCD;
+    const long w2 = G2XX_TOTAL_WORDS(L, HX, c->n_embd, FX, nwg);
+    m->xbuf_bytes = (size_t)(w1 > w2 ? w1 : w2) * 8;
     if (!rc) rc = dev_alloc(m, (void **)&m->xbuf, m->xbuf_bytes, 0);
     if (!rc) rc = g2i_hip(hipMemsetAsync(m->xbuf, 0, m->xbuf_bytes, g2i_stream()), "exchange clear");
     if (rc) return rc;
@@ -572,7 +610,7 @@ int g2_model_set_step(g2_model *m, int on)
 int g2_model_uses_step(const g2_model *m)
 {
     if (!m) return g2i_err(G2_E_ARG, "NULL model");
-    return m->step_on;
+    return m->step_on ? (m->stepx ? 2 : 1) : 0;
 }
 
 int g2_model_uses_graph(const g2_model *m)
@@ -730,9 +768,15 @@ static int step_launch(g2_model *m)
     a.trace = m->trace;
     a.L = c->n_layer; a.E = c->n_embd; a.F = c->ffn_dim; a.NH = c->n_head; a.V = c->vocab_size;
     a.S = G2_KV_MAX_SEQ;
-    a.xlayer = G2X_LAYER_WORDS(c->n_embd, c->n_head, c->ffn_dim);
     a.scale = 1.0f / sqrtf(64.0f);
     m->step_ran = 1;
+    if (m->stepx) {
+        const int HX = (c->n_head + G2_NXCD - 1) / G2_NXCD, FX = (c->ffn_dim + G2_NXCD - 1) / G2_NXCD;
+        a.xlayer = G2XX_LAYER_WORDS(HX, c->n_embd, FX);
+        return g2i_coop_launch(m->dtype == G2_F16 ? G2F_STEPX_F16 : G2F_STEPX_F32, (unsigned)m->step_wgs,
+                               G2_STEP_THREADS, &a);
+    }
+    a.xlayer = G2X_LAYER_WORDS(c->n_embd, c->n_head, c->ffn_dim);
     return g2i_coop_launch(m->dtype == G2_F16 ? G2F_STEP_F16 : G2F_STEP_F32, (unsigned)m->step_wgs,
                            G2_STEP_THREADS, &a);
 }
@@ -756,6 +800,12 @@ static int step_check(g2_model *m, const int *state_words)
     rc = g2i_hip(hipMemsetAsync(m->xbuf, 0, m->xbuf_bytes, g2i_stream()), "exchange clear");
     if (!rc) rc = up(m->state + G2S_ERR, &zero, sizeof zero);
     if (rc) return rc;
+    if (m->stepx) {
+        m->stepx = 0; /* later steps use the all-to-all step kernel */
+        return g2i_err(G2_E_HIP, "XCD-parallel decode step kernel: a hand-off between work-groups timed out "
+                                 "(work-groups not where expected?); the step's outputs are invalid and later "
+                                 "steps use the all-to-all step kernel");
+    }
     return g2i_err(G2_E_HIP, "decode step kernel: a hand-off between work-groups timed out; "
                              "the step's outputs are invalid");
 }

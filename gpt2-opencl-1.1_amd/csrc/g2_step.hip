@@ -89,6 +89,21 @@ __device__ __forceinline__ u64 ll_get(const u64 *p)
 __device__ __forceinline__ unsigned ll_tag(u64 w) { return (unsigned)(w >> 32); }
 __device__ __forceinline__ float ll_val(u64 w) { return __uint_as_float((unsigned)w); }
 
+/* A word for readers on the same XCD only: a plain 64-bit store, which
+ * lands in this XCD's L2, where their agent-scope loads find it (readers on
+ * other XCDs would not see it before the kernel ends). */
+__device__ __forceinline__ void lx_put(u64 *p, float v, unsigned tag)
+{
+    __hip_atomic_store(p, ((u64)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+template <bool LOCAL>
+__device__ __forceinline__ void put(u64 *p, float v, unsigned tag)
+{
+    if constexpr (LOCAL) lx_put(p, v, tag);
+    else ll_put(p, v, tag);
+}
+
 /* Wave-wide sum / max through DPP lane moves (no LDS traffic): butterfly
  * within quads, rotations within 16-lane rows, then the four row results
  * combined in row order.  Every lane gets the result. */
@@ -398,7 +413,7 @@ struct att_lds {
  * j0+4pq..+3 and dims 4dg..+3 (four 16-byte loads of the transposed K
  * cache); weighted sum: thread (d4 = t%16, jg = t/16) takes dims 4d4..+3
  * and positions j0+4jg..+3 (four 16-byte loads of the V cache).  The
- * current position is not read from the cache. */
+ * current position's entries are replaced by the exchanged k and v. */
 struct att_regs {
     f32x4 kv[4], vv[4];
 };
@@ -410,42 +425,48 @@ __device__ __forceinline__ void attn_load(int tid, const g2_step_layer &y, att_r
     const int j0 = ch * 64;
     const int pq = t & 15, dg = t >> 4, jk = j0 + 4 * pq;
     const int d4 = t & 15, jg = t >> 4;
-    if (on && jk < T) {
-        const G2_GLOBAL f32x4 *kb = gl((const f32x4 *)(y.k_cache + (size_t)(h * 64 + 4 * dg) * S + jk));
+    /* unconditional: every address is inside the caches (positions < S =
+     * 1024, dims < E); values of positions >= T or of the current position
+     * are never used.  Skipping loads under a lane mask would make the
+     * compiler wait for all of the wave's earlier stores first. */
+    (void)on; (void)T; (void)pos;
+    const G2_GLOBAL f32x4 *kb = gl((const f32x4 *)(y.k_cache + (size_t)(h * 64 + 4 * dg) * S + jk));
 #pragma unroll
-        for (int d = 0; d < 4; ++d) r.kv[d] = kb[(size_t)d * (S / 4)];
-    }
+    for (int d = 0; d < 4; ++d) r.kv[d] = kb[(size_t)d * (S / 4)];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int j = j0 + 4 * jg + e;
-        if (on && j < T && j != pos) r.vv[e] = *gl((const f32x4 *)(y.v_cache + (size_t)j * E + h * 64 + 4 * d4));
+        r.vv[e] = *gl((const f32x4 *)(y.v_cache + (size_t)j * E + h * 64 + 4 * d4));
     }
 }
 
 /* One 64-position chunk c of single-query attention for head h by the 256
  * threads of one half of the work-group (t = thread in the half): the
  * computation of g2k_attn_part, with the current position's key and value
- * taken from the exchange.  `on` is false for a half without a unit; it
- * still takes part in the barriers. */
-__device__ __forceinline__ void attn_chunk(int tid, const ctx &c, const g2_step_args &a, const u64 *R,
-                                           att_lds &L, att_regs &r, bool on, int h, int ch, int pos,
-                                           int T)
+ * taken from the exchange; the chunk's (max, sum, o[64]) go to pout[0..65].
+ * `on` is false for a half without a unit; it still takes part in the
+ * barriers. */
+template <bool LOCAL>
+__device__ __forceinline__ void attn_chunk(int tid, const ctx &c, float scale, const u64 *src, int qo,
+                                           int ko, int vo, u64 *pout, att_lds &L, att_regs &r, bool on,
+                                           int ch, int pos, int T, u64 *trace_slot = nullptr)
 {
     const int t = tid & 255;
-    const int E = a.E;
     const int j0 = ch * 64;
     const int pq = t & 15, dg = t >> 4, jk = j0 + 4 * pq;
     const int d4 = t & 15, jg = t >> 4;
-    /* q, k and v of head h at this position */
+    /* q, k and v of the head at this position: src[qo + d], src[ko + d],
+     * src[vo + d] */
     if (on && t < 192) {
         const int part = t >> 6, d = t & 63;
-        const int w = part * E + h * 64 + d;
-        u64 v[1] = {ll_get(R + w)};
-        settle(c, R, v, [&](int) { return w; });
+        const int w = (part == 0 ? qo : (part == 1 ? ko : vo)) + d;
+        u64 v[1] = {ll_get(src + w)};
+        settle(c, src, v, [&](int) { return w; });
         float *dst = part == 0 ? L.q : (part == 1 ? L.kn : L.vn);
         dst[d] = ll_val(v[0]);
     }
     __syncthreads();
+    if (trace_slot && tid == 0) *trace_slot = wall_clock64();
     if (on) {
         float s[4] = {0.f, 0.f, 0.f, 0.f};
         if (jk < T) {
@@ -469,7 +490,7 @@ __device__ __forceinline__ void attn_chunk(int tid, const ctx &c, const g2_step_
         float s = 0.f;
 #pragma unroll
         for (int g = 0; g < 16; ++g) s += L.red[g][t];
-        s *= a.scale;
+        s *= scale;
         const float m = wmax(ok ? s : -INFINITY);
         const float p = ok ? expf(s - m) : 0.f;
         const float l = wsum(p);
@@ -500,11 +521,10 @@ __device__ __forceinline__ void attn_chunk(int tid, const ctx &c, const g2_step_
         float o = 0.f;
 #pragma unroll
         for (int g = 0; g < 16; ++g) o += L.red[g][t];
-        u64 *pp = (u64 *)R + G2X_ATT(E) + ((size_t)h * G2_STEP_MAXCH + ch) * 66;
-        ll_put(pp + 2 + t, o, c.tag);
+        put<LOCAL>(pout + 2 + t, o, c.tag);
         if (t == 0) {
-            ll_put(pp, L.stat[0], c.tag);
-            ll_put(pp + 1, L.stat[1], c.tag);
+            put<LOCAL>(pout, L.stat[0], c.tag);
+            put<LOCAL>(pout + 1, L.stat[1], c.tag);
         }
     }
 }
@@ -533,7 +553,7 @@ __device__ __forceinline__ void blk_argmax(int tid, float bv, int bi, float *amv
 #define TRACE(k)                                                                       \
     do {                                                                               \
         if (a.trace && tid == 0)                                                       \
-            a.trace[(size_t)wg * G2_TRACE_STRIDE(a.L) + 16 * l + (k)] = wall_clock64(); \
+            a.trace[(size_t)wg * G2_TRACE_STRIDE(a.L) + 24 * l + (k)] = wall_clock64(); \
     } while (0)
 
 /* The thread index as a value the compiler cannot prove loop-invariant:
@@ -636,7 +656,9 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 const bool on = u < nunits;
                 const int h = on ? u / nch : 0, ch = on ? u % nch : 0;
                 attn_load(tid, y, ar[0], on, h, ch, pos, T, E, S);
-                attn_chunk(tid, c, a, R, att[hf], ar[0], on, h, ch, pos, T);
+                attn_chunk<false>(tid, c, a.scale, R, h * 64, E + h * 64, 2 * E + h * 64,
+                                  R + G2X_ATT(E) + ((size_t)h * G2_STEP_MAXCH + ch) * 66, att[hf], ar[0],
+                                  on, ch, pos, T);
                 __syncthreads();
             }
             TRACE(3);

@@ -391,7 +391,11 @@ class Model:
         check(_lib.g2_model_set_step(self.h, 1 if on else 0))
 
     def uses_step(self):
-        return _lib.g2_model_uses_step(self.h) == 1
+        return _lib.g2_model_uses_step(self.h) >= 1
+
+    def step_kind(self):
+        """2: XCD-parallel step kernel, 1: all-to-all step kernel, 0: per-operator kernels."""
+        return _lib.g2_model_uses_step(self.h)
 
     def prefill(self, ids):
         ids = np.ascontiguousarray(ids, dtype=np.int32)

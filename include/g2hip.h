@@ -212,8 +212,12 @@ int g2_model_uses_graph(const g2_model *m);
  * all layers, the lm_head and the greedy pick; the environment variable
  * G2_STEP=0 or g2_model_set_step(m, 0) selects the per-operator kernels
  * instead.  Replaces the reference's per-op enqueue loop of decode()
- * (main.c:1792-1833) with no counterpart there.  set_step returns G2_E_ARG
- * if on=1 and the model cannot use the kernel; uses_step returns 1 or 0. */
+ * (main.c:1792-1833) with no counterpart there.  The default is the
+ * all-to-all form; G2_STEPX=1 selects the XCD-parallel form (each XCD owns
+ * heads and ffn rows) on a device whose work-groups are dealt to its 8 XCDs
+ * round-robin (checked at g2_init).  set_step returns G2_E_ARG if on=1 and
+ * the model cannot use the kernel; uses_step returns 2 (XCD-parallel step
+ * kernel), 1 (all-to-all step kernel) or 0 (per-operator kernels). */
 int g2_model_set_step(g2_model *m, int on);
 int g2_model_uses_step(const g2_model *m);
 

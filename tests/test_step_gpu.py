@@ -1,11 +1,14 @@
-"""GPU parity of the persistent decode-step kernel (one cooperative launch
-per token running every layer, the lm_head and the greedy pick).
+"""GPU parity of the persistent decode-step kernels (one cooperative launch
+per token running every layer, the lm_head and the greedy pick), in both
+forms: all-to-all (the default) and XCD-parallel (G2_STEPX=1: each XCD owns
+heads and ffn rows, where the device deals work-groups to XCDs
+round-robin).
 
-The fused path decodes with it by default; these tests pin it against the
-CPU oracle (greedy ids, teacher-forced per-step logits within 2e-3 fp32 /
-5e-2 fp16-weight, as for the other paths), against the per-operator decode
-kernels of the same model, at GPT-2 XL width (n_embd 1600, 25 heads, ffn
-6400, vocab 50257) up to the last cache position, and for run-to-run
+The fused path decodes with them by default; these tests pin them against
+the CPU oracle (greedy ids, teacher-forced per-step logits within 2e-3 fp32
+/ 5e-2 fp16-weight, as for the other paths), against the per-operator
+decode kernels of the same model, at GPT-2 XL width (n_embd 1600, 25 heads,
+ffn 6400, vocab 50257) up to the last cache position, and for run-to-run
 determinism (every reduction has a fixed order).
 """
 import numpy as np
@@ -17,6 +20,14 @@ from parity import greedy_agree, random_prompt
 pytestmark = pytest.mark.gpu
 
 SEED = 0x67707432
+KINDS = [pytest.param("0", id="all-to-all"), pytest.param("1", id="xcd")]
+
+
+@pytest.fixture
+def stepx(request, monkeypatch):
+    """Selects the step-kernel form for models created in the test."""
+    monkeypatch.setenv("G2_STEPX", request.param)
+    return request.param
 
 
 def _check(got, ref, f16):
@@ -25,11 +36,12 @@ def _check(got, ref, f16):
 
 
 def test_step_kernel_is_default(g2):
-    for cfg in (g2.make_config(2, 128, 2, vocab_size=256), g2.preset("small")):
+    for cfg in (g2.make_config(2, 128, 2, vocab_size=256), g2.preset("small"), g2.preset("xl")):
         m = g2.Model.synth(cfg, SEED, g2.F16, g2.PATH_FUSED)
         if not m.uses_step():
             m.set_step(True)  # raises with the reason
         assert m.uses_step(), f"E{cfg.n_embd}: the fused path should decode with the step kernel"
+        print(f"[step] E{cfg.n_embd}: step kernel form {m.step_kind()}", flush=True)
         m.free()
     m = g2.Model.synth(g2.make_config(2, 128, 2, vocab_size=256), SEED, g2.F32, g2.PATH_REFERENCE)
     assert not m.uses_step()
@@ -38,15 +50,16 @@ def test_step_kernel_is_default(g2):
     m.free()
 
 
+@pytest.mark.parametrize("stepx", KINDS, indirect=True)
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
-def test_step_matches_operator_kernels(g2, dtype):
+def test_step_matches_operator_kernels(g2, stepx, dtype):
     """Same model, same prompt: the step kernel and the per-operator decode
     kernels give the same greedy ids and logits within the parity bound."""
     cfg = g2.preset("small")
     dt = g2.F16 if dtype == "f16" else g2.F32
     m = g2.Model.synth(cfg, SEED, dt, g2.PATH_FUSED)
     prompt = random_prompt(48, cfg.vocab_size, 11)
-    print(f"[step] small {dtype}: step kernel vs operator kernels", flush=True)
+    print(f"[step] small {dtype} form {m.step_kind()}: step kernel vs operator kernels", flush=True)
     m.set_step(True)
     ids_s, _ = m.generate(prompt, 20)
     lg_s = m.logits()
@@ -68,7 +81,8 @@ def test_step_matches_operator_kernels(g2, dtype):
     m.free()
 
 
-def test_step_xl_width_to_end_of_context(g2):
+@pytest.mark.parametrize("stepx", KINDS, indirect=True)
+def test_step_xl_width_to_end_of_context(g2, stepx):
     """Two layers at GPT-2 XL width (n_embd 1600, 25 heads, ffn 6400, vocab
     50257, fp16 weights): teacher-forced decode logits at positions
     1000..1022 (16 key chunks per head) against the oracle."""
@@ -80,7 +94,7 @@ def test_step_xl_width_to_end_of_context(g2):
     assert m.uses_step()
     P = 1000
     prompt = random_prompt(P, cfg.vocab_size, 77)
-    print(f"[step] XL width L2, prompt {P}", flush=True)
+    print(f"[step] XL width L2 form {m.step_kind()}, prompt {P}", flush=True)
     om.prefill(prompt)
     m.prefill(prompt)
     _check(m.logits(), om.logits(), True)
@@ -95,7 +109,8 @@ def test_step_xl_width_to_end_of_context(g2):
     om.close()
 
 
-def test_step_deterministic(g2):
+@pytest.mark.parametrize("stepx", KINDS, indirect=True)
+def test_step_deterministic(g2, stepx):
     """Two identical runs produce bit-identical ids and logits."""
     cfg = g2.preset("small")
     m = g2.Model.synth(cfg, SEED, g2.F16, g2.PATH_FUSED)
@@ -109,7 +124,8 @@ def test_step_deterministic(g2):
     m.free()
 
 
-def test_step_decode_run_matches_generate(g2):
+@pytest.mark.parametrize("stepx", KINDS, indirect=True)
+def test_step_decode_run_matches_generate(g2, stepx):
     """decode_run (the bench's loop) continues a prefilled cache exactly as
     generate does."""
     cfg = g2.make_config(3, 256, 4, vocab_size=1000)
@@ -119,3 +135,29 @@ def test_step_decode_run_matches_generate(g2):
     run, _ = m.decode_run(int(ids[0]), len(prompt), 39)
     np.testing.assert_array_equal(run, ids[1:40])
     m.free()
+
+
+@pytest.mark.parametrize("cfg_args", [(2, 128, 2, 256), (3, 192, 3, 1000), (1, 64, 1, 50257)],
+                         ids=["tiny", "3-heads", "1-head"])
+def test_stepx_small_shapes(g2, monkeypatch, cfg_args):
+    """XCD-parallel kernel on shapes where some XCDs own no head (n_head < 8)
+    and ffn slices are a few chunks: greedy ids and logits vs the oracle."""
+    monkeypatch.setenv("G2_STEPX", "1")
+    L, E, H, V = cfg_args
+    cfg = g2.make_config(L, E, H, vocab_size=V)
+    for dtype in (g2.F32, g2.F16):
+        f16 = dtype == g2.F16
+        w = g2.synth_weights(cfg, SEED, f16_round=f16)
+        om = oracle.Model(cfg, w)
+        prompt = random_prompt(30, V, 4)
+        ref_ids, top2, ref_lg = om.generate(prompt, 12, logit_steps=4)
+        m = g2.Model.from_host(cfg, w, dtype, g2.PATH_FUSED)
+        print(f"[step] L{L} E{E} H{H} V{V} {'f16' if f16 else 'f32'} form {m.step_kind()}", flush=True)
+        ids, _ = m.generate(prompt, 12)
+        greedy_agree(ids, ref_ids, top2, 1e-2 if f16 else 1e-4)
+        m.prefill(prompt)
+        for k in range(3):
+            m.decode(ref_ids[k], 30 + k)
+            _check(m.logits(), ref_lg[k + 1], f16)
+        m.free()
+        om.close()
