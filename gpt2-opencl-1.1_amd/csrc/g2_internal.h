@@ -54,7 +54,8 @@
     X(ATTN_PREFILL, "g2k_attn_prefill")                                       \
     X(STEP_F32, "g2k_step_f32") X(STEP_F16, "g2k_step_f16")                   \
     X(STEPX_F32, "g2k_stepx_f32") X(STEPX_F16, "g2k_stepx_f16")               \
-    X(XCC_PROBE, "g2k_xcc_probe")
+    X(XCC_PROBE, "g2k_xcc_probe") X(STEP3_F16, "g2k_step3_f16")               \
+    X(TRANSPOSE16, "g2k_transpose16")
 
 #define G2_ENUM_ENTRY(id, name) G2F_##id,
 enum { G2_KERNEL_LIST(G2_ENUM_ENTRY) G2F_COUNT };
@@ -83,6 +84,7 @@ int g2i_step_wgs(void);
 /* 1 if the XCD-parallel step kernel may run: its occupancy fits and a probe
  * launch found work-group w on XCD w % G2_NXCD for every w of the grid. */
 int g2i_stepx_ok(void);
+int g2i_step3_ok(void);
 int g2i_device_alloc(void **p, size_t bytes);
 /* Launch a packed-matvec kernel: fid_f32_64 is the epilogue's first table
  * entry (f32, 64-lane shape); the lane shape and grid follow from K. */

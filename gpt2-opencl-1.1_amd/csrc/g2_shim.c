@@ -34,6 +34,7 @@ static struct {
     int ready, device, cus;
     int step_wgs; /* work-groups of a cooperative step launch (0: unsupported) */
     int stepx_ok; /* the XCD-parallel step kernel may run */
+    int step3_ok; /* the two-role step kernel may run */
     char name[256];
     hipModule_t module;
     hipStream_t stream;
@@ -83,6 +84,7 @@ int g2i_coop_launch(int fid, unsigned gx, unsigned bx, void *args)
 
 int g2i_step_wgs(void) { return G.step_wgs; }
 int g2i_stepx_ok(void) { return G.stepx_ok; }
+int g2i_step3_ok(void) { return G.step3_ok; }
 
 /* The XCD-parallel step kernel hands data between work-groups through the
  * L2 of their XCD and gives the work-groups of one XCD the ranks w / 8,
@@ -228,6 +230,10 @@ int g2_init(int device)
                     rtv, coop, (int)ea, nb[0], nb[1], (int)eo[0], (int)eo[1], fa.numRegs, fa.sharedSizeBytes,
                     fa.maxThreadsPerBlock);
         }
+        int nb3 = 0;
+        G.step3_ok = G.step_wgs && G.step_wgs <= G3_MAXWG &&
+                     hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb3, G.fn[G2F_STEP3_F16], G2_STEP_THREADS, 0) ==
+                         hipSuccess && nb3 >= 1;
         (void)hipGetLastError();
         G.stepx_ok = G.step_wgs ? xcd_mapping_holds(G.step_wgs) : 0;
         if (G.step_wgs && !G.stepx_ok)

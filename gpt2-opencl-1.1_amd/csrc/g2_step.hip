@@ -440,33 +440,20 @@ __device__ __forceinline__ void attn_load(int tid, const g2_step_layer &y, att_r
     }
 }
 
-/* One 64-position chunk c of single-query attention for head h by the 256
- * threads of one half of the work-group (t = thread in the half): the
- * computation of g2k_attn_part, with the current position's key and value
- * taken from the exchange; the chunk's (max, sum, o[64]) go to pout[0..65].
- * `on` is false for a half without a unit; it still takes part in the
- * barriers. */
+/* The attention of one 64-position chunk once L.q, L.kn and L.vn hold the
+ * head's q, k and v at this position (by the 256 threads of one half; t =
+ * thread in the half): the computation of g2k_attn_part, with the current
+ * position's key and value taken from L; the chunk's (max, sum, o[64]) go
+ * to pout[0..65].  `on` is false for a half without a unit; it still takes
+ * part in the three barriers. */
 template <bool LOCAL>
-__device__ __forceinline__ void attn_chunk(int tid, const ctx &c, float scale, const u64 *src, int qo,
-                                           int ko, int vo, u64 *pout, att_lds &L, att_regs &r, bool on,
-                                           int ch, int pos, int T, u64 *trace_slot = nullptr)
+__device__ __forceinline__ void attn_compute(int tid, const ctx &c, float scale, u64 *pout, att_lds &L,
+                                             const att_regs &r, bool on, int ch, int pos, int T)
 {
     const int t = tid & 255;
     const int j0 = ch * 64;
     const int pq = t & 15, dg = t >> 4, jk = j0 + 4 * pq;
     const int d4 = t & 15, jg = t >> 4;
-    /* q, k and v of the head at this position: src[qo + d], src[ko + d],
-     * src[vo + d] */
-    if (on && t < 192) {
-        const int part = t >> 6, d = t & 63;
-        const int w = (part == 0 ? qo : (part == 1 ? ko : vo)) + d;
-        u64 v[1] = {ll_get(src + w)};
-        settle(c, src, v, [&](int) { return w; });
-        float *dst = part == 0 ? L.q : (part == 1 ? L.kn : L.vn);
-        dst[d] = ll_val(v[0]);
-    }
-    __syncthreads();
-    if (trace_slot && tid == 0) *trace_slot = wall_clock64();
     if (on) {
         float s[4] = {0.f, 0.f, 0.f, 0.f};
         if (jk < T) {
@@ -529,6 +516,34 @@ __device__ __forceinline__ void attn_chunk(int tid, const ctx &c, float scale, c
     }
 }
 
+
+/* One 64-position chunk c of single-query attention for head h by the 256
+ * threads of one half of the work-group (t = thread in the half): the
+ * computation of g2k_attn_part, with the current position's key and value
+ * taken from the exchange; the chunk's (max, sum, o[64]) go to pout[0..65].
+ * `on` is false for a half without a unit; it still takes part in the
+ * barriers. */
+template <bool LOCAL>
+__device__ __forceinline__ void attn_chunk(int tid, const ctx &c, float scale, const u64 *src, int qo,
+                                           int ko, int vo, u64 *pout, att_lds &L, att_regs &r, bool on,
+                                           int ch, int pos, int T, u64 *trace_slot = nullptr)
+{
+    const int t = tid & 255;
+    /* q, k and v of the head at this position: src[qo + d], src[ko + d],
+     * src[vo + d] */
+    if (on && t < 192) {
+        const int part = t >> 6, d = t & 63;
+        const int w = (part == 0 ? qo : (part == 1 ? ko : vo)) + d;
+        u64 v[1] = {ll_get(src + w)};
+        settle(c, src, v, [&](int) { return w; });
+        float *dst = part == 0 ? L.q : (part == 1 ? L.kn : L.vn);
+        dst[d] = ll_val(v[0]);
+    }
+    __syncthreads();
+    if (trace_slot && tid == 0) *trace_slot = wall_clock64();
+    attn_compute<LOCAL>(tid, c, scale, pout, L, r, on, ch, pos, T);
+}
+
 __device__ __forceinline__ bool am_better2(float v1, int i1, float v2, int i2)
 {
     return v1 > v2 || (v1 == v2 && i1 < i2);
@@ -565,6 +580,72 @@ __device__ __forceinline__ int fresh_tid()
     int t = threadIdx.x;
     asm volatile("" : "+v"(t));
     return t;
+}
+
+/* LM head and greedy pick, the end of every step kernel: X2 of the last
+ * layer (xlast: E words from nwg producers) -> LayerNorm_f -> logits of the
+ * work-group's head rows -> first-max per work-group (argmax words AM) ->
+ * work-group 0 merges them (g2k_argmax_merge with advance) and advances the
+ * device state.  All threads of the work-group take part. */
+template <typename WT>
+__device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, const u64 *xlast, u64 *AM,
+                                        u32x4 (&wa)[UMAX][4], bool preloaded, float *xres, float *xin,
+                                        float *part, float *red, float *amv, int *ami, lds_flag *flag)
+{
+    /* ---- LM: logits over the head rows, work-group first-max */
+    const int tid = fresh_tid();
+    const int wg = blockIdx.x, nwg = gridDim.x, l = a.L;
+    const int E = a.E, V = a.V;
+    const int ngen = a.state[G2S_NGEN], min_new = a.state[G2S_MIN_NEW];
+    const int pos = clampi(a.state[G2S_POS], 0, a.S - 1);
+    const unsigned seq = (unsigned)a.state[G2S_SEQ];
+    constexpr int NPE = (G2_STEP_MAXE + NT - 1) / NT;
+    const ln_params<NPE> lpf = ln_load<NPE>(tid, gl(a.lnf_w), gl(a.lnf_b), E);
+    const plan p = make_plan<WT>(a.lm_w, V, E);
+    if (!preloaded) load_set<UMAX>(tid, wa, p, 0);
+    fetch<NPE>(tid, c, xlast, E, nwg, xres, flag);
+    TRACE(0);
+    layernorm(tid, xres, xin, lpf, E, red);
+    matvec<WT, UMAX>(tid, wa, p, xin, part);
+    const int masked = ngen < min_new ? G2_EOS_ID : -1;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    if (tid < p.nrows) {
+        const int r = p.r0 + tid;
+        const float v = row_sum(p, part, tid);
+        glw(a.logits)[r] = v;
+        bv = r == masked ? -1e30f : v;
+        bi = r;
+    }
+    blk_argmax(tid, bv, bi, amv, ami);
+    if (tid == 0) {
+        ll_put(AM + 2 * wg, amv[0], c.tag);
+        ll_put(AM + 2 * wg + 1, __int_as_float(ami[0]), c.tag);
+    }
+    TRACE(1);
+    if (wg != 0) return;
+
+    /* ---- greedy pick (g2k_argmax_merge with advance) */
+    __syncthreads();
+    fetch<2>(tid, c, AM, 2 * nwg, nwg, xin, flag);
+    bv = -INFINITY;
+    bi = 0x7fffffff;
+    for (int b = tid; b < nwg; b += NT) {
+        const float v = xin[2 * b];
+        const int i = __float_as_int(xin[2 * b + 1]);
+        if (am_better2(v, i, bv, bi)) { bv = v; bi = i; }
+    }
+    blk_argmax(tid, bv, bi, amv, ami);
+    if (tid == 0) {
+        const int tk = (ami[0] >= 0 && ami[0] < V) ? ami[0] : 0;
+        const int ng = clampi(ngen, 0, G2S_WORDS - G2S_IDS - 1);
+        a.state[G2S_IDS + ng] = tk;
+        a.state[G2S_TOK] = tk;
+        a.state[G2S_NGEN] = ng + 1;
+        a.state[G2S_POS] = pos + 1;
+        a.state[G2S_SEQ] = (int)(seq + 1u);
+    }
+    TRACE(2);
 }
 
 template <typename WT>
@@ -759,55 +840,9 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         }
     }
 
-    /* ---- LM: logits over the head rows, work-group first-max */
-    const int tid = fresh_tid();
-    const int l = a.L;
-    const ln_params<NPE> lpf = ln_load<NPE>(tid, gl(a.lnf_w), gl(a.lnf_b), E);
-    fetch<NPE>(tid, c, X + (size_t)(a.L - 1) * a.xlayer + G2X_X2(E, NH, F), E, nwg, xres, (lds_flag *)&flag);
-    TRACE(0);
-    layernorm(tid, xres, xin, lpf, E, red);
-    const plan p = make_plan<WT>(a.lm_w, V, E);
-    matvec<WT, UMAX>(tid, wa, p, xin, part);
-    const int masked = ngen < min_new ? G2_EOS_ID : -1;
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
-    if (tid < p.nrows) {
-        const int r = p.r0 + tid;
-        const float v = row_sum(p, part, tid);
-        glw(a.logits)[r] = v;
-        bv = r == masked ? -1e30f : v;
-        bi = r;
-    }
-    blk_argmax(tid, bv, bi, amv, ami);
-    u64 *AM = X + (size_t)a.L * a.xlayer;
-    if (tid == 0) {
-        ll_put(AM + 2 * wg, amv[0], c.tag);
-        ll_put(AM + 2 * wg + 1, __int_as_float(ami[0]), c.tag);
-    }
-    TRACE(1);
-    if (wg != 0) return;
-
-    /* ---- greedy pick (g2k_argmax_merge with advance) */
-    __syncthreads();
-    fetch<2>(tid, c, AM, 2 * nwg, nwg, xin, (lds_flag *)&flag);
-    bv = -INFINITY;
-    bi = 0x7fffffff;
-    for (int b = tid; b < nwg; b += NT) {
-        const float v = xin[2 * b];
-        const int i = __float_as_int(xin[2 * b + 1]);
-        if (am_better2(v, i, bv, bi)) { bv = v; bi = i; }
-    }
-    blk_argmax(tid, bv, bi, amv, ami);
-    if (tid == 0) {
-        const int tk = (ami[0] >= 0 && ami[0] < V) ? ami[0] : 0;
-        const int ng = clampi(ngen, 0, G2S_WORDS - G2S_IDS - 1);
-        a.state[G2S_IDS + ng] = tk;
-        a.state[G2S_TOK] = tk;
-        a.state[G2S_NGEN] = ng + 1;
-        a.state[G2S_POS] = pos + 1;
-        a.state[G2S_SEQ] = (int)(seq + 1u);
-    }
-    TRACE(2);
+    /* the first batch of lm_head rows was loaded by the last fc2 phase */
+    lm_pick<WT>(a, c, X + (size_t)(a.L - 1) * a.xlayer + G2X_X2(E, NH, F), X + (size_t)a.L * a.xlayer, wa, true,
+                xres, xin, part, red, amv, ami, (lds_flag *)&flag);
 }
 
 } /* namespace g2step */

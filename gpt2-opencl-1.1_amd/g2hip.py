@@ -394,7 +394,8 @@ class Model:
         return _lib.g2_model_uses_step(self.h) >= 1
 
     def step_kind(self):
-        """2: XCD-parallel step kernel, 1: all-to-all step kernel, 0: per-operator kernels."""
+        """3: two-role step kernel, 2: XCD-parallel step kernel, 1: all-to-all step kernel,
+        0: per-operator kernels."""
         return _lib.g2_model_uses_step(self.h)
 
     def prefill(self, ids):

@@ -20,14 +20,26 @@ from parity import greedy_agree, random_prompt
 pytestmark = pytest.mark.gpu
 
 SEED = 0x67707432
-KINDS = [pytest.param("0", id="all-to-all"), pytest.param("1", id="xcd")]
+KINDS = [pytest.param("a2a", id="all-to-all"), pytest.param("xcd", id="xcd"),
+         pytest.param("two-role", id="two-role")]
+ENV = {"a2a": {"G2_STEPX": "0", "G2_STEP3": "0"}, "xcd": {"G2_STEPX": "1", "G2_STEP3": "0"},
+       "two-role": {"G2_STEPX": "0", "G2_STEP3": "1"}}
+KIND_ID = {"a2a": 1, "xcd": 2, "two-role": 3}
 
 
 @pytest.fixture
 def stepx(request, monkeypatch):
     """Selects the step-kernel form for models created in the test."""
-    monkeypatch.setenv("G2_STEPX", request.param)
+    for k, v in ENV[request.param].items():
+        monkeypatch.setenv(k, v)
     return request.param
+
+
+def _expect_kind(m, kind, f16=True):
+    """The two-role form runs fp16-weight models; the others run both."""
+    if kind == "two-role" and not f16:
+        return
+    assert m.step_kind() == KIND_ID[kind], f"expected step kernel form {kind}, got {m.step_kind()}"
 
 
 def _check(got, ref, f16):
@@ -60,6 +72,8 @@ def test_step_matches_operator_kernels(g2, stepx, dtype):
     m = g2.Model.synth(cfg, SEED, dt, g2.PATH_FUSED)
     prompt = random_prompt(48, cfg.vocab_size, 11)
     print(f"[step] small {dtype} form {m.step_kind()}: step kernel vs operator kernels", flush=True)
+    if stepx != "xcd":
+        _expect_kind(m, stepx, dtype == "f16")
     m.set_step(True)
     ids_s, _ = m.generate(prompt, 20)
     lg_s = m.logits()
@@ -92,6 +106,8 @@ def test_step_xl_width_to_end_of_context(g2, stepx):
     om = oracle.Model(cfg, w, kslice=4)
     m = g2.Model.from_host(cfg, w, g2.F16, g2.PATH_FUSED)
     assert m.uses_step()
+    if stepx != "xcd":
+        _expect_kind(m, stepx)
     P = 1000
     prompt = random_prompt(P, cfg.vocab_size, 77)
     print(f"[step] XL width L2 form {m.step_kind()}, prompt {P}", flush=True)
@@ -137,12 +153,14 @@ def test_step_decode_run_matches_generate(g2, stepx):
     m.free()
 
 
+@pytest.mark.parametrize("stepx", [pytest.param("xcd", id="xcd"), pytest.param("two-role", id="two-role")],
+                         indirect=True)
 @pytest.mark.parametrize("cfg_args", [(2, 128, 2, 256), (3, 192, 3, 1000), (1, 64, 1, 50257)],
                          ids=["tiny", "3-heads", "1-head"])
-def test_stepx_small_shapes(g2, monkeypatch, cfg_args):
-    """XCD-parallel kernel on shapes where some XCDs own no head (n_head < 8)
-    and ffn slices are a few chunks: greedy ids and logits vs the oracle."""
-    monkeypatch.setenv("G2_STEPX", "1")
+def test_stepx_small_shapes(g2, stepx, cfg_args):
+    """The XCD-parallel and two-role kernels on small shapes: some XCDs own
+    no head (n_head < 8), most work-groups own no ffn or output rows, ffn
+    slices are a few chunks.  Greedy ids and logits vs the oracle."""
     L, E, H, V = cfg_args
     cfg = g2.make_config(L, E, H, vocab_size=V)
     for dtype in (g2.F32, g2.F16):
@@ -153,6 +171,8 @@ def test_stepx_small_shapes(g2, monkeypatch, cfg_args):
         ref_ids, top2, ref_lg = om.generate(prompt, 12, logit_steps=4)
         m = g2.Model.from_host(cfg, w, dtype, g2.PATH_FUSED)
         print(f"[step] L{L} E{E} H{H} V{V} {'f16' if f16 else 'f32'} form {m.step_kind()}", flush=True)
+        if stepx == "two-role":
+            _expect_kind(m, stepx, f16)
         ids, _ = m.generate(prompt, 12)
         greedy_agree(ids, ref_ids, top2, 1e-2 if f16 else 1e-4)
         m.prefill(prompt)
