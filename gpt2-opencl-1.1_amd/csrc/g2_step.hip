@@ -183,14 +183,16 @@ __device__ __forceinline__ void settle(const ctx &c, const u64 *src, u64 (&v)[NP
 /* All threads: dst[w] = value of src[w] for w < n <= NP*NT once it carries
  * the tag (thread tid takes w = tid + NT*i).
  *
- * Waiting must not flood the memory system: if every thread of every
- * work-group re-read all of its words each round trip, a 6400-word vector
- * would cost ~13 MB of coherent reads per round, competing with the weight
- * stream.  So after one speculative read of everything, a work-group that
- * found stale words waits on nsent sentinel words only (word n*k/nsent for
- * k < nsent: the first word of each producer when n is split evenly over
- * nsent producers), then re-reads just its stale words.  Ends with a
- * barrier; `flag` is an LDS word of the caller. */
+ * Vectors of up to 4 words per thread (n <= 2048): after one speculative
+ * read, each thread polls its own stale words until they carry the tag; a
+ * word is then seen one round trip after it lands.  Larger vectors must not
+ * flood the memory system (a 6400-word vector re-read by every work-group
+ * each round trip would be ~13 MB of coherent reads per round, competing
+ * with the weight stream), so a work-group that found stale words waits on
+ * nsent sentinel words only (word n*k/nsent for k < nsent: the first word
+ * of each producer when n is split evenly over nsent producers), then
+ * re-reads just its stale words.  Ends with a barrier; `flag` is an LDS
+ * word of the caller. */
 template <int NP>
 __device__ __forceinline__ void fetch(int tid, const ctx &c, const u64 *src, int n, int nsent,
                                       float *dst, lds_flag *flag)
@@ -201,6 +203,18 @@ __device__ __forceinline__ void fetch(int tid, const ctx &c, const u64 *src, int
     for (int i = 0; i < NP; ++i) {
         const int w = tid + NT * i;
         v[i] = w < n ? ll_get(src + w) : filler;
+    }
+    if constexpr (NP <= 4) {
+        (void)nsent;
+        (void)flag;
+        settle(c, src, v, [&](int i) { const int w = tid + NT * i; return w < n ? w : -1; });
+#pragma unroll
+        for (int i = 0; i < NP; ++i) {
+            const int w = tid + NT * i;
+            if (w < n) dst[w] = ll_val(v[i]);
+        }
+        __syncthreads();
+        return;
     }
     if (tid == 0) *flag = 0;
     __syncthreads();
@@ -226,20 +240,6 @@ __device__ __forceinline__ void fetch(int tid, const ctx &c, const u64 *src, int
     __syncthreads();
 }
 
-/* Sum over the 512-thread work-group, wave totals added in wave order.
- * `red` must not be rewritten before every thread has read it (callers
- * alternate buffers). */
-__device__ __forceinline__ float blk_sum(int tid, float v, float *red)
-{
-    v = wsum(v);
-    if ((tid & 63) == 0) red[tid >> 6] = v;
-    __syncthreads();
-    float t = red[0];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) t += red[w];
-    return t;
-}
-
 /* LayerNorm parameters of the thread's entries i = tid + NT*k, loaded at
  * the start of a phase so their latency overlaps the input wait. */
 template <int NE>
@@ -253,11 +253,25 @@ __device__ __forceinline__ ln_params<NE> ln_load(int tid, const G2_GLOBAL float 
     ln_params<NE> p;
 #pragma unroll
     for (int k = 0; k < NE; ++k) {
-        const int i = tid + NT * k;
-        p.g[k] = i < E ? g[i] : 0.f;
-        p.b[k] = i < E ? b[i] : 0.f;
+        const int i = min(tid + NT * k, E - 1); /* unconditional, as in load_set */
+        p.g[k] = g[i];
+        p.b[k] = b[i];
     }
     return p;
+}
+
+/* Sum over the 512-thread work-group, wave totals added in wave order.
+ * `red` must not be rewritten before every thread has read it (callers
+ * alternate buffers). */
+__device__ __forceinline__ float blk_sum(int tid, float v, float *red)
+{
+    v = wsum(v);
+    if ((tid & 63) == 0) red[tid >> 6] = v;
+    __syncthreads();
+    float t = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) t += red[w];
+    return t;
 }
 
 /* xin = LayerNorm(x) over E entries (both in LDS): mean, then biased
@@ -321,7 +335,13 @@ __device__ __forceinline__ plan make_plan(const void *W, int N, int K)
     return p;
 }
 
-/* Issue the loads of one batch (NW*UM units) into a register set. */
+/* Issue the loads of one batch (NW*UM units) into a register set.  The
+ * loads are unconditional, every address clamped into the work-group's
+ * share (lanes past a segment end to its last chunk, which the same
+ * instruction fetches anyway; units past the share to its first row): a
+ * load under a lane condition makes the compiler wait for every load in
+ * flight before the value is first used.  Dot products ignore the clamped
+ * chunks (their x is zero) and the units past the share. */
 template <int UM>
 __device__ __forceinline__ void load_set(int tid, u32x4 (&w)[UM][4], const plan &p, int batch)
 {
@@ -335,9 +355,8 @@ __device__ __forceinline__ void load_set(int tid, u32x4 (&w)[UM][4], const plan 
         const int c1 = min(p.C, c0 + p.SL);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int cc = c0 + lane + 64 * i;
-            w[j][i] = (u32x4){0u, 0u, 0u, 0u};
-            if (uv && cc < c1) w[j][i] = __builtin_nontemporal_load(gl(p.W) + (size_t)row * p.C + cc);
+            const int cc = min(c0 + lane + 64 * i, c1 - 1);
+            w[j][i] = __builtin_nontemporal_load(gl(p.W) + (size_t)row * p.C + cc);
         }
     }
 }
@@ -706,7 +725,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             TRACE(0);
             const plan p = make_plan<WT>(y.qkv_w, 3 * E, E);
             const ln_params<NPE> lp = ln_load<NPE>(tid, gl(y.ln1_w), gl(y.ln1_b), E);
-            const float bias = tid < p.nrows && y.qkv_b ? gl(y.qkv_b)[p.r0 + tid] : 0.f;
+            const float bias = gl(y.qkv_b)[min(p.r0 + tid, 3 * E - 1)]; /* used by tid < nrows */
             if (l > 0) {
                 fetch<NPE>(tid, c, X + (size_t)(l - 1) * a.xlayer + G2X_X2(E, NH, F), E, nwg, xres, (lds_flag *)&flag);
             }
@@ -780,7 +799,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         {
             const int tid = fresh_tid();
             const plan p = make_plan<WT>(y.proj_w, E, E);
-            const float bias = tid < p.nrows && y.proj_b ? gl(y.proj_b)[p.r0 + tid] : 0.f;
+            const float bias = gl(y.proj_b)[min(p.r0 + tid, E - 1)];
             fetch<NPE>(tid, c, R + G2X_O(E, NH), E, NH, xin, (lds_flag *)&flag);
             TRACE(5);
             matvec<WT, UPROJ>(tid, wp, p, xin, part);
@@ -800,7 +819,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             const int tid = fresh_tid();
             const plan p = make_plan<WT>(y.fc_w, F, E);
             const ln_params<NPE> lp = ln_load<NPE>(tid, gl(y.ln2_w), gl(y.ln2_b), E);
-            const float bias = tid < p.nrows && y.fc_b ? gl(y.fc_b)[p.r0 + tid] : 0.f;
+            const float bias = gl(y.fc_b)[min(p.r0 + tid, F - 1)];
             fetch<NPE>(tid, c, R + G2X_X1(E, NH), E, nwg, xres, (lds_flag *)&flag);
             TRACE(7);
             layernorm(tid, xres, xin, lp, E, red);
@@ -822,7 +841,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         {
             const int tid = fresh_tid();
             const plan p = make_plan<WT>(y.fc2_w, E, F);
-            const float bias = tid < p.nrows && y.fc2_b ? gl(y.fc2_b)[p.r0 + tid] : 0.f;
+            const float bias = gl(y.fc2_b)[min(p.r0 + tid, E - 1)];
             fetch<PMAX>(tid, c, R + G2X_H(E, NH), F, nwg, xin, (lds_flag *)&flag);
             TRACE(9);
             matvec<WT, UMAX>(tid, wa, p, xin, part);
