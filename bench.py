@@ -26,7 +26,14 @@ their accumulation order) on the host's cores, decoding a bounded sample of
 the same workload -- a few forwards at positions 512.. over the KV cache the
 GPU prefill produced.
 
+traffic: HBM bytes per launch of that kernel from rocprofv3 counter runs
+(FETCH_SIZE and WRITE_SIZE, one run each), each scaled by what the same
+counter reads for a plain device copy of known size (`--copy-probe`); the
+figures are read from profiles/g2k_step_f16_xl_traffic.json when it exists
+and matches this workload, else traffic is null.
+
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+       python bench.py --copy-probe   (device copies of 1 GiB, for counter calibration)
 """
 import argparse
 import json
@@ -55,6 +62,36 @@ def step_bytes(cfg, w_bytes, kv_bytes, positions):
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+COPY_BYTES = 1 << 30
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "g2k_step_f16_xl_traffic.json")
+
+
+def copy_probe():
+    """Five device-to-device copies of COPY_BYTES (torch's copy kernel): the
+    known-size reference for calibrating the FETCH_SIZE / WRITE_SIZE
+    counters."""
+    import torch
+    x = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    y = torch.empty_like(x)
+    for _ in range(5):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "copies": 5}), flush=True)
+
+
+def measured_traffic(kernel, workload):
+    """HBM bytes per launch from the committed counter summary, if it was
+    taken on this kernel and workload."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if t.get("kernel") != kernel or t.get("workload") != workload:
+        return None
+    return t.get("bytes_per_launch")
 
 
 def cpu_baseline(g2, m, cfg, token, n_steps=4):
@@ -93,7 +130,11 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--config", default="xl", choices=["small", "medium", "large", "xl"])
     ap.add_argument("--fp32", action="store_true", help="fp32 weights instead of fp16")
+    ap.add_argument("--copy-probe", action="store_true", help="device copies of 1 GiB for counter calibration")
     args = ap.parse_args()
+    if args.copy_probe:
+        copy_probe()
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} (WORLD_SIZE {world}) is not "
@@ -145,13 +186,16 @@ def main():
     bytes_step = step_bytes(cfg, 2 if f16 else 4, 4, range(P, P + n_dec))
     achieved = bytes_step / (step_ms_events * 1e-3) / 1e9
 
+    kind = m.step_kind()
+    kname = ({1: "g2k_step", 2: "g2k_stepx", 3: "g2k_step3"}.get(kind, "") + ("_f16" if f16 else "_f32")) if kind else ""
+    workload = (f"GPT-2 {args.config.upper()} {'fp16' if f16 else 'fp32'}-weight batch-1 greedy decode: {P}-token "
+                f"random prompt, {n_dec} decode forwards (positions {P}..{P + n_dec - 1})")
     result = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic",
-        "config": {"workload": f"GPT-2 {args.config.upper()} {'fp16' if f16 else 'fp32'}-weight batch-1 greedy "
-                               f"decode: {P}-token random prompt, {n_dec} decode forwards (positions {P}..{P + n_dec - 1})",
+        "config": {"workload": workload,
                    "weights": "f16" if f16 else "f32", "kv_cache": "f32", "accumulate": "f32",
                    "decode_engine": "persistent step kernel" if m.uses_step() else
                    ("per-operator kernels, graph replay" if m.uses_graph() == 1 else "per-operator kernels")},
@@ -159,8 +203,9 @@ def main():
         "prefill_ms": round(min(prefill_ms), 3),
         "decode_ms_per_token": round(step_ms_events / n_dec, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": (f"g2k_step_{'f16' if f16 else 'f32'} (one launch per decode token)" if m.uses_step()
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(kname, workload) if kname else None,
+                     "kernel": (f"{kname} (one launch per decode token)" if kname
                                 else "decode step (per-operator kernels)"),
                      "bytes_per_launch": round(bytes_step / n_dec)},
     }
