@@ -468,6 +468,124 @@ G2_GEMM(g2k_gemm_nk_f32_qkv, float, true, GEPI_QKV)
 G2_GEMM(g2k_gemm_nk_f16_qkv, _Float16, true, GEPI_QKV)
 
 /* ======================================================================
+ * fp16 MFMA GEMM for the fused prefill with fp16 weights:
+ * C[M,N] = A[M,K] . W[N,K]^T + bias with the epilogues of g2_gemm_args.
+ *
+ * A is fp32.  It enters the fp16 matrix cores as two halves, a_hi =
+ * fp16(a) and a_lo = fp16(a - a_hi), so every product a*w is computed as
+ * a_hi*w + a_lo*w with 22 significant bits of a and fp32 accumulation; the
+ * weights are exact in fp16.  This keeps the fp32 activations of the
+ * reference (main.c:1739-1790 runs its matmuls in fp32) at twice the cost
+ * of a plain fp16 product, still far below the fp32 MFMA rate.
+ *
+ * Tile 64x64x64, 256 threads = 2x2 waves of 32x32, each wave a 2x2 grid of
+ * v_mfma_f32_16x16x32_f16: lane l supplies A[l%16][8(l/16)..+7] and
+ * W[l%16][8(l/16)..+7] (8 consecutive k), the result lane l holds rows
+ * 4(l/16)+r, column l%16.  Requires N % 64 == 0 and K % 64 == 0 (the
+ * fused path's matrices: multiples of the head dim); rows >= M are zero.
+ * ==================================================================== */
+typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
+
+template <int EPI>
+__device__ void hgemm_impl(const g2_gemm_args &a)
+{
+    constexpr int BM = 64, BN = 64, BK = 64, LD = BK + 8; /* halves per LDS row */
+    __shared__ __attribute__((aligned(16))) _Float16 Ah[BM * LD];
+    __shared__ __attribute__((aligned(16))) _Float16 Al[BM * LD];
+    __shared__ __attribute__((aligned(16))) _Float16 Bs[BN * LD];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int M = a.M, N = a.N, K = a.K;
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    /* staging: thread -> tile row r, 16 consecutive k from kq */
+    const int r = tid >> 2, kq = (tid & 3) * 16;
+    const bool arow = m0 + r < M;
+    const float *ap = a.A + (size_t)min(m0 + r, M - 1) * K + kq;
+    const _Float16 *wrow = (const _Float16 *)a.B + (size_t)(n0 + r) * K + kq;
+    const int fr = lane & 15, fk = 8 * (lane >> 4);
+
+    for (int k0 = 0; k0 < K; k0 += BK) {
+        f32x4 av[4];
+        h16x8 bv[2];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) av[q] = *(const f32x4 *)(ap + k0 + 4 * q);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) bv[q] = *(const h16x8 *)(wrow + k0 + 8 * q);
+        h16x8 hi[2], lo[2];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const float x = arow ? av[e >> 2][e & 3] : 0.f;
+            const _Float16 h = (_Float16)x;
+            hi[e >> 3][e & 7] = h;
+            lo[e >> 3][e & 7] = (_Float16)(x - (float)h);
+        }
+        __syncthreads(); /* the previous tile has been consumed */
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            *(h16x8 *)(Ah + r * LD + kq + 8 * q) = hi[q];
+            *(h16x8 *)(Al + r * LD + kq + 8 * q) = lo[q];
+            *(h16x8 *)(Bs + r * LD + kq + 8 * q) = bv[q];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 32) {
+            h16x8 afh[2], afl[2], bf[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int row = (wm * 32 + i * 16 + fr) * LD + kk + fk;
+                afh[i] = *(const h16x8 *)(Ah + row);
+                afl[i] = *(const h16x8 *)(Al + row);
+            }
+#pragma unroll
+            for (int j = 0; j < 2; ++j) bf[j] = *(const h16x8 *)(Bs + (wn * 32 + j * 16 + fr) * LD + kk + fk);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afh[i], bf[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afl[i], bf[j], acc[i][j], 0, 0, 0);
+                }
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + q;
+                const int n = n0 + wn * 32 + j * 16 + (lane & 15);
+                if (m >= M || n >= N) continue;
+                float v = acc[i][j][q];
+                if (a.bias) v += a.bias[n];
+                if (EPI == GEPI_STORE) {
+                    a.C[(size_t)m * N + n] = v;
+                } else if (EPI == GEPI_GELU) {
+                    a.C[(size_t)m * N + n] = gelu_f(v);
+                } else if (EPI == GEPI_RESID) {
+                    a.C[(size_t)m * N + n] = v + a.C[(size_t)m * N + n];
+                } else {
+                    const int E = a.E, pos = a.pos0 + m;
+                    if (n < E) a.q_out[(size_t)m * E + n] = v;
+                    else if (n < 2 * E) a.k_cache[(size_t)(n - E) * a.S + pos] = v;
+                    else a.v_cache[(size_t)pos * E + (n - 2 * E)] = v;
+                }
+            }
+}
+
+G2K void g2k_hgemm_store(const g2_gemm_args a) { hgemm_impl<GEPI_STORE>(a); }
+G2K void g2k_hgemm_gelu(const g2_gemm_args a) { hgemm_impl<GEPI_GELU>(a); }
+G2K void g2k_hgemm_resid(const g2_gemm_args a) { hgemm_impl<GEPI_RESID>(a); }
+G2K void g2k_hgemm_qkv(const g2_gemm_args a) { hgemm_impl<GEPI_QKV>(a); }
+
+/* ======================================================================
  * Causal attention over a prompt (prefill), head dim 64
  *
  * grid (NH, ceil(P/64)), 256 threads: thread (r = tid/4, g = tid%4) owns

@@ -921,6 +921,14 @@ static int fused_prefill(g2_model *m, int P)
 {
     const int E = m->cfg.n_embd, F = m->cfg.ffn_dim, NH = m->cfg.n_head;
     const int f16 = m->dtype == G2_F16;
+    /* fp16 weights: the split-activation fp16 MFMA GEMM (n_embd and ffn are
+     * multiples of 64 on the fused path); G2_PREFILL_F32MFMA=1 keeps the
+     * fp32-MFMA GEMM for comparison */
+    const char *pe = getenv("G2_PREFILL_F32MFMA");
+    const int h = f16 && E % 64 == 0 && F % 64 == 0 && !(pe && pe[0] == '1');
+    const int f_qkv = h ? G2F_HGEMM_QKV : (f16 ? G2F_GEMM_NK_F16_QKV : G2F_GEMM_NK_F32_QKV);
+    const int f_resid = h ? G2F_HGEMM_RESID : (f16 ? G2F_GEMM_NK_F16_RESID : G2F_GEMM_NK_F32_RESID);
+    const int f_gelu = h ? G2F_HGEMM_GELU : (f16 ? G2F_GEMM_NK_F16_GELU : G2F_GEMM_NK_F32_GELU);
     g2_embed_args e = { m->wte, m->wpe, m->hidden, m->ids_dev, NULL, E, P, 0 };
     int rc = g2i_launch(f16 ? G2F_EMBED_F16 : G2F_EMBED_F32, cdivu(E, 256), (unsigned)P, 256, &e);
     for (int l = 0; l < m->cfg.n_layer && !rc; ++l) {
@@ -931,23 +939,19 @@ static int fused_prefill(g2_model *m, int P)
         g.A = m->ln_out; g.B = y->qkv_w; g.bias = y->qkv_b; g.q_out = m->q;
         g.k_cache = y->k_cache; g.v_cache = y->v_cache; g.M = P; g.N = 3 * E; g.K = E;
         g.E = E; g.S = G2_KV_MAX_SEQ; g.pos0 = 0;
-        if (!rc) rc = g2i_launch(f16 ? G2F_GEMM_NK_F16_QKV : G2F_GEMM_NK_F32_QKV,
-                                 cdivu(3 * E, 64), cdivu(P, 64), 256, &g);
+        if (!rc) rc = g2i_launch(f_qkv, cdivu(3 * E, 64), cdivu(P, 64), 256, &g);
         g2_attnp_args t = { m->q, y->k_cache, y->v_cache, m->attn, P, E, NH, G2_KV_MAX_SEQ, 1.0f / sqrtf(64.0f) };
         if (!rc) rc = g2i_launch(G2F_ATTN_PREFILL, (unsigned)NH, cdivu(P, 64), 256, &t);
         memset(&g, 0, sizeof g);
         g.A = m->attn; g.B = y->proj_w; g.bias = y->proj_b; g.C = m->hidden; g.M = P; g.N = E; g.K = E;
-        if (!rc) rc = g2i_launch(f16 ? G2F_GEMM_NK_F16_RESID : G2F_GEMM_NK_F32_RESID,
-                                 cdivu(E, 64), cdivu(P, 64), 256, &g);
+        if (!rc) rc = g2i_launch(f_resid, cdivu(E, 64), cdivu(P, 64), 256, &g);
         if (!rc) rc = g2_layernorm(m->hidden, m->ln_out, y->ln2_w, y->ln2_b, E, P);
         memset(&g, 0, sizeof g);
         g.A = m->ln_out; g.B = y->fc_w; g.bias = y->fc_b; g.C = m->ffn1; g.M = P; g.N = F; g.K = E;
-        if (!rc) rc = g2i_launch(f16 ? G2F_GEMM_NK_F16_GELU : G2F_GEMM_NK_F32_GELU,
-                                 cdivu(F, 64), cdivu(P, 64), 256, &g);
+        if (!rc) rc = g2i_launch(f_gelu, cdivu(F, 64), cdivu(P, 64), 256, &g);
         memset(&g, 0, sizeof g);
         g.A = m->ffn1; g.B = y->fc2_w; g.bias = y->fc2_b; g.C = m->hidden; g.M = P; g.N = E; g.K = F;
-        if (!rc) rc = g2i_launch(f16 ? G2F_GEMM_NK_F16_RESID : G2F_GEMM_NK_F32_RESID,
-                                 cdivu(E, 64), cdivu(P, 64), 256, &g);
+        if (!rc) rc = g2i_launch(f_resid, cdivu(E, 64), cdivu(P, 64), 256, &g);
     }
     if (!rc) rc = fused_lm_head(m, m->hidden + (size_t)(P - 1) * E, 1);
     return rc;

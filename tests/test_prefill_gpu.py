@@ -1,0 +1,43 @@
+"""GPU parity of the fused prefill with fp16 weights, whose matmuls run on
+the fp16 matrix cores with the fp32 activations split into two fp16 halves
+(g2k_hgemm_*): last-position logits against the CPU oracle (5e-2, as for
+every fp16-weight path) and against the fp32-MFMA GEMM of the same library
+(G2_PREFILL_F32MFMA=1), which the split must match to fp32-level
+accumulation differences, at GPT-2 XL width and for ragged prompt lengths
+(not multiples of the 64-row tile) up to the 1023-position limit.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle
+from parity import random_prompt
+
+pytestmark = pytest.mark.gpu
+
+SEED = 0x67707432
+
+
+@pytest.mark.parametrize("P", [1, 37, 64, 200, 1023])
+def test_prefill_split_fp16_mfma(g2, monkeypatch, P):
+    cfg = g2.make_config(2, 1600, 25, vocab_size=50257)
+    w = g2.synth_weights(cfg, SEED, f16_round=True)
+    prompt = random_prompt(P, cfg.vocab_size, 100 + P)
+    print(f"[prefill] XL width L2, P {P}", flush=True)
+    monkeypatch.delenv("G2_PREFILL_F32MFMA", raising=False)
+    m = g2.Model.from_host(cfg, w, g2.F16, g2.PATH_FUSED)
+    m.prefill(prompt)
+    lg_h = m.logits().copy()
+    m.free()
+    monkeypatch.setenv("G2_PREFILL_F32MFMA", "1")
+    m = g2.Model.from_host(cfg, w, g2.F16, g2.PATH_FUSED)
+    m.prefill(prompt)
+    lg_f = m.logits().copy()
+    m.free()
+    om = oracle.Model(cfg, w, kslice=4)
+    om.prefill(prompt)
+    ref = om.logits()
+    om.close()
+    np.testing.assert_allclose(lg_h, ref, rtol=5e-2, atol=5e-2)
+    np.testing.assert_allclose(lg_h, lg_f, rtol=1e-3, atol=2e-3)
+    assert int(np.argmax(lg_h)) == int(np.argmax(ref)) or \
+        np.sort(ref)[-1] - np.sort(ref)[-2] < 1e-2
