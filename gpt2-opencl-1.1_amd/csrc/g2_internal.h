@@ -57,7 +57,8 @@
     X(XCC_PROBE, "g2k_xcc_probe") X(STEP3_F16, "g2k_step3_f16")               \
     X(TRANSPOSE16, "g2k_transpose16")                                         \
     X(HGEMM_STORE, "g2k_hgemm_store") X(HGEMM_GELU, "g2k_hgemm_gelu")         \
-    X(HGEMM_RESID, "g2k_hgemm_resid") X(HGEMM_QKV, "g2k_hgemm_qkv")
+    X(HGEMM_RESID, "g2k_hgemm_resid") X(HGEMM_QKV, "g2k_hgemm_qkv")           \
+    X(ATTN_PREFILL_MFMA, "g2k_attn_prefill_mfma")
 
 #define G2_ENUM_ENTRY(id, name) G2F_##id,
 enum { G2_KERNEL_LIST(G2_ENUM_ENTRY) G2F_COUNT };

@@ -671,6 +671,146 @@ G2K void g2k_attn_prefill(const g2_attnp_args a)
     }
 }
 
+/* The same attention on the fp32 matrix cores (v_mfma_f32_16x16x4f32):
+ * grid (NH, ceil(P/64)), 256 threads; wave w owns query rows 16w..16w+15
+ * of the block.  Per 64-key block: S = Q K^T (4 tiles of 16 keys, 16 k
+ * steps of 4 dims), scaled and causally masked, online softmax over the
+ * block (row statistics reduced across the 16 lanes of a row group), P
+ * re-laid through LDS into the operand layout, O += P V (4 tiles of 16
+ * dims, 16 k steps of 4 keys).  fp32 throughout, as the reference.
+ * Operand layout: lane l supplies A[l%16][k0 + l/16] and B[k0 + l/16][l%16];
+ * the result lane l holds rows 4(l/16)+r, column l%16. */
+template <int CTRL>
+__device__ __forceinline__ float apf_dpp(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+/* max / sum over the 16 lanes of a DPP row (rotations 8, 4, 2, 1) */
+__device__ __forceinline__ float row16_max(float v)
+{
+    v = fmaxf(v, apf_dpp<0x128>(v));
+    v = fmaxf(v, apf_dpp<0x124>(v));
+    v = fmaxf(v, apf_dpp<0x122>(v));
+    return fmaxf(v, apf_dpp<0x121>(v));
+}
+__device__ __forceinline__ float row16_sum(float v)
+{
+    v += apf_dpp<0x128>(v);
+    v += apf_dpp<0x124>(v);
+    v += apf_dpp<0x122>(v);
+    return v + apf_dpp<0x121>(v);
+}
+
+G2K void g2k_attn_prefill_mfma(const g2_attnp_args a)
+{
+    constexpr int LD = 68;
+    __shared__ __attribute__((aligned(16))) float Kt[64 * LD]; /* [dim][key] */
+    __shared__ __attribute__((aligned(16))) float Vs[64 * LD]; /* [key][dim] */
+    __shared__ float Ps[4][16 * LD];                            /* per wave [row][key] */
+    const int h = blockIdx.x, qb = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
+    if (h >= a.NH || qb * 64 >= a.P) return;
+    const int E = a.E, P = a.P;
+    /* Q operand: lane holds Q[row 16w + lr][dim 4s + lg], s < 16 */
+    float qa[16];
+    {
+        const int i = min(qb * 64 + 16 * wave + lr, P - 1);
+        const float *qp = a.q + (size_t)i * E + h * 64 + lg;
+#pragma unroll
+        for (int st = 0; st < 16; ++st) qa[st] = qp[4 * st];
+    }
+    f32x4 o[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) o[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    float m[4], l[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { m[r] = -INFINITY; l[r] = 0.f; }
+    const int i_base = qb * 64 + 16 * wave + 4 * lg; /* query row of result r: i_base + r */
+    const int sr = tid >> 2, sq = (tid & 3) * 16;    /* staging: row, 16 columns */
+    for (int kb = 0; kb <= qb; ++kb) {
+        const int j0 = kb * 64;
+        f32x4 kv[4], vv[4];
+        {
+            const float *kp = a.k_cache + (size_t)(h * 64 + sr) * a.S + min(j0 + sq, a.S - 16);
+            const float *vp = a.v_cache + (size_t)min(j0 + sr, a.S - 1) * E + h * 64 + sq;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                kv[q] = *(const f32x4 *)(kp + 4 * q);
+                vv[q] = *(const f32x4 *)(vp + 4 * q);
+            }
+        }
+        __syncthreads(); /* the previous block has been consumed */
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            *(f32x4 *)(Kt + sr * LD + sq + 4 * q) = kv[q];
+            *(f32x4 *)(Vs + sr * LD + sq + 4 * q) = vv[q];
+        }
+        __syncthreads();
+        /* S = Q K^T: tile t covers keys 16t..16t+15 */
+        f32x4 sacc[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            sacc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < 16; ++st)
+                sacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[st], Kt[(4 * st + lg) * LD + 16 * t + lr], sacc[t],
+                                                                0, 0, 0);
+        }
+        /* scale, causal mask, online softmax per row */
+        float alpha[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = i_base + r;
+            float bm = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int j = j0 + 16 * t + lr;
+                const float v = (i < P && j <= i) ? sacc[t][r] * a.scale : -INFINITY;
+                sacc[t][r] = v;
+                bm = fmaxf(bm, v);
+            }
+            bm = row16_max(bm);
+            const float mn = fmaxf(m[r], bm);
+            const float ms = mn == -INFINITY ? 0.f : mn;
+            alpha[r] = expf(m[r] - ms);
+            float ps = 0.f;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float p = expf(sacc[t][r] - ms);
+                sacc[t][r] = p;
+                ps += p;
+            }
+            l[r] = fmaf(l[r], alpha[r], row16_sum(ps));
+            m[r] = mn;
+        }
+        /* P to LDS in [row][key], read back as the A operand */
+        float *pw = Ps[wave];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pw[(4 * lg + r) * LD + 16 * t + lr] = sacc[t][r];
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[t][r] *= alpha[r];
+#pragma unroll
+            for (int st = 0; st < 16; ++st)
+                o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(pw[lr * LD + 4 * st + lg], Vs[(4 * st + lg) * LD + 16 * t + lr],
+                                                             o[t], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int i = i_base + r;
+        if (i >= P) continue;
+        const float inv = 1.0f / l[r];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) a.out[(size_t)i * E + h * 64 + 16 * t + lr] = o[t][r] * inv;
+    }
+}
+
 /* Fused decode kernels (packed matvecs, single-query attention). */
 #include "g2_decode.hip"
 

@@ -941,7 +941,7 @@ static int fused_prefill(g2_model *m, int P)
         g.E = E; g.S = G2_KV_MAX_SEQ; g.pos0 = 0;
         if (!rc) rc = g2i_launch(f_qkv, cdivu(3 * E, 64), cdivu(P, 64), 256, &g);
         g2_attnp_args t = { m->q, y->k_cache, y->v_cache, m->attn, P, E, NH, G2_KV_MAX_SEQ, 1.0f / sqrtf(64.0f) };
-        if (!rc) rc = g2i_launch(G2F_ATTN_PREFILL, (unsigned)NH, cdivu(P, 64), 256, &t);
+        if (!rc) rc = g2i_launch(G2F_ATTN_PREFILL_MFMA, (unsigned)NH, cdivu(P, 64), 256, &t);
         memset(&g, 0, sizeof g);
         g.A = m->attn; g.B = y->proj_w; g.bias = y->proj_b; g.C = m->hidden; g.M = P; g.N = E; g.K = E;
         if (!rc) rc = g2i_launch(f_resid, cdivu(E, 64), cdivu(P, 64), 256, &g);
