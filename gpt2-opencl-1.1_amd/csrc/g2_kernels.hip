@@ -510,13 +510,15 @@ __device__ void hgemm_impl(const g2_gemm_args &a)
     const _Float16 *wrow = (const _Float16 *)a.B + (size_t)(n0 + r) * K + kq;
     const int fr = lane & 15, fk = 8 * (lane >> 4);
 
+    /* the next tile's global loads are issued before the current tile's
+     * matrix products, so they overlap */
+    f32x4 av[4];
+    h16x8 bv[2];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) av[q] = *(const f32x4 *)(ap + 4 * q);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) bv[q] = *(const h16x8 *)(wrow + 8 * q);
     for (int k0 = 0; k0 < K; k0 += BK) {
-        f32x4 av[4];
-        h16x8 bv[2];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) av[q] = *(const f32x4 *)(ap + k0 + 4 * q);
-#pragma unroll
-        for (int q = 0; q < 2; ++q) bv[q] = *(const h16x8 *)(wrow + k0 + 8 * q);
         h16x8 hi[2], lo[2];
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
@@ -533,6 +535,13 @@ __device__ void hgemm_impl(const g2_gemm_args &a)
             *(h16x8 *)(Bs + r * LD + kq + 8 * q) = bv[q];
         }
         __syncthreads();
+        {
+            const int kn = min(k0 + BK, K - BK); /* the last tile reloads itself */
+#pragma unroll
+            for (int q = 0; q < 4; ++q) av[q] = *(const f32x4 *)(ap + kn + 4 * q);
+#pragma unroll
+            for (int q = 0; q < 2; ++q) bv[q] = *(const h16x8 *)(wrow + kn + 8 * q);
+        }
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 32) {
             h16x8 afh[2], afl[2], bf[2];

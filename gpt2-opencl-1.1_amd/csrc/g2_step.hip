@@ -355,7 +355,8 @@ __device__ __forceinline__ void load_set(int tid, u32x4 (&w)[UM][4], const plan 
         const int c1 = min(p.C, c0 + p.SL);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int cc = min(c0 + lane + 64 * i, c1 - 1);
+            /* a unit past the share reads one chunk with every lane (one line) */
+            const int cc = uv ? min(c0 + lane + 64 * i, c1 - 1) : 0;
             w[j][i] = __builtin_nontemporal_load(gl(p.W) + (size_t)row * p.C + cc);
         }
     }
