@@ -58,7 +58,8 @@
     X(TRANSPOSE16, "g2k_transpose16")                                         \
     X(HGEMM_STORE, "g2k_hgemm_store") X(HGEMM_GELU, "g2k_hgemm_gelu")         \
     X(HGEMM_RESID, "g2k_hgemm_resid") X(HGEMM_QKV, "g2k_hgemm_qkv")           \
-    X(ATTN_PREFILL_MFMA, "g2k_attn_prefill_mfma")
+    X(ATTN_PREFILL_MFMA, "g2k_attn_prefill_mfma")                             \
+    X(HGEMM_PARTIAL, "g2k_hgemm_partial") X(SPLITK_RESID, "g2k_splitk_resid")
 
 #define G2_ENUM_ENTRY(id, name) G2F_##id,
 enum { G2_KERNEL_LIST(G2_ENUM_ENTRY) G2F_COUNT };
@@ -80,6 +81,9 @@ int g2i_hip(hipError_t e, const char *what);
 int g2i_ready(void);
 hipStream_t g2i_stream(void);
 int g2i_launch(int fid, unsigned gx, unsigned gy, unsigned bx, void *args);
+int g2i_launch3(int fid, unsigned gx, unsigned gy, unsigned gz, unsigned bx, void *args);
+/* largest K split of the fp16 prefill GEMM (its slice buffer holds this many) */
+#define G2_PF_MAXSPLIT 5
 /* Cooperative launch (all gx work-groups co-resident) of a 1-D grid. */
 int g2i_coop_launch(int fid, unsigned gx, unsigned bx, void *args);
 /* Work-groups of the persistent step kernel's grid (0: not supported). */

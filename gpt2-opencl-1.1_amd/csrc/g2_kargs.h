@@ -36,7 +36,10 @@ enum {
  * B layout G2_BNK: [N,K] row-major (packed, output-major).
  * Epilogues: store (C = acc + bias), gelu (C = gelu(acc + bias)),
  * resid (C = C + (acc + bias), in place), qkv (columns < E to q_out[M,E],
- * E..2E-1 to k_cache[(n-E)*S + pos0+m], 2E..3E-1 to v_cache[(pos0+m)*E + n-2E]). */
+ * E..2E-1 to k_cache[(n-E)*S + pos0+m], 2E..3E-1 to v_cache[(pos0+m)*E + n-2E]),
+ * partial (the fp16 split-K GEMM: K slice z of ksplit equal slices to
+ * part[z*M*N + m*N + n], no bias; g2k_splitk_resid adds the slices in
+ * order, the bias and the residual). */
 typedef struct {
     const float *A;
     const void *B;
@@ -47,7 +50,18 @@ typedef struct {
     float *v_cache;
     int M, N, K;
     int E, S, pos0;
+    float *part;
+    int ksplit;
 } g2_gemm_args;
+
+/* C[m,n] = C[m,n] + ((sum over z < ks in order of part[z*M*N + m*N + n]) +
+ * bias[n]) for m < M, n < N. */
+typedef struct {
+    const float *part;
+    const float *bias;
+    float *C;
+    int M, N, ks;
+} g2_skred_args;
 
 /* Reference-layout matvec, first pass: partial[split*N + n] = sum over the
  * split's contiguous k-range of A[k] B[k*N + n]; grid (column tiles, splits). */

@@ -348,7 +348,7 @@ extern "C" __global__ __launch_bounds__(1024) void g2k_attn_out(const g2_attnout
  * MFMA 16x16x4 f32 operand layout: lane l supplies A[l%16][l/16] and
  * B[l/16][l%16]; the result lane l holds rows 4*(l/16)+r, column l%16.
  * ==================================================================== */
-enum { GEPI_STORE = 0, GEPI_GELU = 1, GEPI_RESID = 2, GEPI_QKV = 3 };
+enum { GEPI_STORE = 0, GEPI_GELU = 1, GEPI_RESID = 2, GEPI_QKV = 3, GEPI_PARTIAL = 4 };
 
 template <typename BT, bool BNK, int EPI>
 __device__ void gemm_impl(const g2_gemm_args &a)
@@ -496,7 +496,10 @@ __device__ void hgemm_impl(const g2_gemm_args &a)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const int M = a.M, N = a.N, K = a.K;
+    const int M = a.M, N = a.N, Kfull = a.K;
+    /* split-K (GEPI_PARTIAL): this work-group's K slice */
+    const int K = EPI == GEPI_PARTIAL ? Kfull / a.ksplit : Kfull;
+    const int kz0 = EPI == GEPI_PARTIAL ? (int)blockIdx.z * K : 0;
     f32x4 acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -506,8 +509,8 @@ __device__ void hgemm_impl(const g2_gemm_args &a)
     /* staging: thread -> tile row r, 16 consecutive k from kq */
     const int r = tid >> 2, kq = (tid & 3) * 16;
     const bool arow = m0 + r < M;
-    const float *ap = a.A + (size_t)min(m0 + r, M - 1) * K + kq;
-    const _Float16 *wrow = (const _Float16 *)a.B + (size_t)(n0 + r) * K + kq;
+    const float *ap = a.A + (size_t)min(m0 + r, M - 1) * Kfull + kz0 + kq;
+    const _Float16 *wrow = (const _Float16 *)a.B + (size_t)(n0 + r) * Kfull + kz0 + kq;
     const int fr = lane & 15, fk = 8 * (lane >> 4);
 
     /* the next tile's global loads are issued before the current tile's
@@ -573,6 +576,10 @@ __device__ void hgemm_impl(const g2_gemm_args &a)
                 const int n = n0 + wn * 32 + j * 16 + (lane & 15);
                 if (m >= M || n >= N) continue;
                 float v = acc[i][j][q];
+                if (EPI == GEPI_PARTIAL) {
+                    a.part[(size_t)blockIdx.z * M * N + (size_t)m * N + n] = v;
+                    continue;
+                }
                 if (a.bias) v += a.bias[n];
                 if (EPI == GEPI_STORE) {
                     a.C[(size_t)m * N + n] = v;
@@ -587,6 +594,23 @@ __device__ void hgemm_impl(const g2_gemm_args &a)
                     else a.v_cache[(size_t)pos * E + (n - 2 * E)] = v;
                 }
             }
+}
+
+G2K void g2k_hgemm_partial(const g2_gemm_args a) { hgemm_impl<GEPI_PARTIAL>(a); }
+
+/* The split-K residual epilogue: slices summed in order, then + bias, then
+ * added to C (the order of the single-pass resid epilogue, with the dot
+ * product summed per slice). */
+G2K void g2k_splitk_resid(const g2_skred_args a)
+{
+    const size_t MN = (size_t)a.M * a.N;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < MN; i += (size_t)gridDim.x * 256) {
+        float v = a.part[i];
+        for (int z = 1; z < a.ks; ++z) v += a.part[(size_t)z * MN + i];
+        const int n = (int)(i % (size_t)a.N);
+        if (a.bias) v += a.bias[n];
+        a.C[i] = v + a.C[i];
+    }
 }
 
 G2K void g2k_hgemm_store(const g2_gemm_args a) { hgemm_impl<GEPI_STORE>(a); }

@@ -46,6 +46,7 @@ struct g2_model {
     /* workspaces (main.c:1451-1490) */
     float *hidden, *ln_out, *attn, *attn_proj, *ffn1, *ffn2, *qkv_new, *qkv_full;
     float *last_hidden, *logits, *partial, *scores, *q;
+    float *pf_part; /* split-K slices of the fp16 prefill GEMM */
     int *ids_dev;
     /* fused path */
     int *state;
@@ -322,6 +323,7 @@ static int alloc_workspaces(g2_model *m)
     A(m->attn_proj, S * E * 4); A(m->ffn1, S * F * 4); A(m->ffn2, S * E * 4);
     A(m->qkv_new, T * 4); A(m->qkv_full, S * T * 4); A(m->last_hidden, E * 4);
     A(m->logits, V * 4); A(m->ids_dev, S * 4); A(m->partial, 8 * V * 4);
+    if (m->path == G2_PATH_FUSED && m->dtype == G2_F16) A(m->pf_part, (size_t)G2_PF_MAXSPLIT * S * E * 4);
     A(m->scores, NH * S * 4); A(m->q, S * E * 4);
     A(m->state, G2S_WORDS * 4);
     A(m->att_part, NH * G2_ATTN_MAX_CHUNKS * 66 * 4);
@@ -374,7 +376,7 @@ int g2_model_free(g2_model *m)
     void *bufs[] = { m->wte, m->wpe, m->lnf_w, m->lnf_b, m->lm_head, m->hidden, m->ln_out,
                      m->attn, m->attn_proj, m->ffn1, m->ffn2, m->qkv_new, m->qkv_full,
                      m->last_hidden, m->logits, m->partial, m->scores, m->q, m->ids_dev,
-                     m->state, m->att_part, m->am_part, m->step_layers, m->xbuf, m->trace };
+                     m->state, m->att_part, m->am_part, m->step_layers, m->xbuf, m->trace, m->pf_part };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; ++i)
         if (bufs[i]) hipFree(bufs[i]);
     for (int l = 0; l < m->cfg.n_layer; ++l) {
@@ -917,6 +919,28 @@ static int set_state(g2_model *m, int pos, int tok, int min_new, int ngen)
     return up(m->state, h, sizeof h);
 }
 
+/* C += A . W^T + bias (the residual matmuls of the fp16 prefill: proj, fc2)
+ * as split-K slices when a single pass would leave the GPU under-filled. */
+static int prefill_resid(g2_model *m, const float *A, const void *W, const float *bias, float *C, int P, int N,
+                         int K)
+{
+    const unsigned gx = cdivu(N, 64), gy = cdivu(P, 64);
+    int ks = 1;
+    for (int k = G2_PF_MAXSPLIT; k > 1; --k)
+        if ((K / 64) % k == 0 && gx * gy * (unsigned)k <= 1024) { ks = k; break; }
+    if (gx * gy >= 512) ks = 1;
+    g2_gemm_args g;
+    memset(&g, 0, sizeof g);
+    g.A = A; g.B = W; g.bias = bias; g.C = C; g.M = P; g.N = N; g.K = K;
+    if (ks == 1) return g2i_launch(G2F_HGEMM_RESID, gx, gy, 256, &g);
+    g.part = m->pf_part; g.ksplit = ks;
+    int rc = g2i_launch3(G2F_HGEMM_PARTIAL, gx, gy, (unsigned)ks, 256, &g);
+    g2_skred_args r = { m->pf_part, bias, C, P, N, ks };
+    if (!rc) rc = g2i_launch(G2F_SPLITK_RESID, cdivu((unsigned)(P * N), 256) < 2048 ? cdivu((unsigned)(P * N), 256) : 2048,
+                             1, 256, &r);
+    return rc;
+}
+
 static int fused_prefill(g2_model *m, int P)
 {
     const int E = m->cfg.n_embd, F = m->cfg.ffn_dim, NH = m->cfg.n_head;
@@ -944,14 +968,16 @@ static int fused_prefill(g2_model *m, int P)
         if (!rc) rc = g2i_launch(G2F_ATTN_PREFILL_MFMA, (unsigned)NH, cdivu(P, 64), 256, &t);
         memset(&g, 0, sizeof g);
         g.A = m->attn; g.B = y->proj_w; g.bias = y->proj_b; g.C = m->hidden; g.M = P; g.N = E; g.K = E;
-        if (!rc) rc = g2i_launch(f_resid, cdivu(E, 64), cdivu(P, 64), 256, &g);
+        if (!rc) rc = h ? prefill_resid(m, m->attn, y->proj_w, y->proj_b, m->hidden, P, E, E)
+                        : g2i_launch(f_resid, cdivu(E, 64), cdivu(P, 64), 256, &g);
         if (!rc) rc = g2_layernorm(m->hidden, m->ln_out, y->ln2_w, y->ln2_b, E, P);
         memset(&g, 0, sizeof g);
         g.A = m->ln_out; g.B = y->fc_w; g.bias = y->fc_b; g.C = m->ffn1; g.M = P; g.N = F; g.K = E;
         if (!rc) rc = g2i_launch(f_gelu, cdivu(F, 64), cdivu(P, 64), 256, &g);
         memset(&g, 0, sizeof g);
         g.A = m->ffn1; g.B = y->fc2_w; g.bias = y->fc2_b; g.C = m->hidden; g.M = P; g.N = E; g.K = F;
-        if (!rc) rc = g2i_launch(f_resid, cdivu(E, 64), cdivu(P, 64), 256, &g);
+        if (!rc) rc = h ? prefill_resid(m, m->ffn1, y->fc2_w, y->fc2_b, m->hidden, P, E, F)
+                        : g2i_launch(f_resid, cdivu(E, 64), cdivu(P, 64), 256, &g);
     }
     if (!rc) rc = fused_lm_head(m, m->hidden + (size_t)(P - 1) * E, 1);
     return rc;

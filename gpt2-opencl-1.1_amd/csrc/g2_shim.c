@@ -75,6 +75,15 @@ int g2i_launch(int fid, unsigned gx, unsigned gy, unsigned bx, void *args)
                    g2_kernel_names[fid]);
 }
 
+int g2i_launch3(int fid, unsigned gx, unsigned gy, unsigned gz, unsigned bx, void *args)
+{
+    void *params[1] = { args };
+    if (gx == 0 || gy == 0 || gz == 0) return G2_OK;
+    return g2i_hip(hipModuleLaunchKernel(G.fn[fid], gx, gy, gz, bx, 1, 1, 0,
+                                         G.stream, params, NULL),
+                   g2_kernel_names[fid]);
+}
+
 int g2i_coop_launch(int fid, unsigned gx, unsigned bx, void *args)
 {
     void *params[1] = { args };
