@@ -93,10 +93,12 @@ __device__ __forceinline__ void xload_t(int tid, u32x4 (&w)[UM * CPL], const xpl
         const int c1 = min(p.C, c0 + p.SL);
 #pragma unroll
         for (int i = 0; i < CPL; ++i) {
-            const int cc = c0 + lane + 64 * i;
-            w[j * CPL + i] = (u32x4){0u, 0u, 0u, 0u};
-            if (uv && cc < c1)
-                w[j * CPL + i] = __builtin_nontemporal_load(gl(p.W) + (size_t)row * p.Crow + p.cbase + cc);
+            /* unconditional loads keep the compiler's waits exact; the chunk
+             * is clamped into the row, also for an empty slice (an XCD
+             * without heads has no proj columns: c1 = 0) */
+            const int cc = uv ? min(c0 + lane + 64 * i, c1 - 1) : 0;
+            const int ca = max(0, min(p.cbase + cc, p.Crow - 1));
+            w[j * CPL + i] = __builtin_nontemporal_load(gl(p.W) + (size_t)row * p.Crow + ca);
         }
     }
 }
@@ -261,7 +263,7 @@ __device__ __forceinline__ void stepx_impl(const g2_step_args &a)
             XTRACE(0);
             const xplan p = xmake<WT>(y.qkv_w, E, 0, E, 192 * nh, r, G, hb * 64, 64 * nh, E);
             const ln_params<NPE> lp = ln_load<NPE>(tid, gl(y.ln1_w), gl(y.ln1_b), E);
-            const float bias = tid < p.nrows && y.qkv_b ? gl(y.qkv_b)[xrow(p, tid)] : 0.f;
+            const float bias = gl(y.qkv_b)[xrow(p, min(tid, max(p.nrows - 1, 0)))];
             if (l > 0)
                 fetch<NPE>(tid, c, Xb + (size_t)(l - 1) * a.xlayer + (size_t)X * LW + G2XL_X2(HX, E, FX), E, G,
                            xres, (lds_flag *)&flag);
@@ -346,7 +348,7 @@ __device__ __forceinline__ void stepx_impl(const g2_step_args &a)
         /* ---- RED1: x' = (sum of partials + b) + x on this rank's rows */
         {
             const int tid = fresh_tid();
-            const float bias = tid < rnr && y.proj_b ? gl(y.proj_b)[rn0 + tid] : 0.f;
+            const float bias = gl(y.proj_b)[min(rn0 + tid, E - 1)];
             fetch_partials(tid, c, PP, E, rn0, rnr, xin);
             XTRACE(17);
             if (tid < rnr) {
@@ -363,7 +365,7 @@ __device__ __forceinline__ void stepx_impl(const g2_step_args &a)
             const int tid = fresh_tid();
             const xplan p = xmake<WT>(y.fc_w, E, 0, E, nf, r, G, fb, nf, 0);
             const ln_params<NPE> lp = ln_load<NPE>(tid, gl(y.ln2_w), gl(y.ln2_b), E);
-            const float bias = tid < p.nrows && y.fc_b ? gl(y.fc_b)[xrow(p, tid)] : 0.f;
+            const float bias = gl(y.fc_b)[xrow(p, min(tid, max(p.nrows - 1, 0)))];
             fetch<NPE>(tid, c, LR + G2XL_X1(HX), E, G, xres, (lds_flag *)&flag);
             XTRACE(7);
             layernorm(tid, xres, xin, lp, E, red);
@@ -395,7 +397,7 @@ __device__ __forceinline__ void stepx_impl(const g2_step_args &a)
         /* ---- RED2: x'' = (sum of partials + b) + x' */
         {
             const int tid = fresh_tid();
-            const float bias = tid < rnr && y.fc2_b ? gl(y.fc2_b)[rn0 + tid] : 0.f;
+            const float bias = gl(y.fc2_b)[min(rn0 + tid, E - 1)];
             fetch_partials(tid, c, P2, E, rn0, rnr, xin);
             XTRACE(18);
             if (tid < rnr) {
