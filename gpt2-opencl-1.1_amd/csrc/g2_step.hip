@@ -133,6 +133,26 @@ __device__ __forceinline__ float wmax(float v)
     return fmaxf(fmaxf(row_lane(v, 0), row_lane(v, 16)), fmaxf(row_lane(v, 32), row_lane(v, 48)));
 }
 
+/* Wave sums of four per-lane values at once (a transposed reduction):
+ * lanes 32-63 of a are swapped with lanes 0-31 of b, and of c with d
+ * (v_permlane32_swap), the pairs added; then odd rows of (a,b) with even
+ * rows of (c,d) (v_permlane16_swap), added; then each 16-lane row summed by
+ * rotations.  Returns, in every lane of row 0 / 1 / 2 / 3 (lanes 0-15,
+ * 16-31, 32-47, 48-63), the total of a / c / b / d. */
+__device__ __forceinline__ float wsum4(float a, float b, float c, float d)
+{
+    const auto s1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    const float ab = __uint_as_float(s1[0]) + __uint_as_float(s1[1]);
+    const auto s2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(d), false, false);
+    const float cd = __uint_as_float(s2[0]) + __uint_as_float(s2[1]);
+    const auto s3 = __builtin_amdgcn_permlane16_swap(__float_as_uint(ab), __float_as_uint(cd), false, false);
+    float v = __uint_as_float(s3[0]) + __uint_as_float(s3[1]);
+    v += dpp<0x128>(v); /* row_ror:8 */
+    v += dpp<0x124>(v); /* row_ror:4 */
+    v += dpp<0x122>(v); /* row_ror:2 */
+    return v + dpp<0x121>(v); /* row_ror:1 */
+}
+
 struct ctx {
     unsigned tag;
     u64 *abort_w;
@@ -260,44 +280,44 @@ __device__ __forceinline__ ln_params<NE> ln_load(int tid, const G2_GLOBAL float 
     return p;
 }
 
-/* Sum over the 512-thread work-group, wave totals added in wave order.
- * `red` must not be rewritten before every thread has read it (callers
- * alternate buffers). */
-__device__ __forceinline__ float blk_sum(int tid, float v, float *red)
-{
-    v = wsum(v);
-    if ((tid & 63) == 0) red[tid >> 6] = v;
-    __syncthreads();
-    float t = red[0];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) t += red[w];
-    return t;
-}
-
-/* xin = LayerNorm(x) over E entries (both in LDS): mean, then biased
- * variance of (x - mean), eps 1e-5, (x - mean) * inv_std * g + b
- * (layernorm, math.cl:283-311).  Ends with a barrier. */
+/* xin = LayerNorm(x) over E entries (both in LDS): (x - mean) * inv_std *
+ * g + b with the biased variance, eps 1e-5 (layernorm, math.cl:283-311).
+ * One block reduction: every thread sums d = x - x0 and d^2 over its
+ * entries, x0 = x[0] (a shift that keeps the variance E[d^2] - E[d]^2 free
+ * of cancellation when |mean| >> std); the two sums are reduced together,
+ * wave totals added in wave order.  Ends with a barrier. */
 template <int NE>
 __device__ __forceinline__ void layernorm(int tid, const float *x, float *xin, const ln_params<NE> &lp,
                                           int E, float *red)
 {
-    float s = 0.f;
-#pragma unroll
-    for (int k = 0; k < NE; ++k) {
-        const int i = tid + NT * k;
-        if (i < E) s += x[i];
-    }
-    const float mean = blk_sum(tid, s, red) / (float)E;
-    float q = 0.f;
+    const float x0 = x[0];
+    float s = 0.f, q = 0.f;
 #pragma unroll
     for (int k = 0; k < NE; ++k) {
         const int i = tid + NT * k;
         if (i < E) {
-            const float d = x[i] - mean;
+            const float d = x[i] - x0;
+            s += d;
             q = fmaf(d, d, q);
         }
     }
-    const float inv = 1.0f / sqrtf(blk_sum(tid, q, red + NW) / (float)E + 1e-5f);
+    s = wsum(s);
+    q = wsum(q);
+    if ((tid & 63) == 0) {
+        red[tid >> 6] = s;
+        red[NW + (tid >> 6)] = q;
+    }
+    __syncthreads();
+    float S = red[0], Q = red[NW];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) {
+        S += red[w];
+        Q += red[NW + w];
+    }
+    const float md = S / (float)E;
+    const float mean = x0 + md;
+    const float var = fmaxf(Q / (float)E - md * md, 0.f);
+    const float inv = 1.0f / sqrtf(var + 1e-5f);
 #pragma unroll
     for (int k = 0; k < NE; ++k) {
         const int i = tid + NT * k;
@@ -385,15 +405,33 @@ __device__ __forceinline__ void dot_set(int tid, const u32x4 (&w)[UM][4], const 
             xv[i][e] = v.x; xv[i][e + 1] = v.y; xv[i][e + 2] = v.z; xv[i][e + 3] = v.w;
         }
     }
+    if constexpr (UM == 4) {
+        /* the four units' sums in one transposed reduction: unit j's total
+         * lands in row (0, 2, 1, 3)[j] of the wave */
+        float acc[4];
 #pragma unroll
-    for (int j = 0; j < UM; ++j) {
-        const int u = batch * NW * UM + wave + NW * j;
-        if (u >= p.nunits) break; /* wave-uniform */
-        float acc = 0.f;
+        for (int j = 0; j < 4; ++j) {
+            acc[j] = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc += chunk_dot<WT>(w[j][i], xv[i]);
-        acc = wsum(acc);
-        if (lane == 0) part[u] = acc;
+            for (int i = 0; i < 4; ++i) acc[j] += chunk_dot<WT>(w[j][i], xv[i]);
+        }
+        const float v = wsum4(acc[0], acc[1], acc[2], acc[3]);
+        if ((lane & 15) == 0) {
+            const int j = (lane >> 4) == 0 ? 0 : ((lane >> 4) == 1 ? 2 : ((lane >> 4) == 2 ? 1 : 3));
+            const int u = batch * NW * UM + wave + NW * j;
+            if (u < p.nunits) part[u] = v;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < UM; ++j) {
+            const int u = batch * NW * UM + wave + NW * j;
+            if (u >= p.nunits) break; /* wave-uniform */
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc += chunk_dot<WT>(w[j][i], xv[i]);
+            acc = wsum(acc);
+            if (lane == 0) part[u] = acc;
+        }
     }
 }
 
