@@ -59,7 +59,10 @@
     X(HGEMM_STORE, "g2k_hgemm_store") X(HGEMM_GELU, "g2k_hgemm_gelu")         \
     X(HGEMM_RESID, "g2k_hgemm_resid") X(HGEMM_QKV, "g2k_hgemm_qkv")           \
     X(ATTN_PREFILL_MFMA, "g2k_attn_prefill_mfma")                             \
-    X(HGEMM_PARTIAL, "g2k_hgemm_partial") X(SPLITK_RESID, "g2k_splitk_resid")
+    X(HGEMM_PARTIAL, "g2k_hgemm_partial") X(SPLITK_RESID, "g2k_splitk_resid") \
+    X(HGEMM2_GELU, "g2k_hgemm2_gelu") X(HGEMM2_RESID, "g2k_hgemm2_resid")     \
+    X(HGEMM2_QKV, "g2k_hgemm2_qkv") X(HGEMM2_PARTIAL, "g2k_hgemm2_partial")   \
+    X(LAYERNORM_SPLIT, "g2k_layernorm_split")
 
 #define G2_ENUM_ENTRY(id, name) G2F_##id,
 enum { G2_KERNEL_LIST(G2_ENUM_ENTRY) G2F_COUNT };
@@ -88,6 +91,8 @@ int g2i_launch3(int fid, unsigned gx, unsigned gy, unsigned gz, unsigned bx, voi
 int g2i_coop_launch(int fid, unsigned gx, unsigned bx, void *args);
 /* Work-groups of the persistent step kernel's grid (0: not supported). */
 int g2i_step_wgs(void);
+/* compute units of the device (after g2_init) */
+int g2i_cus(void);
 /* 1 if the XCD-parallel step kernel may run: its occupancy fits and a probe
  * launch found work-group w on XCD w % G2_NXCD for every w of the grid. */
 int g2i_stepx_ok(void);

@@ -52,6 +52,11 @@ typedef struct {
     int E, S, pos0;
     float *part;
     int ksplit;
+    /* the 128x128 fp16 GEMM (g2k_hgemm2_*): A given as its fp16 halves
+     * Ah = fp16(a), Al = fp16(a - Ah), [M,K] each (A unused); epilogue
+     * gelu_split writes gelu(acc + bias) as halves to Ch, Cl [M,N] */
+    const uint16_t *Ah, *Al;
+    uint16_t *Ch, *Cl;
 } g2_gemm_args;
 
 /* C[m,n] = C[m,n] + ((sum over z < ks in order of part[z*M*N + m*N + n]) +
@@ -96,6 +101,16 @@ typedef struct {
     const float *beta;
     int E, rows;
 } g2_ln_args;
+
+/* LayerNorm whose rows are written as fp16 halves hi = fp16(y), lo =
+ * fp16(y - hi), [rows,E] each (the A operand of g2k_hgemm2_*). */
+typedef struct {
+    const float *x;
+    uint16_t *hi, *lo;
+    const float *gamma;
+    const float *beta;
+    int E, rows;
+} g2_lnsplit_args;
 
 typedef struct {
     float *a;
@@ -299,6 +314,9 @@ typedef struct {
     float *out;
     int P, E, NH, S;
     float scale;
+    /* non-NULL: the output is written as fp16 halves (see g2_lnsplit_args)
+     * to out_hi, out_lo [P,E] instead of to out */
+    uint16_t *out_hi, *out_lo;
 } g2_attnp_args;
 
 #endif /* G2_KARGS_H */

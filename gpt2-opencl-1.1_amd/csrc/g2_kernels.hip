@@ -205,15 +205,29 @@ G2K void g2k_reduce(const g2_reduce_args a)
     a.C[n] = s;
 }
 
+/* An fp32 value as the two fp16 halves the split-activation GEMMs take:
+ * hi = fp16(v), lo = fp16(v - hi), both round-to-nearest-even. */
+__device__ __forceinline__ void split_store(uint16_t *hi, uint16_t *lo, size_t i, float v)
+{
+    /* v is the rounded fp32 value (no fusing of the producer's last product
+     * into v - hi), exactly what a consumer splitting the stored fp32 sees */
+#pragma clang fp contract(off)
+    const _Float16 h = (_Float16)v;
+    const _Float16 l = (_Float16)(v - (float)h);
+    hi[i] = __builtin_bit_cast(uint16_t, h);
+    lo[i] = __builtin_bit_cast(uint16_t, l);
+}
+
 /* ---- layernorm (math.cl:283-311): one work-group per row, two-pass mean and
- * biased variance, eps 1e-5, out = (x-mean)*inv_std*gamma + beta. */
-G2K void g2k_layernorm(const g2_ln_args a)
+ * biased variance, eps 1e-5, out = (x-mean)*inv_std*gamma + beta.  SPLIT:
+ * the row is written as fp16 halves (g2_lnsplit_args), same arithmetic. */
+template <bool SPLIT, typename ARGS>
+__device__ void layernorm_impl(const ARGS &a)
 {
     __shared__ float red4[4];
     const int row = blockIdx.x;
     if (row >= a.rows) return;
     const float *x = a.x + (size_t)row * a.E;
-    float *o = a.out + (size_t)row * a.E;
     float s = 0.f;
     for (int i = threadIdx.x; i < a.E; i += 256) s += x[i];
     const float mean = block_sum(s, red4) / (float)a.E;
@@ -224,9 +238,15 @@ G2K void g2k_layernorm(const g2_ln_args a)
     }
     const float var = block_sum(q, red4) / (float)a.E;
     const float inv = 1.0f / sqrtf(var + 1e-5f);
-    for (int i = threadIdx.x; i < a.E; i += 256)
-        o[i] = fmaf((x[i] - mean) * inv, a.gamma[i], a.beta[i]);
+    for (int i = threadIdx.x; i < a.E; i += 256) {
+        const float y = fmaf((x[i] - mean) * inv, a.gamma[i], a.beta[i]);
+        if constexpr (SPLIT) split_store(a.hi, a.lo, (size_t)row * a.E + i, y);
+        else a.out[(size_t)row * a.E + i] = y;
+    }
 }
+
+G2K void g2k_layernorm(const g2_ln_args a) { layernorm_impl<false>(a); }
+G2K void g2k_layernorm_split(const g2_lnsplit_args a) { layernorm_impl<true>(a); }
 
 /* ---- add_inplace (math.cl:314-322) and gelu (math.cl:325-330) ---------- */
 G2K void g2k_add(const g2_ew_args a)
@@ -348,7 +368,7 @@ extern "C" __global__ __launch_bounds__(1024) void g2k_attn_out(const g2_attnout
  * MFMA 16x16x4 f32 operand layout: lane l supplies A[l%16][l/16] and
  * B[l/16][l%16]; the result lane l holds rows 4*(l/16)+r, column l%16.
  * ==================================================================== */
-enum { GEPI_STORE = 0, GEPI_GELU = 1, GEPI_RESID = 2, GEPI_QKV = 3, GEPI_PARTIAL = 4 };
+enum { GEPI_STORE = 0, GEPI_GELU = 1, GEPI_RESID = 2, GEPI_QKV = 3, GEPI_PARTIAL = 4, GEPI_GELU_SPLIT = 5 };
 
 template <typename BT, bool BNK, int EPI>
 __device__ void gemm_impl(const g2_gemm_args &a)
@@ -613,6 +633,166 @@ G2K void g2k_splitk_resid(const g2_skred_args a)
     }
 }
 
+/* ======================================================================
+ * The same GEMM for prompts of more than 64 rows, on 128x128 tiles:
+ * 16 waves in 4x4, each 32x32 = 2x2 blocks of v_mfma_f32_16x16x32_f16
+ * with the fragment layout above, K in steps of 64.  The activations
+ * arrive already split into their fp16 halves (Ah, Al: written so by the
+ * producing LayerNorm, attention or GELU epilogue), so a step's three
+ * tiles (a_hi, a_lo, weights; 128 rows x 128 B each) are plain fp16.
+ *
+ * The tiles go from global memory straight into LDS (global_load_lds_
+ * dwordx4: lane l of an instruction writes 16 bytes at LDS base + 16 l),
+ * three steps in a ring, issued two steps ahead; a step waits for its own
+ * loads only (vmcnt(3): the 3 loads per wave of the step after it may
+ * still be in flight), then one barrier.  The tile needs the 144 KB of LDS
+ * of a CU, so the work-group is as wide as a work-group can be: the rate
+ * at which one CU streams its tiles grew with the number of waves issuing
+ * them (4, 8, 16 waves: 11.5, 10.0, 9.1 ms for the 512-token XL prefill).
+ * Rows are XOR-swizzled in 16-byte chunks (chunk c of row r at slot c ^
+ * (r / 2 % 8)) so the 16 rows of a fragment read fall on distinct banks.
+ * Per 32-k half a wave issues its 4 a_hi products, then its 4 a_lo
+ * products, which is the order of hgemm_impl for every output element.
+ * Requires N % 64 == 0 and K % 64 == 0 (per split-K slice); rows >= M and
+ * columns >= N are computed from clamped reads and not stored.
+ * ==================================================================== */
+namespace hg2 {
+constexpr int BM = 128, BN = 128, BK = 64, NS = 3;
+constexpr int TB = BM * BK * 2;  /* bytes of one 128 x 64 fp16 tile */
+constexpr int STAGE = 3 * TB;    /* a_hi, a_lo, weights: 48 KB */
+typedef __attribute__((address_space(3))) void lds_t;
+
+/* Wait until this wave's loads of the current step have landed (those of
+ * the next step, 3 per wave, may remain), then wait for every wave. */
+__device__ __forceinline__ void step_barrier() { asm volatile("s_waitcnt vmcnt(3)\n\ts_barrier" ::: "memory"); }
+
+/* The wave's products of one step from the stage at st. */
+__device__ __forceinline__ void mma(f32x4 (&acc)[2][2], const unsigned char *st, int wm, int wn, int lane)
+{
+    const int fr = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += 32) {
+        h16x8 afh[2], afl[2], bf[2];
+        const int slot = (((kk + 8 * g) >> 3) ^ (fr >> 1)) << 4;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const unsigned char *row = st + (wm * 32 + i * 16 + fr) * 128 + slot;
+            afh[i] = *(const h16x8 *)row;
+            afl[i] = *(const h16x8 *)(row + TB);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) bf[j] = *(const h16x8 *)(st + 2 * TB + (wn * 32 + j * 16 + fr) * 128 + slot);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afh[i], bf[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afl[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+}
+} /* namespace hg2 */
+
+template <int EPI>
+__device__ void hgemm2_impl(const g2_gemm_args &a)
+{
+    using namespace hg2;
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[NS * STAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2, wn = wave & 3; /* 4 x 4 waves of 32 x 32 */
+    const int M = a.M, N = a.N, Kfull = a.K;
+    /* Tile of this work-group.  The grid is 1-D per K slice: work-group w
+     * runs on XCD w % 8 (consecutive work-groups go to consecutive XCDs),
+     * so w -> (column block 8 (s / nmb) + w % 8, row block s % nmb), s =
+     * w / 8, puts all row blocks of a column block on one XCD, whose L2
+     * then fetches that weight block once.  Column blocks past the last
+     * (the grid is padded to a multiple of 8) have no work. */
+    const int nmb = (M + BM - 1) / BM, nnb = (N + BN - 1) / BN;
+    const int sw = (int)blockIdx.x >> 3;
+    const int nb = 8 * (sw / nmb) + ((int)blockIdx.x & 7), mb = sw % nmb;
+    if (nb >= nnb) return;
+    const int m0 = mb * BM, n0 = nb * BN;
+    /* split-K (GEPI_PARTIAL): this work-group's K slice, steps [s0, s1) of
+     * the Kfull / 64 (slices differ by at most one step) */
+    const int nkt = Kfull / BK;
+    const int s0 = EPI == GEPI_PARTIAL ? (int)(((long)nkt * blockIdx.z) / a.ksplit) : 0;
+    const int s1 = EPI == GEPI_PARTIAL ? (int)(((long)nkt * (blockIdx.z + 1)) / a.ksplit) : nkt;
+    const int kz0 = s0 * BK, nk = s1 - s0;
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+
+    /* this lane's load sources: wave w fills rows 8w..8w+7 of each tile
+     * with one instruction (lane -> row l/8, slot l%8); each slot holds the
+     * chunk that the swizzle puts there */
+    const int row = 8 * wave + (lane >> 3);
+    const int ch = (lane & 7) ^ ((row >> 1) & 7);
+    const size_t ao = (size_t)min(m0 + row, M - 1) * Kfull + kz0 + 8 * ch;
+    const _Float16 *hsrc = (const _Float16 *)a.Ah + ao, *lsrc = (const _Float16 *)a.Al + ao;
+    const _Float16 *bsrc = (const _Float16 *)a.B + (size_t)min(n0 + row, N - 1) * Kfull + kz0 + 8 * ch;
+    /* step t's loads into stage buffer b (steps past the last reload it) */
+    auto issue = [&](int t, int b) {
+        const int k = min(t, nk - 1) * BK;
+        unsigned char *st = lds + b * STAGE + (8 * wave) * 128;
+        __builtin_amdgcn_global_load_lds(hsrc + k, (lds_t *)st, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(lsrc + k, (lds_t *)(st + TB), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(bsrc + k, (lds_t *)(st + 2 * TB), 16, 0, 0);
+    };
+
+    issue(0, 0);
+    issue(1, 1);
+    int cur = 0;
+    for (int t = 0; t < nk; ++t) {
+        step_barrier(); /* step t has landed; the buffer of step t-1 is free */
+        const int nb2 = cur == 0 ? 2 : cur - 1;
+        issue(t + 2, nb2);
+        mma(acc, lds + cur * STAGE, wm, wn, lane);
+        cur = cur == 2 ? 0 : cur + 1;
+    }
+    /* no load may land in LDS after the work-group has ended */
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + q;
+                const int n = n0 + wn * 32 + j * 16 + (lane & 15);
+                if (m >= M || n >= N) continue;
+                float v = acc[i][j][q];
+                if (EPI == GEPI_PARTIAL) {
+                    a.part[(size_t)blockIdx.z * M * N + (size_t)m * N + n] = v;
+                    continue;
+                }
+                if (a.bias) v += a.bias[n];
+                if (EPI == GEPI_GELU_SPLIT) {
+                    split_store(a.Ch, a.Cl, (size_t)m * N + n, gelu_f(v));
+                } else if (EPI == GEPI_RESID) {
+                    a.C[(size_t)m * N + n] = v + a.C[(size_t)m * N + n];
+                } else {
+                    const int E = a.E, pos = a.pos0 + m;
+                    if (n < E) a.q_out[(size_t)m * E + n] = v;
+                    else if (n < 2 * E) a.k_cache[(size_t)(n - E) * a.S + pos] = v;
+                    else a.v_cache[(size_t)pos * E + (n - 2 * E)] = v;
+                }
+            }
+}
+
+/* one work-group of 16 waves per CU (144 KB of LDS), 4 waves per SIMD */
+#define G2K_HG2 extern "C" __global__ __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(4, 4)))
+G2K_HG2 void g2k_hgemm2_gelu(const g2_gemm_args a) { hgemm2_impl<GEPI_GELU_SPLIT>(a); }
+G2K_HG2 void g2k_hgemm2_resid(const g2_gemm_args a) { hgemm2_impl<GEPI_RESID>(a); }
+G2K_HG2 void g2k_hgemm2_qkv(const g2_gemm_args a) { hgemm2_impl<GEPI_QKV>(a); }
+G2K_HG2 void g2k_hgemm2_partial(const g2_gemm_args a) { hgemm2_impl<GEPI_PARTIAL>(a); }
+
 G2K void g2k_hgemm_store(const g2_gemm_args a) { hgemm_impl<GEPI_STORE>(a); }
 G2K void g2k_hgemm_gelu(const g2_gemm_args a) { hgemm_impl<GEPI_GELU>(a); }
 G2K void g2k_hgemm_resid(const g2_gemm_args a) { hgemm_impl<GEPI_RESID>(a); }
@@ -840,7 +1020,11 @@ G2K void g2k_attn_prefill_mfma(const g2_attnp_args a)
         if (i >= P) continue;
         const float inv = 1.0f / l[r];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) a.out[(size_t)i * E + h * 64 + 16 * t + lr] = o[t][r] * inv;
+        for (int t = 0; t < 4; ++t) {
+            const size_t idx = (size_t)i * E + h * 64 + 16 * t + lr;
+            if (a.out_hi) split_store(a.out_hi, a.out_lo, idx, o[t][r] * inv);
+            else a.out[idx] = o[t][r] * inv;
+        }
     }
 }
 

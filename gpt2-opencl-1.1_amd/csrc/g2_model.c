@@ -920,21 +920,34 @@ static int set_state(g2_model *m, int pos, int tok, int min_new, int ngen)
 }
 
 /* C += A . W^T + bias (the residual matmuls of the fp16 prefill: proj, fc2)
- * as split-K slices when a single pass would leave the GPU under-filled. */
-static int prefill_resid(g2_model *m, const float *A, const void *W, const float *bias, float *C, int P, int N,
-                         int K)
+ * as split-K slices when a single pass would leave the GPU under-filled.
+ * big: the 128x128 kernel, which takes A as its fp16 halves Ah, Al and
+ * whose work-groups (one per CU) should all run at once: its slice count
+ * is the largest that keeps tiles x slices within the CU count; it splits
+ * the K steps into slices that differ by at most one step. */
+static int prefill_resid(g2_model *m, const float *A, const uint16_t *Ah, const uint16_t *Al, const void *W,
+                         const float *bias, float *C, int P, int N, int K, int big)
 {
     const unsigned gx = cdivu(N, 64), gy = cdivu(P, 64);
     int ks = 1;
     for (int k = G2_PF_MAXSPLIT; k > 1; --k)
         if ((K / 64) % k == 0 && gx * gy * (unsigned)k <= 1024) { ks = k; break; }
     if (gx * gy >= 512) ks = 1;
+    if (big) {
+        const unsigned tiles = cdivu(N, 128) * cdivu(P, 128), cus = (unsigned)g2i_cus();
+        ks = 1;
+        for (int k = G2_PF_MAXSPLIT; k > 1; --k)
+            if (tiles * (unsigned)k <= cus && k <= K / 64) { ks = k; break; }
+    }
+    /* the 128x128 kernel: a 1-D grid of 8 * ceil(column blocks / 8) * row blocks */
+    const unsigned bx = big ? 8 * cdivu(cdivu(N, 128), 8) * cdivu(P, 128) : gx, by = big ? 1 : gy;
     g2_gemm_args g;
     memset(&g, 0, sizeof g);
     g.A = A; g.B = W; g.bias = bias; g.C = C; g.M = P; g.N = N; g.K = K;
-    if (ks == 1) return g2i_launch(G2F_HGEMM_RESID, gx, gy, 256, &g);
+    g.Ah = Ah; g.Al = Al;
+    if (ks == 1) return g2i_launch(big ? G2F_HGEMM2_RESID : G2F_HGEMM_RESID, bx, by, big ? 1024 : 256, &g);
     g.part = m->pf_part; g.ksplit = ks;
-    int rc = g2i_launch3(G2F_HGEMM_PARTIAL, gx, gy, (unsigned)ks, 256, &g);
+    int rc = g2i_launch3(big ? G2F_HGEMM2_PARTIAL : G2F_HGEMM_PARTIAL, bx, by, (unsigned)ks, big ? 1024 : 256, &g);
     g2_skred_args r = { m->pf_part, bias, C, P, N, ks };
     if (!rc) rc = g2i_launch(G2F_SPLITK_RESID, cdivu((unsigned)(P * N), 256) < 2048 ? cdivu((unsigned)(P * N), 256) : 2048,
                              1, 256, &r);
@@ -950,33 +963,52 @@ static int fused_prefill(g2_model *m, int P)
      * fp32-MFMA GEMM for comparison */
     const char *pe = getenv("G2_PREFILL_F32MFMA");
     const int h = f16 && E % 64 == 0 && F % 64 == 0 && !(pe && pe[0] == '1');
-    const int f_qkv = h ? G2F_HGEMM_QKV : (f16 ? G2F_GEMM_NK_F16_QKV : G2F_GEMM_NK_F32_QKV);
+    /* prompts of more than 64 rows: the 128x128 tiles (G2_PREFILL_GEMM64=1
+     * keeps the 64x64 ones, whose results are identical) */
+    const char *p64 = getenv("G2_PREFILL_GEMM64");
+    const int big = h && P > 64 && !(p64 && p64[0] == '1');
+    const int f_qkv = big ? G2F_HGEMM2_QKV : h ? G2F_HGEMM_QKV : (f16 ? G2F_GEMM_NK_F16_QKV : G2F_GEMM_NK_F32_QKV);
     const int f_resid = h ? G2F_HGEMM_RESID : (f16 ? G2F_GEMM_NK_F16_RESID : G2F_GEMM_NK_F32_RESID);
-    const int f_gelu = h ? G2F_HGEMM_GELU : (f16 ? G2F_GEMM_NK_F16_GELU : G2F_GEMM_NK_F32_GELU);
+    const int f_gelu = big ? G2F_HGEMM2_GELU : h ? G2F_HGEMM_GELU : (f16 ? G2F_GEMM_NK_F16_GELU : G2F_GEMM_NK_F32_GELU);
+    /* the 128x128 GEMMs take their activations as fp16 halves, written by
+     * the producers into the fp32 buffers' memory: hi in the first half, lo
+     * in the second, each [G2_KV_MAX_SEQ rows][width] */
+    const size_t cap = G2_KV_MAX_SEQ;
+    uint16_t *ln_h = (uint16_t *)m->ln_out, *ln_l = ln_h + cap * E;
+    uint16_t *at_h = (uint16_t *)m->attn, *at_l = at_h + cap * E;
+    uint16_t *ff_h = (uint16_t *)m->ffn1, *ff_l = ff_h + cap * F;
     g2_embed_args e = { m->wte, m->wpe, m->hidden, m->ids_dev, NULL, E, P, 0 };
     int rc = g2i_launch(f16 ? G2F_EMBED_F16 : G2F_EMBED_F32, cdivu(E, 256), (unsigned)P, 256, &e);
     for (int l = 0; l < m->cfg.n_layer && !rc; ++l) {
         g2_layer *y = &m->L[l];
-        rc = g2_layernorm(m->hidden, m->ln_out, y->ln1_w, y->ln1_b, E, P);
+        g2_lnsplit_args ls = { m->hidden, ln_h, ln_l, y->ln1_w, y->ln1_b, E, P };
+        rc = big ? g2i_launch(G2F_LAYERNORM_SPLIT, (unsigned)P, 1, 256, &ls)
+                 : g2_layernorm(m->hidden, m->ln_out, y->ln1_w, y->ln1_b, E, P);
         g2_gemm_args g;
         memset(&g, 0, sizeof g);
-        g.A = m->ln_out; g.B = y->qkv_w; g.bias = y->qkv_b; g.q_out = m->q;
+        g.A = m->ln_out; g.Ah = ln_h; g.Al = ln_l; g.B = y->qkv_w; g.bias = y->qkv_b; g.q_out = m->q;
         g.k_cache = y->k_cache; g.v_cache = y->v_cache; g.M = P; g.N = 3 * E; g.K = E;
         g.E = E; g.S = G2_KV_MAX_SEQ; g.pos0 = 0;
-        if (!rc) rc = g2i_launch(f_qkv, cdivu(3 * E, 64), cdivu(P, 64), 256, &g);
-        g2_attnp_args t = { m->q, y->k_cache, y->v_cache, m->attn, P, E, NH, G2_KV_MAX_SEQ, 1.0f / sqrtf(64.0f) };
+        if (!rc) rc = big ? g2i_launch(f_qkv, 8 * cdivu(cdivu(3 * E, 128), 8) * cdivu(P, 128), 1, 1024, &g)
+                          : g2i_launch(f_qkv, cdivu(3 * E, 64), cdivu(P, 64), 256, &g);
+        g2_attnp_args t = { m->q, y->k_cache, y->v_cache, m->attn, P, E, NH, G2_KV_MAX_SEQ, 1.0f / sqrtf(64.0f),
+                            big ? at_h : NULL, big ? at_l : NULL };
         if (!rc) rc = g2i_launch(G2F_ATTN_PREFILL_MFMA, (unsigned)NH, cdivu(P, 64), 256, &t);
         memset(&g, 0, sizeof g);
         g.A = m->attn; g.B = y->proj_w; g.bias = y->proj_b; g.C = m->hidden; g.M = P; g.N = E; g.K = E;
-        if (!rc) rc = h ? prefill_resid(m, m->attn, y->proj_w, y->proj_b, m->hidden, P, E, E)
+        if (!rc) rc = h ? prefill_resid(m, m->attn, at_h, at_l, y->proj_w, y->proj_b, m->hidden, P, E, E, big)
                         : g2i_launch(f_resid, cdivu(E, 64), cdivu(P, 64), 256, &g);
-        if (!rc) rc = g2_layernorm(m->hidden, m->ln_out, y->ln2_w, y->ln2_b, E, P);
+        g2_lnsplit_args ls2 = { m->hidden, ln_h, ln_l, y->ln2_w, y->ln2_b, E, P };
+        if (!rc) rc = big ? g2i_launch(G2F_LAYERNORM_SPLIT, (unsigned)P, 1, 256, &ls2)
+                          : g2_layernorm(m->hidden, m->ln_out, y->ln2_w, y->ln2_b, E, P);
         memset(&g, 0, sizeof g);
         g.A = m->ln_out; g.B = y->fc_w; g.bias = y->fc_b; g.C = m->ffn1; g.M = P; g.N = F; g.K = E;
-        if (!rc) rc = g2i_launch(f_gelu, cdivu(F, 64), cdivu(P, 64), 256, &g);
+        g.Ah = ln_h; g.Al = ln_l; g.Ch = ff_h; g.Cl = ff_l;
+        if (!rc) rc = big ? g2i_launch(f_gelu, 8 * cdivu(cdivu(F, 128), 8) * cdivu(P, 128), 1, 1024, &g)
+                          : g2i_launch(f_gelu, cdivu(F, 64), cdivu(P, 64), 256, &g);
         memset(&g, 0, sizeof g);
         g.A = m->ffn1; g.B = y->fc2_w; g.bias = y->fc2_b; g.C = m->hidden; g.M = P; g.N = E; g.K = F;
-        if (!rc) rc = h ? prefill_resid(m, m->ffn1, y->fc2_w, y->fc2_b, m->hidden, P, E, F)
+        if (!rc) rc = h ? prefill_resid(m, m->ffn1, ff_h, ff_l, y->fc2_w, y->fc2_b, m->hidden, P, E, F, big)
                         : g2i_launch(f_resid, cdivu(E, 64), cdivu(P, 64), 256, &g);
     }
     if (!rc) rc = fused_lm_head(m, m->hidden + (size_t)(P - 1) * E, 1);

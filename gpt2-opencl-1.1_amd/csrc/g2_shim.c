@@ -92,6 +92,7 @@ int g2i_coop_launch(int fid, unsigned gx, unsigned bx, void *args)
 }
 
 int g2i_step_wgs(void) { return G.step_wgs; }
+int g2i_cus(void) { return G.cus > 0 ? G.cus : 1; }
 int g2i_stepx_ok(void) { return G.stepx_ok; }
 int g2i_step3_ok(void) { return G.step3_ok; }
 

@@ -41,3 +41,25 @@ def test_prefill_split_fp16_mfma(g2, monkeypatch, P):
     np.testing.assert_allclose(lg_h, lg_f, rtol=1e-3, atol=2e-3)
     assert int(np.argmax(lg_h)) == int(np.argmax(ref)) or \
         np.sort(ref)[-1] - np.sort(ref)[-2] < 1e-2
+
+
+@pytest.mark.parametrize("P", [65, 200, 512, 1023])
+def test_prefill_gemm_tiles_agree(g2, monkeypatch, P):
+    """Prompts of more than 64 rows run the 128x128-tile GEMM (operands
+    staged through LDS by asynchronous loads, activations split into their
+    fp16 halves by the kernels that produce them); it sums every output in
+    the order of the 64x64-tile GEMM (G2_PREFILL_GEMM64=1), which splits
+    the stored fp32 activations itself.  The logits agree to fp32 rounding
+    (1e-5; 1.3e-6 measured at P 65)."""
+    cfg = g2.make_config(2, 1600, 25, vocab_size=50257)
+    w = g2.synth_weights(cfg, SEED, f16_round=True)
+    prompt = random_prompt(P, cfg.vocab_size, 200 + P)
+    print(f"[prefill] XL width L2, P {P}: 128x128 vs 64x64 tiles", flush=True)
+    out = []
+    for v in ("0", "1"):
+        monkeypatch.setenv("G2_PREFILL_GEMM64", v)
+        m = g2.Model.from_host(cfg, w, g2.F16, g2.PATH_FUSED)
+        m.prefill(prompt)
+        out.append(m.logits().copy())
+        m.free()
+    np.testing.assert_allclose(out[0], out[1], rtol=1e-5, atol=1e-5)
