@@ -885,8 +885,12 @@ G2K void g2k_attn_prefill(const g2_attnp_args a)
 }
 
 /* The same attention on the fp32 matrix cores (v_mfma_f32_16x16x4f32):
- * grid (NH, ceil(P/64)), 256 threads; wave w owns query rows 16w..16w+15
- * of the block.  Per 64-key block: S = Q K^T (4 tiles of 16 keys, 16 k
+ * grid (NH, ceil(P/64)), 512 threads; waves w and w + 4 own query rows
+ * 16w..16w+15 of the block, the first over the even key blocks, the
+ * second over the odd ones, each with its own online softmax, combined at
+ * the end (the kernel lasts as long as its longest rows, whose key blocks
+ * are thus shared by two waves).  Per 64-key block: S = Q K^T (4 tiles of
+ * 16 keys, 16 k
  * steps of 4 dims), scaled and causally masked, online softmax over the
  * block (row statistics reduced across the 16 lanes of a row group), P
  * re-laid through LDS into the operand layout, O += P V (4 tiles of 16
@@ -914,20 +918,31 @@ __device__ __forceinline__ float row16_sum(float v)
     return v + apf_dpp<0x121>(v);
 }
 
-G2K void g2k_attn_prefill_mfma(const g2_attnp_args a)
+extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_mfma(const g2_attnp_args a)
 {
-    constexpr int LD = 68;
-    __shared__ __attribute__((aligned(16))) float Kt[64 * LD]; /* [dim][key] */
-    __shared__ __attribute__((aligned(16))) float Vs[64 * LD]; /* [key][dim] */
-    __shared__ float Ps[4][16 * LD];                            /* per wave [row][key] */
+    /* The tiles are stored so that a lane's operands of all four 16-wide
+     * tiles are 16 contiguous bytes (one ds_read_b128 for 4 products):
+     * Kt[d][pk(k)] and Vs[k][pk(d)] with pk(c) = 4 (c % 16) + c / 16 (the
+     * column 16 t + l of tile t at 4 l + t), and each wave's P as
+     * [row][pp(k)], pp(k) = 16 (k % 4) + k / 4 (its 16 values of a k-step
+     * group contiguous).  Row pitches of 68 floats spread the staging
+     * writes over the banks. */
+    constexpr int LD = 68, LDP = 68;
+    __shared__ __attribute__((aligned(16))) float Kt[2][64 * LD]; /* per half [dim][pk(key)] */
+    __shared__ __attribute__((aligned(16))) float Vs[2][64 * LD]; /* per half [key][pk(dim)] */
+    __shared__ __attribute__((aligned(16))) float Ps[8][16 * LDP]; /* per wave [row][pp(key)] */
     const int h = blockIdx.x, qb = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
+    /* wave w: row group rg = w % 4 (query rows 16 rg..16 rg + 15 of the
+     * block) over the key blocks of its half hs = w / 4 (kb = hs, hs + 2,
+     * ...), so the blocks of the longest rows are shared by two waves */
+    const int rg = wave & 3, hs = wave >> 2;
     if (h >= a.NH || qb * 64 >= a.P) return;
     const int E = a.E, P = a.P;
-    /* Q operand: lane holds Q[row 16w + lr][dim 4s + lg], s < 16 */
+    /* Q operand: lane holds Q[row 16 rg + lr][dim 4s + lg], s < 16 */
     float qa[16];
     {
-        const int i = min(qb * 64 + 16 * wave + lr, P - 1);
+        const int i = min(qb * 64 + 16 * rg + lr, P - 1);
         const float *qp = a.q + (size_t)i * E + h * 64 + lg;
 #pragma unroll
         for (int st = 0; st < 16; ++st) qa[st] = qp[4 * st];
@@ -938,37 +953,51 @@ G2K void g2k_attn_prefill_mfma(const g2_attnp_args a)
     float m[4], l[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) { m[r] = -INFINITY; l[r] = 0.f; }
-    const int i_base = qb * 64 + 16 * wave + 4 * lg; /* query row of result r: i_base + r */
-    const int sr = tid >> 2, sq = (tid & 3) * 16;    /* staging: row, 16 columns */
-    for (int kb = 0; kb <= qb; ++kb) {
-        const int j0 = kb * 64;
-        f32x4 kv[4], vv[4];
-        {
-            const float *kp = a.k_cache + (size_t)(h * 64 + sr) * a.S + min(j0 + sq, a.S - 16);
-            const float *vp = a.v_cache + (size_t)min(j0 + sr, a.S - 1) * E + h * 64 + sq;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                kv[q] = *(const f32x4 *)(kp + 4 * q);
-                vv[q] = *(const f32x4 *)(vp + 4 * q);
-            }
-        }
-        __syncthreads(); /* the previous block has been consumed */
+    const int i_base = qb * 64 + 16 * rg + 4 * lg;      /* query row of result r: i_base + r */
+    const int sr = (tid & 255) >> 2, sq = (tid & 3) * 16; /* staging (per half): row, 16 columns */
+    /* key block kb's staging loads (kb clamped to the last block: the loads
+     * stay unconditional, see load_set in the step kernel) */
+    f32x4 kv[4], vv[4];
+    auto kvload = [&](int kb) {
+        const int jb = min(kb, qb) * 64;
+        const float *kp = a.k_cache + (size_t)(h * 64 + sr) * a.S + min(jb + sq, a.S - 16);
+        const float *vp = a.v_cache + (size_t)min(jb + sr, a.S - 1) * E + h * 64 + sq;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            *(f32x4 *)(Kt + sr * LD + sq + 4 * q) = kv[q];
-            *(f32x4 *)(Vs + sr * LD + sq + 4 * q) = vv[q];
+            kv[q] = *(const f32x4 *)(kp + 4 * q);
+            vv[q] = *(const f32x4 *)(vp + 4 * q);
         }
+    };
+    kvload(hs);
+    const int nit = (qb + 2) >> 1; /* block pairs */
+    for (int it = 0; it < nit; ++it) {
+        const int kb = 2 * it + hs, j0 = kb * 64;
+        __syncthreads(); /* the previous blocks have been consumed */
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int c = sq + 4 * q + e, pc = 4 * (c & 15) + (c >> 4);
+                Kt[hs][sr * LD + pc] = kv[q][e];
+                Vs[hs][sr * LD + pc] = vv[q][e];
+            }
         __syncthreads();
-        /* S = Q K^T: tile t covers keys 16t..16t+15 */
+        kvload(kb + 2); /* the next block streams in during this one's products */
+        if (kb > qb) continue; /* the odd half of an odd block count (wave-uniform) */
+        const float *Kb = Kt[hs], *Vb = Vs[hs];
+        /* S = Q K^T: tile t covers keys 16t..16t+15; the four tiles'
+         * product chains interleave (no product waits for the one before) */
         f32x4 sacc[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            sacc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < 4; ++t) sacc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        f32x4 kb4[16];
 #pragma unroll
-            for (int st = 0; st < 16; ++st)
-                sacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[st], Kt[(4 * st + lg) * LD + 16 * t + lr], sacc[t],
-                                                                0, 0, 0);
-        }
+        for (int st = 0; st < 16; ++st) kb4[st] = *(const f32x4 *)(Kb + (4 * st + lg) * LD + 4 * lr);
+#pragma unroll
+        for (int st = 0; st < 16; ++st)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                sacc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[st], kb4[st][t], sacc[t], 0, 0, 0);
         /* scale, causal mask, online softmax per row */
         float alpha[4];
 #pragma unroll
@@ -1001,18 +1030,51 @@ G2K void g2k_attn_prefill_mfma(const g2_attnp_args a)
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) pw[(4 * lg + r) * LD + 16 * t + lr] = sacc[t][r];
+            for (int r = 0; r < 4; ++r) {
+                const int k = 16 * t + lr;
+                pw[(4 * lg + r) * LDP + 16 * (k & 3) + (k >> 2)] = sacc[t][r];
+            }
         __builtin_amdgcn_wave_barrier();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int r = 0; r < 4; ++r) o[t][r] *= alpha[r];
+        f32x4 pa4[4], vb4[16];
 #pragma unroll
-            for (int st = 0; st < 16; ++st)
-                o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(pw[lr * LD + 4 * st + lg], Vs[(4 * st + lg) * LD + 16 * t + lr],
-                                                             o[t], 0, 0, 0);
+        for (int q = 0; q < 4; ++q) pa4[q] = *(const f32x4 *)(pw + lr * LDP + 16 * lg + 4 * q);
+#pragma unroll
+        for (int st = 0; st < 16; ++st) vb4[st] = *(const f32x4 *)(Vb + (4 * st + lg) * LD + 4 * lr);
+#pragma unroll
+        for (int st = 0; st < 16; ++st)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa4[st >> 2][st & 3], vb4[st][t], o[t], 0, 0, 0);
+    }
+    /* combine the halves: the odd half's (max, sum, o) through LDS (the
+     * staging tiles are free), scaled to the common max */
+    __syncthreads();
+    float *xw = Kt[0] + (size_t)(rg * 64 + lane) * 24; /* 4 waves x 64 lanes x 24 floats <= 2 tiles */
+    if (hs == 1) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            xw[r] = m[r];
+            xw[4 + r] = l[r];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xw[8 + 4 * t + r] = o[t][r];
         }
+    }
+    __syncthreads();
+    if (hs == 1) return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float m1 = xw[r], l1 = xw[4 + r];
+        const float mx = fmaxf(m[r], m1);
+        const float f0 = m[r] == -INFINITY ? 0.f : expf(m[r] - mx);
+        const float f1 = m1 == -INFINITY ? 0.f : expf(m1 - mx);
+        l[r] = l[r] * f0 + l1 * f1;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) o[t][r] = o[t][r] * f0 + xw[8 + 4 * t + r] * f1;
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {

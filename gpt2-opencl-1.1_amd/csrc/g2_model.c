@@ -993,7 +993,7 @@ static int fused_prefill(g2_model *m, int P)
                           : g2i_launch(f_qkv, cdivu(3 * E, 64), cdivu(P, 64), 256, &g);
         g2_attnp_args t = { m->q, y->k_cache, y->v_cache, m->attn, P, E, NH, G2_KV_MAX_SEQ, 1.0f / sqrtf(64.0f),
                             big ? at_h : NULL, big ? at_l : NULL };
-        if (!rc) rc = g2i_launch(G2F_ATTN_PREFILL_MFMA, (unsigned)NH, cdivu(P, 64), 256, &t);
+        if (!rc) rc = g2i_launch(G2F_ATTN_PREFILL_MFMA, (unsigned)NH, cdivu(P, 64), 512, &t);
         memset(&g, 0, sizeof g);
         g.A = m->attn; g.B = y->proj_w; g.bias = y->proj_b; g.C = m->hidden; g.M = P; g.N = E; g.K = E;
         if (!rc) rc = h ? prefill_resid(m, m->attn, at_h, at_l, y->proj_w, y->proj_b, m->hidden, P, E, E, big)
