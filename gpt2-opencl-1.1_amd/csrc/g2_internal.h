@@ -62,7 +62,7 @@
     X(HGEMM_PARTIAL, "g2k_hgemm_partial") X(SPLITK_RESID, "g2k_splitk_resid") \
     X(HGEMM2_GELU, "g2k_hgemm2_gelu") X(HGEMM2_RESID, "g2k_hgemm2_resid")     \
     X(HGEMM2_QKV, "g2k_hgemm2_qkv") X(HGEMM2_PARTIAL, "g2k_hgemm2_partial")   \
-    X(LAYERNORM_SPLIT, "g2k_layernorm_split")
+    X(LAYERNORM_SPLIT, "g2k_layernorm_split") X(SPLITK_RESID_LN, "g2k_splitk_resid_ln")
 
 #define G2_ENUM_ENTRY(id, name) G2F_##id,
 enum { G2_KERNEL_LIST(G2_ENUM_ENTRY) G2F_COUNT };

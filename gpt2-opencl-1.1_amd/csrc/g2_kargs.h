@@ -60,13 +60,18 @@ typedef struct {
 } g2_gemm_args;
 
 /* C[m,n] = C[m,n] + ((sum over z < ks in order of part[z*M*N + m*N + n]) +
- * bias[n]) for m < M, n < N. */
+ * bias[n]) for m < M, n < N.  g2k_splitk_resid_ln (grid M, N <=
+ * G2_SKLN_MAXN) then writes LayerNorm(C[m,:]; ln_g, ln_b) as fp16 halves
+ * to hi, lo [M,N] (see g2_lnsplit_args). */
 typedef struct {
     const float *part;
     const float *bias;
     float *C;
     int M, N, ks;
+    const float *ln_g, *ln_b;
+    uint16_t *hi, *lo;
 } g2_skred_args;
+#define G2_SKLN_MAXN 2048
 
 /* Reference-layout matvec, first pass: partial[split*N + n] = sum over the
  * split's contiguous k-range of A[k] B[k*N + n]; grid (column tiles, splits). */

@@ -793,6 +793,60 @@ G2K_HG2 void g2k_hgemm2_resid(const g2_gemm_args a) { hgemm2_impl<GEPI_RESID>(a)
 G2K_HG2 void g2k_hgemm2_qkv(const g2_gemm_args a) { hgemm2_impl<GEPI_QKV>(a); }
 G2K_HG2 void g2k_hgemm2_partial(const g2_gemm_args a) { hgemm2_impl<GEPI_PARTIAL>(a); }
 
+/* The split-K residual epilogue fused with the LayerNorm that follows it
+ * in the prefill (proj -> ln_2, fc2 -> the next layer's ln_1): one
+ * work-group per row sums the slices, bias and residual as
+ * g2k_splitk_resid does, keeps the row in registers, and normalises it as
+ * g2k_layernorm does (same sums in the same order), writing the fp16
+ * halves of the next GEMM's operand. */
+G2K void g2k_splitk_resid_ln(const g2_skred_args a)
+{
+    constexpr int PT = G2_SKLN_MAXN / 256;
+    __shared__ float red4[4];
+    const int m = blockIdx.x, N = a.N;
+    if (m >= a.M) return;
+    const size_t MN = (size_t)a.M * N, row = (size_t)m * N;
+    constexpr int ZMAX = 8; /* slices read at once (ks <= ZMAX) */
+    float xv[PT];
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < PT; ++k) {
+        const int n = threadIdx.x + 256 * k;
+        xv[k] = 0.f;
+        if (n < N) {
+            /* every slice's load issued before the first sum */
+            float pz[ZMAX];
+#pragma unroll
+            for (int z = 0; z < ZMAX; ++z) pz[z] = z < a.ks ? a.part[(size_t)z * MN + row + n] : 0.f;
+            const float c = a.C[row + n];
+            float v = pz[0];
+#pragma unroll
+            for (int z = 1; z < ZMAX; ++z)
+                if (z < a.ks) v += pz[z];
+            if (a.bias) v += a.bias[n];
+            v = v + c;
+            a.C[row + n] = v;
+            xv[k] = v;
+            s += v;
+        }
+    }
+    const float mean = block_sum(s, red4) / (float)N;
+    float q = 0.f;
+#pragma unroll
+    for (int k = 0; k < PT; ++k)
+        if (threadIdx.x + 256 * k < N) {
+            const float d = xv[k] - mean;
+            q = fmaf(d, d, q);
+        }
+    const float var = block_sum(q, red4) / (float)N;
+    const float inv = 1.0f / sqrtf(var + 1e-5f);
+#pragma unroll
+    for (int k = 0; k < PT; ++k) {
+        const int n = threadIdx.x + 256 * k;
+        if (n < N) split_store(a.hi, a.lo, row + n, fmaf((xv[k] - mean) * inv, a.ln_g[n], a.ln_b[n]));
+    }
+}
+
 G2K void g2k_hgemm_store(const g2_gemm_args a) { hgemm_impl<GEPI_STORE>(a); }
 G2K void g2k_hgemm_gelu(const g2_gemm_args a) { hgemm_impl<GEPI_GELU>(a); }
 G2K void g2k_hgemm_resid(const g2_gemm_args a) { hgemm_impl<GEPI_RESID>(a); }

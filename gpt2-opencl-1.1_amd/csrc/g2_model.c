@@ -926,8 +926,13 @@ static int set_state(g2_model *m, int pos, int tok, int min_new, int ngen)
  * is the largest that keeps tiles x slices within the CU count; it splits
  * the K steps into slices that differ by at most one step. */
 static int prefill_resid(g2_model *m, const float *A, const uint16_t *Ah, const uint16_t *Al, const void *W,
-                         const float *bias, float *C, int P, int N, int K, int big)
+                         const float *bias, float *C, int P, int N, int K, int big, const float *ln_g,
+                         const float *ln_b, uint16_t *hi, uint16_t *lo, int *ln_done)
 {
+    /* ln_g (with big): the LayerNorm that follows, fused into the slice
+     * sum when there are slices (*ln_done = 1); otherwise left to the
+     * caller */
+    *ln_done = 0;
     const unsigned gx = cdivu(N, 64), gy = cdivu(P, 64);
     int ks = 1;
     for (int k = G2_PF_MAXSPLIT; k > 1; --k)
@@ -948,7 +953,11 @@ static int prefill_resid(g2_model *m, const float *A, const uint16_t *Ah, const 
     if (ks == 1) return g2i_launch(big ? G2F_HGEMM2_RESID : G2F_HGEMM_RESID, bx, by, big ? 1024 : 256, &g);
     g.part = m->pf_part; g.ksplit = ks;
     int rc = g2i_launch3(big ? G2F_HGEMM2_PARTIAL : G2F_HGEMM_PARTIAL, bx, by, (unsigned)ks, big ? 1024 : 256, &g);
-    g2_skred_args r = { m->pf_part, bias, C, P, N, ks };
+    g2_skred_args r = { m->pf_part, bias, C, P, N, ks, ln_g, ln_b, hi, lo };
+    if (!rc && ln_g && big && N <= G2_SKLN_MAXN) {
+        *ln_done = 1;
+        return g2i_launch(G2F_SPLITK_RESID_LN, (unsigned)P, 1, 256, &r);
+    }
     if (!rc) rc = g2i_launch(G2F_SPLITK_RESID, cdivu((unsigned)(P * N), 256) < 2048 ? cdivu((unsigned)(P * N), 256) : 2048,
                              1, 256, &r);
     return rc;
@@ -979,11 +988,13 @@ static int fused_prefill(g2_model *m, int P)
     uint16_t *ff_h = (uint16_t *)m->ffn1, *ff_l = ff_h + cap * F;
     g2_embed_args e = { m->wte, m->wpe, m->hidden, m->ids_dev, NULL, E, P, 0 };
     int rc = g2i_launch(f16 ? G2F_EMBED_F16 : G2F_EMBED_F32, cdivu(E, 256), (unsigned)P, 256, &e);
+    int ln1_done = 0; /* the previous layer's fc2 sum already wrote this layer's ln_1 */
     for (int l = 0; l < m->cfg.n_layer && !rc; ++l) {
         g2_layer *y = &m->L[l];
         g2_lnsplit_args ls = { m->hidden, ln_h, ln_l, y->ln1_w, y->ln1_b, E, P };
-        rc = big ? g2i_launch(G2F_LAYERNORM_SPLIT, (unsigned)P, 1, 256, &ls)
-                 : g2_layernorm(m->hidden, m->ln_out, y->ln1_w, y->ln1_b, E, P);
+        if (!ln1_done)
+            rc = big ? g2i_launch(G2F_LAYERNORM_SPLIT, (unsigned)P, 1, 256, &ls)
+                     : g2_layernorm(m->hidden, m->ln_out, y->ln1_w, y->ln1_b, E, P);
         g2_gemm_args g;
         memset(&g, 0, sizeof g);
         g.A = m->ln_out; g.Ah = ln_h; g.Al = ln_l; g.B = y->qkv_w; g.bias = y->qkv_b; g.q_out = m->q;
@@ -996,11 +1007,14 @@ static int fused_prefill(g2_model *m, int P)
         if (!rc) rc = g2i_launch(G2F_ATTN_PREFILL_MFMA, (unsigned)NH, cdivu(P, 64), 512, &t);
         memset(&g, 0, sizeof g);
         g.A = m->attn; g.B = y->proj_w; g.bias = y->proj_b; g.C = m->hidden; g.M = P; g.N = E; g.K = E;
-        if (!rc) rc = h ? prefill_resid(m, m->attn, at_h, at_l, y->proj_w, y->proj_b, m->hidden, P, E, E, big)
+        int ln2_done = 0;
+        if (!rc) rc = h ? prefill_resid(m, m->attn, at_h, at_l, y->proj_w, y->proj_b, m->hidden, P, E, E, big,
+                                        y->ln2_w, y->ln2_b, ln_h, ln_l, &ln2_done)
                         : g2i_launch(f_resid, cdivu(E, 64), cdivu(P, 64), 256, &g);
         g2_lnsplit_args ls2 = { m->hidden, ln_h, ln_l, y->ln2_w, y->ln2_b, E, P };
-        if (!rc) rc = big ? g2i_launch(G2F_LAYERNORM_SPLIT, (unsigned)P, 1, 256, &ls2)
-                          : g2_layernorm(m->hidden, m->ln_out, y->ln2_w, y->ln2_b, E, P);
+        if (!rc && !ln2_done)
+            rc = big ? g2i_launch(G2F_LAYERNORM_SPLIT, (unsigned)P, 1, 256, &ls2)
+                     : g2_layernorm(m->hidden, m->ln_out, y->ln2_w, y->ln2_b, E, P);
         memset(&g, 0, sizeof g);
         g.A = m->ln_out; g.B = y->fc_w; g.bias = y->fc_b; g.C = m->ffn1; g.M = P; g.N = F; g.K = E;
         g.Ah = ln_h; g.Al = ln_l; g.Ch = ff_h; g.Cl = ff_l;
@@ -1008,7 +1022,10 @@ static int fused_prefill(g2_model *m, int P)
                           : g2i_launch(f_gelu, cdivu(F, 64), cdivu(P, 64), 256, &g);
         memset(&g, 0, sizeof g);
         g.A = m->ffn1; g.B = y->fc2_w; g.bias = y->fc2_b; g.C = m->hidden; g.M = P; g.N = E; g.K = F;
-        if (!rc) rc = h ? prefill_resid(m, m->ffn1, ff_h, ff_l, y->fc2_w, y->fc2_b, m->hidden, P, E, F, big)
+        const g2_layer *yn = l + 1 < m->cfg.n_layer ? &m->L[l + 1] : NULL;
+        ln1_done = 0;
+        if (!rc) rc = h ? prefill_resid(m, m->ffn1, ff_h, ff_l, y->fc2_w, y->fc2_b, m->hidden, P, E, F, big,
+                                        yn ? yn->ln1_w : NULL, yn ? yn->ln1_b : NULL, ln_h, ln_l, &ln1_done)
                         : g2i_launch(f_resid, cdivu(E, 64), cdivu(P, 64), 256, &g);
     }
     if (!rc) rc = fused_lm_head(m, m->hidden + (size_t)(P - 1) * E, 1);
