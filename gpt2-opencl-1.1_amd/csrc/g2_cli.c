@@ -1,13 +1,17 @@
 /*
- * g2_cli.c -- ids-driven command-line driver (the reference's main(),
- * main.c:1967-2200, without the tokenizer: prompts are token ids).
+ * g2_cli.c -- command-line driver (the reference's main(), main.c:1967-2200).
  *
  *   g2run (--model DIR | --synth small|medium|large|xl) [--seed S]
- *         [--format fp32|fp16] [--path fused|reference]
- *         (--ids 1,2,3 | --random-prompt P) [--max-tokens N] [--min-tokens N]
+ *         [--format fp32|fp16] [--path fused|reference] [--tokenizer DIR]
+ *         (--prompt TEXT | --ids 1,2,3 | --random-prompt P)
+ *         [--max-tokens N] [--min-tokens N]
  *
- * Greedy decoding (temperature 0, repetition penalty off).  Prints the
- * generated ids and a timing summary in the style of main.c:2162-2169.
+ * Greedy decoding (temperature 0, repetition penalty off).  A text prompt is
+ * encoded with vocab.json + merges.txt from --tokenizer (default: the
+ * --model directory, which holds them as the reference's does, main.c:6,
+ * 2057) to at most 1023 ids (main.c:2093); with a tokenizer loaded the
+ * generated ids are also printed as text (main.c:1954).  Prints the ids and
+ * a timing summary in the style of main.c:2162-2169.
  */
 #include <stdio.h>
 #include <stdlib.h>
@@ -37,7 +41,7 @@ static void die(const char *what, int rc)
 
 int main(int argc, char **argv)
 {
-    const char *model_dir = NULL, *synth = NULL, *ids_arg = NULL;
+    const char *model_dir = NULL, *synth = NULL, *ids_arg = NULL, *text = NULL, *tok_dir = NULL;
     unsigned long long seed = 0x67707432ULL;
     int dtype = G2_F32, path = G2_PATH_FUSED, random_prompt = 0, max_new = 32, min_new = 1;
     for (int i = 1; i < argc; ++i) {
@@ -49,18 +53,32 @@ int main(int argc, char **argv)
         else if (!strcmp(a, "--format") && v) { dtype = !strcmp(v, "fp16") ? G2_F16 : G2_F32; ++i; }
         else if (!strcmp(a, "--path") && v) { path = !strcmp(v, "reference") ? G2_PATH_REFERENCE : G2_PATH_FUSED; ++i; }
         else if (!strcmp(a, "--ids") && v) { ids_arg = v; ++i; }
+        else if (!strcmp(a, "--prompt") && v) { text = v; ++i; }
+        else if (!strcmp(a, "--tokenizer") && v) { tok_dir = v; ++i; }
         else if (!strcmp(a, "--random-prompt") && v) { random_prompt = atoi(v); ++i; }
         else if (!strcmp(a, "--max-tokens") && v) { max_new = atoi(v); ++i; }
         else if (!strcmp(a, "--min-tokens") && v) { min_new = atoi(v); ++i; }
         else {
             fprintf(stderr, "usage: %s (--model DIR | --synth small|medium|large|xl) [--seed S] "
-                            "[--format fp32|fp16] [--path fused|reference] "
-                            "(--ids a,b,c | --random-prompt P) [--max-tokens N] [--min-tokens N]\n", argv[0]);
+                            "[--format fp32|fp16] [--path fused|reference] [--tokenizer DIR] "
+                            "(--prompt TEXT | --ids a,b,c | --random-prompt P) [--max-tokens N] "
+                            "[--min-tokens N]\n", argv[0]);
             return EXIT_FAILURE;
         }
     }
-    if ((!model_dir && !synth) || (!ids_arg && random_prompt <= 0)) {
-        fprintf(stderr, "need a model (--model/--synth) and a prompt (--ids/--random-prompt)\n");
+    if ((!model_dir && !synth) || (!ids_arg && !text && random_prompt <= 0)) {
+        fprintf(stderr, "need a model (--model/--synth) and a prompt (--prompt/--ids/--random-prompt)\n");
+        return EXIT_FAILURE;
+    }
+    g2_tokenizer *tok = NULL;
+    if (!tok_dir && model_dir && text) tok_dir = model_dir;
+    if (tok_dir) {
+        const int trc = g2_tok_load(tok_dir, &tok);
+        if (trc) die("g2_tok_load", trc);
+        printf("Tokenizer: %d tokens.\n", g2_tok_vocab_size(tok));
+    }
+    if (text && !tok) {
+        fprintf(stderr, "--prompt needs vocab.json and merges.txt (--tokenizer DIR)\n");
         return EXIT_FAILURE;
     }
     int rc = g2_init(0);
@@ -87,7 +105,14 @@ int main(int argc, char **argv)
 
     int prompt[G2_MAX_SEQ];
     int P = 0;
-    if (ids_arg) {
+    if (text) {
+        P = g2_tok_encode(tok, text, prompt, G2_MAX_SEQ - 1);
+        if (P < 1) {
+            fprintf(stderr, "the prompt encodes to no tokens\n");
+            return EXIT_FAILURE;
+        }
+        printf("Prompt: %d tokens\n", P);
+    } else if (ids_arg) {
         const char *s = ids_arg;
         while (*s && P < G2_MAX_SEQ - 1) {
             prompt[P++] = (int)strtol(s, (char **)&s, 10);
@@ -108,6 +133,11 @@ int main(int argc, char **argv)
     printf("Generated:");
     for (int i = 0; i < n; ++i) printf(" %d", out[i]);
     printf("\n");
+    if (tok) {
+        char *txt = malloc(16 * (size_t)G2_MAX_SEQ * 4 + 1);
+        if (txt && g2_tok_decode(tok, out, n, txt, 16 * G2_MAX_SEQ * 4 + 1) >= 0) printf("Text: %s\n", txt);
+        free(txt);
+    }
     printf("Decode graph replay: %d\n", g2_model_uses_graph(m));
     fprintf(stderr,
             "Timing:\n"
@@ -116,6 +146,7 @@ int main(int argc, char **argv)
             t[0], P, t[0] > 0 ? P / (t[0] * 1e-3) : 0.0, n - 1, t[1],
             n > 1 ? t[1] / (n - 1) : 0.0, n > 1 && t[1] > 0 ? (n - 1) / (t[1] * 1e-3) : 0.0);
     free(out);
+    g2_tok_free(tok);
     g2_model_free(m);
     g2_shutdown();
     return EXIT_SUCCESS;

@@ -438,3 +438,64 @@ class Model:
         check(_lib.g2_decode_run(self.h, int(token), int(start_pos), int(n_steps), int(forbid_eos),
                                  out.ctypes.data, C.byref(ms)))
         return out, ms.value
+
+
+# ---------------------------------------------------------------- text
+
+_sig("g2_tok_load", _i, C.c_char_p, C.POINTER(_vp))
+_sig("g2_tok_free", None, _vp)
+_sig("g2_tok_vocab_size", _i, _vp)
+_sig("g2_tok_encode", _i, _vp, C.c_char_p, _vp, _i)
+_sig("g2_tok_decode", _i, _vp, _vp, _i, _vp, _i)
+
+
+class Tokenizer:
+    """GPT-2 byte-level BPE over vocab.json + merges.txt in a directory,
+    with the reference tokenizer's behaviour (tokenizer.c; gpt2_encode /
+    gpt2_decode -> encode / decode).  Host-only: needs no device."""
+
+    def __init__(self, directory):
+        h = _vp()
+        check(_lib.g2_tok_load(os.fsencode(str(directory)), C.byref(h)))
+        self.h = h
+
+    def free(self):
+        if self.h:
+            _lib.g2_tok_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    @property
+    def vocab_size(self):
+        return _lib.g2_tok_vocab_size(self.h)
+
+    def encode(self, text, max_ids=MAX_SEQ - 1):
+        """ids of UTF-8 text (str or bytes without NUL), at most max_ids
+        (main.c encodes prompts with MAX_SEQ_LEN - 1)."""
+        raw = text.encode("utf-8") if isinstance(text, str) else bytes(text)
+        if b"\0" in raw:
+            raise G2Error(G2_E_ARG, "text contains NUL")
+        buf = np.empty(max(int(max_ids), 1), dtype=np.int32)
+        n = _lib.g2_tok_encode(self.h, raw, buf.ctypes.data, int(max_ids))
+        if n < 0:
+            raise G2Error(G2_E_ARG, "g2_tok_encode: bad arguments")
+        return buf[:n].copy()
+
+    def decode(self, ids, max_bytes=None):
+        """bytes of the ids (undecodable code points as '?'), truncated to
+        max_bytes - 1 bytes (default: enough for every token)."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        cap = int(max_bytes) if max_bytes is not None else 64 * max(len(ids), 1) + 1
+        out = C.create_string_buffer(cap)
+        n = _lib.g2_tok_decode(self.h, ids.ctypes.data, len(ids), out, cap)
+        if n < 0:
+            raise G2Error(G2_E_ARG, "g2_tok_decode: bad arguments")
+        return out.raw[:n]
+
+    def decode_text(self, ids):
+        return self.decode(ids).decode("utf-8", errors="replace")

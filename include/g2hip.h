@@ -261,6 +261,25 @@ int g2_generate(g2_model *m, const int *prompt, int n_prompt, int max_new,
 int g2_decode_run(g2_model *m, int token, int start_pos, int n_steps,
                   int forbid_eos, int *out_ids, double *elapsed_ms);
 
+/* ---- text prompts: GPT-2 byte-level BPE (replaces tokenizer.h / tokenizer.c)
+ * Host-only; no device is needed.  Same behaviour as the reference's
+ * tokenizer: ASCII-class pre-tokenisation, byte alphabet, ranked merges,
+ * tokens missing from the vocabulary dropped. */
+typedef struct g2_tokenizer g2_tokenizer;
+
+/* vocab.json and merges.txt from the directory (gpt2_tokenizer_load,
+ * tokenizer.h:11); G2_OK or an error code, *out NULL on failure. */
+int g2_tok_load(const char *dir, g2_tokenizer **out);
+void g2_tok_free(g2_tokenizer *t);                 /* gpt2_tokenizer_free, tokenizer.h:12 */
+int g2_tok_vocab_size(const g2_tokenizer *t);      /* tokenizer.h:24: largest id + 1 */
+/* UTF-8 text to at most max_ids ids (gpt2_encode, tokenizer.h:15): the count
+ * written, or -1 on a NULL argument or max_ids <= 0. */
+int g2_tok_encode(const g2_tokenizer *t, const char *text, int *ids, int max_ids);
+/* ids to UTF-8, NUL-terminated, at most max_bytes - 1 bytes (gpt2_decode,
+ * tokenizer.h:19): the bytes written, or -1 on a NULL argument or
+ * max_bytes <= 0. */
+int g2_tok_decode(const g2_tokenizer *t, const int *ids, int n, char *out, int max_bytes);
+
 #ifdef __cplusplus
 }
 #endif
