@@ -185,7 +185,7 @@ static int step_supported(const g2_model *m, int nwg, const char **why)
     const int ve = m->dtype == G2_F16 ? 8 : 4;
     const int E = c->n_embd, F = c->ffn_dim, V = c->vocab_size;
     if (m->path != G2_PATH_FUSED) { *why = "not the fused path"; return 0; }
-    if (nwg <= 0 || nwg > G2_STEP_THREADS) { *why = "the device has no cooperative step grid"; return 0; }
+    if (nwg <= 0 || nwg > G2_STEP_THREADS) { *why = "no cooperative step grid (unsupported, or refused at g2_init)"; return 0; }
     if (E > G2_STEP_MAXE || F > G2_STEP_MAXF) { *why = "n_embd or ffn above the step kernel's ceilings"; return 0; }
     if (E % ve || F % ve || E != 64 * c->n_head) { *why = "sizes not multiples of the weight chunk or head dim not 64"; return 0; }
     const int dims[5][2] = { { 3 * E, E }, { E, E }, { F, E }, { E, F }, { V, E } };

@@ -100,10 +100,12 @@ int g2i_step3_ok(void) { return G.step3_ok; }
  * L2 of their XCD and gives the work-groups of one XCD the ranks w / 8,
  * which are distinct if consecutive work-groups go to consecutive XCDs (the
  * dispatcher's round-robin, whatever XCD it starts from).  Check that with
- * a probe launch of the same shape; 1 if it holds for every work-group. */
-static int xcd_mapping_holds(int nwg)
+ * a probe launch of the same shape; 1 if it holds for every work-group, 0
+ * if not, -1 if the cooperative launch itself is refused (*err: its error). */
+static int xcd_mapping_holds(int nwg, hipError_t *err)
 {
     int ok = 0, nb = 0, *d = NULL;
+    *err = hipSuccess;
     if (nwg <= 0 || nwg % G2_NXCD) return 0;
     if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, G.fn[G2F_STEPX_F16], G2_STEP_THREADS, 0) != hipSuccess || nb < 1)
         return 0;
@@ -114,9 +116,10 @@ static int xcd_mapping_holds(int nwg)
     if (hipMalloc((void **)&d, (size_t)nwg * sizeof(int)) == hipSuccess &&
         hipMemsetAsync(d, 0xff, (size_t)nwg * sizeof(int), G.stream) == hipSuccess) {
         void *params[1] = { &d };
-        if (hipModuleLaunchCooperativeKernel(G.fn[G2F_XCC_PROBE], (unsigned)nwg, 1, 1, G2_STEP_THREADS, 1, 1, 0,
-                                             G.stream, params) == hipSuccess &&
-            hipMemcpyAsync(h, d, (size_t)nwg * sizeof(int), hipMemcpyDeviceToHost, G.stream) == hipSuccess &&
+        *err = hipModuleLaunchCooperativeKernel(G.fn[G2F_XCC_PROBE], (unsigned)nwg, 1, 1, G2_STEP_THREADS, 1, 1, 0,
+                                                G.stream, params);
+        if (*err != hipSuccess) ok = -1;
+        else if (hipMemcpyAsync(h, d, (size_t)nwg * sizeof(int), hipMemcpyDeviceToHost, G.stream) == hipSuccess &&
             hipStreamSynchronize(G.stream) == hipSuccess) {
             ok = h[0] >= 0 && h[0] < G2_NXCD;
             for (int w = 0; w < nwg && ok; ++w)
@@ -245,8 +248,17 @@ int g2_init(int device)
                      hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb3, G.fn[G2F_STEP3_F16], G2_STEP_THREADS, 0) ==
                          hipSuccess && nb3 >= 1;
         (void)hipGetLastError();
-        G.stepx_ok = G.step_wgs ? xcd_mapping_holds(G.step_wgs) : 0;
-        if (G.step_wgs && !G.stepx_ok)
+        hipError_t ec = hipSuccess;
+        const int xm = G.step_wgs ? xcd_mapping_holds(G.step_wgs, &ec) : 0;
+        G.stepx_ok = xm == 1;
+        if (xm < 0) {
+            /* A device grants cooperative launches to one process at a time:
+             * a second process on the same GPU is refused them. */
+            fprintf(stderr, "g2hip: cooperative launch refused (HIP error %d: %s; another process on this GPU "
+                            "may hold it); decode uses per-operator kernels\n", (int)ec, hipGetErrorString(ec));
+            G.step_wgs = 0;
+            G.step3_ok = 0;
+        } else if (G.step_wgs && !G.stepx_ok)
             fprintf(stderr, "g2hip: work-groups are not dealt to XCDs round-robin on this device; "
                             "decode uses the all-to-all step kernel\n");
     }

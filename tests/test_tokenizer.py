@@ -157,7 +157,9 @@ def test_errors(lib_tok, tmp_path):
 @pytest.mark.gpu
 def test_cli_text_prompt(g2):
     """g2run --prompt: the text is encoded with the fixture vocabulary, the
-    model generates from those ids, and the output is printed as text."""
+    model generates from those ids, and the output is printed as text.  The
+    child runs while this process holds the GPU, so its cooperative launches
+    are refused and it decodes with the per-operator kernels."""
     import subprocess
     exe = os.path.join(os.path.dirname(HERE), "gpt2-opencl-1.1_amd", "g2run")
     text = "the kernel decode cache"
