@@ -246,6 +246,13 @@ typedef struct {
 #define G2_STEP_MAXUNITS 512 /* (row, segment) units per work-group and phase */
 #define G2_STEP_MAXCH 16    /* 64-position key chunks per head */
 #define G2X_HEAD 64         /* words before the first layer region (word 0: abort) */
+/* Loader-wave decode step (g2k_step4_f16, same arguments and exchange
+ * layout): 8 computing waves + 4 loader waves; weight rows pass through an
+ * LDS ring of 1 KB blocks; lm_head rows go through it G2_STEP4_LM_ROWS at a
+ * time.  Every matrix share must fit the ring. */
+#define G2_STEP4_THREADS 768
+#define G2_STEP4_RING_BLOCKS 104
+#define G2_STEP4_LM_ROWS 16
 
 /* Word offsets inside one layer region (E = n_embd, NH heads, F = ffn):
  * QKV outputs [3E], attention chunk partials [NH][G2_STEP_MAXCH][66],

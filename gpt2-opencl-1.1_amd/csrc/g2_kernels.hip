@@ -1151,6 +1151,7 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_mfma(const g2
 #include "g2_step.hip"
 #include "g2_stepx.hip"
 #include "g2_step3.hip"
+#include "g2_step4.hip"
 
 /* dst = transpose of the 16-bit [R][C] matrix src, 32x32 tiles through LDS
  * (the step kernels' input-major fc2 copy). */

@@ -59,6 +59,7 @@ struct g2_model {
     int step_on;   /* decode steps run the step kernel */
     int stepx;     /* ... in its XCD-parallel form */
     int step3;     /* ... in its two-role form */
+    int step4;     /* ... in its loader-wave form */
     int step_ran;  /* a step kernel ran since the last error check */
     const char *step_why; /* why the step kernel cannot run this model */
     unsigned long long *trace; /* phase timestamps, when G2_STEP_TRACE names a file */
@@ -247,6 +248,22 @@ static int step3_supported(const g2_model *m, int nwg)
     return 1;
 }
 
+/* Whether the loader-wave step kernel (g2k_step4_f16) can run this model on
+ * a grid of nwg work-groups: fp16 weights, and every work-group's share of
+ * every matrix (and G2_STEP4_LM_ROWS lm_head rows) fits its LDS ring. */
+static int step4_supported(const g2_model *m, int nwg)
+{
+    const g2_config *c = &m->cfg;
+    const long E = c->n_embd, F = c->ffn_dim;
+    if (m->dtype != G2_F16 || nwg <= 0) return 0;
+    const long ring = (long)G2_STEP4_RING_BLOCKS * 1024;
+    const long share[5] = { (3 * E + nwg - 1) / nwg * E * 2, (E + nwg - 1) / nwg * E * 2,
+                            (F + nwg - 1) / nwg * E * 2, (E + nwg - 1) / nwg * F * 2, G2_STEP4_LM_ROWS * E * 2 };
+    for (int i = 0; i < 5; ++i)
+        if (share[i] > ring) return 0;
+    return 1;
+}
+
 /* The input-major copy of every layer's fc2 weights for the two-role kernel
  * (a device transpose of the packed [E][F] matrix). */
 static int step3_fc2_copies(g2_model *m)
@@ -291,6 +308,8 @@ static int step_setup(g2_model *m)
     free(t);
     const char *envx = getenv("G2_STEPX");
     m->stepx = envx && envx[0] == '1' && g2i_stepx_ok() && stepx_supported(m, nwg);
+    const char *env4 = getenv("G2_STEP4");
+    m->step4 = !m->step3 && !m->stepx && env4 && env4[0] == '1' && g2i_step4_ok() && step4_supported(m, nwg);
     const long w1 = G2X_TOTAL_WORDS(L, c->n_embd, c->n_head, c->ffn_dim, nwg);
     const int HX = (c->n_head + G2_NXCD - 1) / G2_NXCD, FX = (c->ffn_dim + G2_NXCD - 1) / G2_NXCD;
     const long w2 = G2XX_TOTAL_WORDS(L, HX, c->n_embd, FX, nwg);
@@ -660,7 +679,7 @@ int g2_model_set_step(g2_model *m, int on)
 int g2_model_uses_step(const g2_model *m)
 {
     if (!m) return g2i_err(G2_E_ARG, "NULL model");
-    return m->step_on ? (m->step3 ? 3 : (m->stepx ? 2 : 1)) : 0;
+    return m->step_on ? (m->step3 ? 3 : (m->stepx ? 2 : (m->step4 ? 4 : 1))) : 0;
 }
 
 int g2_model_uses_graph(const g2_model *m)
@@ -831,6 +850,7 @@ static int step_launch(g2_model *m)
                                G2_STEP_THREADS, &a);
     }
     a.xlayer = G2X_LAYER_WORDS(c->n_embd, c->n_head, c->ffn_dim);
+    if (m->step4) return g2i_coop_launch(G2F_STEP4_F16, (unsigned)m->step_wgs, G2_STEP4_THREADS, &a);
     return g2i_coop_launch(m->dtype == G2_F16 ? G2F_STEP_F16 : G2F_STEP_F32, (unsigned)m->step_wgs,
                            G2_STEP_THREADS, &a);
 }

@@ -35,6 +35,7 @@ static struct {
     int step_wgs; /* work-groups of a cooperative step launch (0: unsupported) */
     int stepx_ok; /* the XCD-parallel step kernel may run */
     int step3_ok; /* the two-role step kernel may run */
+    int step4_ok; /* the loader-wave step kernel may run */
     char name[256];
     hipModule_t module;
     hipStream_t stream;
@@ -95,6 +96,7 @@ int g2i_step_wgs(void) { return G.step_wgs; }
 int g2i_cus(void) { return G.cus > 0 ? G.cus : 1; }
 int g2i_stepx_ok(void) { return G.stepx_ok; }
 int g2i_step3_ok(void) { return G.step3_ok; }
+int g2i_step4_ok(void) { return G.step4_ok; }
 
 /* The XCD-parallel step kernel hands data between work-groups through the
  * L2 of their XCD and gives the work-groups of one XCD the ranks w / 8,
@@ -247,6 +249,10 @@ int g2_init(int device)
         G.step3_ok = G.step_wgs && G.step_wgs <= G3_MAXWG &&
                      hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb3, G.fn[G2F_STEP3_F16], G2_STEP_THREADS, 0) ==
                          hipSuccess && nb3 >= 1;
+        int nb4 = 0;
+        G.step4_ok = G.step_wgs &&
+                     hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb4, G.fn[G2F_STEP4_F16], G2_STEP4_THREADS, 0) ==
+                         hipSuccess && nb4 >= 1;
         (void)hipGetLastError();
         hipError_t ec = hipSuccess;
         const int xm = G.step_wgs ? xcd_mapping_holds(G.step_wgs, &ec) : 0;
@@ -258,6 +264,7 @@ int g2_init(int device)
                             "may hold it); decode uses per-operator kernels\n", (int)ec, hipGetErrorString(ec));
             G.step_wgs = 0;
             G.step3_ok = 0;
+            G.step4_ok = 0;
         } else if (G.step_wgs && !G.stepx_ok)
             fprintf(stderr, "g2hip: work-groups are not dealt to XCDs round-robin on this device; "
                             "decode uses the all-to-all step kernel\n");

@@ -153,6 +153,12 @@ __device__ __forceinline__ float wsum4(float a, float b, float c, float d)
     return v + dpp<0x121>(v); /* row_ror:1 */
 }
 
+/* Work-group barrier of the helpers below; a kernel whose work-group has
+ * waves outside the computation passes its own barrier object instead. */
+struct wg_bar {
+    __device__ __forceinline__ void operator()() const { __syncthreads(); }
+};
+
 struct ctx {
     unsigned tag;
     u64 *abort_w;
@@ -211,11 +217,13 @@ __device__ __forceinline__ void settle(const ctx &c, const u64 *src, u64 (&v)[NP
  * with the weight stream), so a work-group that found stale words waits on
  * nsent sentinel words only (word n*k/nsent for k < nsent: the first word
  * of each producer when n is split evenly over nsent producers), then
- * re-reads just its stale words.  Ends with a barrier; `flag` is an LDS
- * word of the caller. */
-template <int NP>
+ * re-reads just its stale words.  SENT selects the sentinel scheme for
+ * every size (for a kernel whose polling must leave the memory queue to a
+ * weight stream).  Ends with a barrier; `flag` is an LDS word of the
+ * caller. */
+template <int NP, typename BAR = wg_bar, bool SENT = false>
 __device__ __forceinline__ void fetch(int tid, const ctx &c, const u64 *src, int n, int nsent,
-                                      float *dst, lds_flag *flag)
+                                      float *dst, lds_flag *flag, BAR bar = BAR())
 {
     const u64 filler = (u64)c.tag << 32;
     u64 v[NP];
@@ -224,7 +232,7 @@ __device__ __forceinline__ void fetch(int tid, const ctx &c, const u64 *src, int
         const int w = tid + NT * i;
         v[i] = w < n ? ll_get(src + w) : filler;
     }
-    if constexpr (NP <= 4) {
+    if constexpr (NP <= 4 && !SENT) {
         (void)nsent;
         (void)flag;
         settle(c, src, v, [&](int i) { const int w = tid + NT * i; return w < n ? w : -1; });
@@ -233,23 +241,23 @@ __device__ __forceinline__ void fetch(int tid, const ctx &c, const u64 *src, int
             const int w = tid + NT * i;
             if (w < n) dst[w] = ll_val(v[i]);
         }
-        __syncthreads();
+        bar();
         return;
     }
     if (tid == 0) *flag = 0;
-    __syncthreads();
+    bar();
     unsigned bad = 0;
 #pragma unroll
     for (int i = 0; i < NP; ++i) bad |= (unsigned)(ll_tag(v[i]) != c.tag);
     if (bad) *flag = 1;
-    __syncthreads();
+    bar();
     if (*flag && !*c.dead) {
         if (tid < nsent) {
             const int w = (int)(((long)n * tid) / nsent);
             u64 sv[1] = {ll_get(src + w)};
             settle(c, src, sv, [&](int) { return w; });
         }
-        __syncthreads();
+        bar();
         settle(c, src, v, [&](int i) { const int w = tid + NT * i; return w < n ? w : -1; });
     }
 #pragma unroll
@@ -257,7 +265,7 @@ __device__ __forceinline__ void fetch(int tid, const ctx &c, const u64 *src, int
         const int w = tid + NT * i;
         if (w < n) dst[w] = ll_val(v[i]);
     }
-    __syncthreads();
+    bar();
 }
 
 /* LayerNorm parameters of the thread's entries i = tid + NT*k, loaded at
@@ -286,9 +294,9 @@ __device__ __forceinline__ ln_params<NE> ln_load(int tid, const G2_GLOBAL float 
  * entries, x0 = x[0] (a shift that keeps the variance E[d^2] - E[d]^2 free
  * of cancellation when |mean| >> std); the two sums are reduced together,
  * wave totals added in wave order.  Ends with a barrier. */
-template <int NE>
+template <int NE, typename BAR = wg_bar>
 __device__ __forceinline__ void layernorm(int tid, const float *x, float *xin, const ln_params<NE> &lp,
-                                          int E, float *red)
+                                          int E, float *red, BAR bar = BAR())
 {
     const float x0 = x[0];
     float s = 0.f, q = 0.f;
@@ -307,7 +315,7 @@ __device__ __forceinline__ void layernorm(int tid, const float *x, float *xin, c
         red[tid >> 6] = s;
         red[NW + (tid >> 6)] = q;
     }
-    __syncthreads();
+    bar();
     float S = red[0], Q = red[NW];
 #pragma unroll
     for (int w = 1; w < NW; ++w) {
@@ -323,7 +331,7 @@ __device__ __forceinline__ void layernorm(int tid, const float *x, float *xin, c
         const int i = tid + NT * k;
         if (i < E) xin[i] = fmaf((x[i] - mean) * inv, lp.g[k], lp.b[k]);
     }
-    __syncthreads();
+    bar();
 }
 
 /* A work-group's share of one packed matrix W[N,K] (output-major): rows
@@ -486,15 +494,20 @@ __device__ __forceinline__ void attn_load(int tid, const g2_step_layer &y, att_r
     /* unconditional: every address is inside the caches (positions < S =
      * 1024, dims < E); values of positions >= T or of the current position
      * are never used.  Skipping loads under a lane mask would make the
-     * compiler wait for all of the wave's earlier stores first. */
-    (void)on; (void)T; (void)pos;
-    const G2_GLOBAL f32x4 *kb = gl((const f32x4 *)(y.k_cache + (size_t)(h * 64 + 4 * dg) * S + jk));
+     * compiler wait for all of the wave's earlier stores first.  A half
+     * without a unit points every lane at the first 16 bytes of the caches,
+     * so its loads cost one line each instead of 32 KB of memory traffic
+     * queued in front of the work-group's later reads. */
+    (void)T; (void)pos;
+    const size_t koff = on ? (size_t)(h * 64 + 4 * dg) * S + jk : 0, kstr = on ? (size_t)(S / 4) : 0;
+    const G2_GLOBAL f32x4 *kb = gl((const f32x4 *)(y.k_cache + koff));
 #pragma unroll
-    for (int d = 0; d < 4; ++d) r.kv[d] = kb[(size_t)d * (S / 4)];
+    for (int d = 0; d < 4; ++d) r.kv[d] = kb[(size_t)d * kstr];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const int j = j0 + 4 * jg + e;
-        r.vv[e] = *gl((const f32x4 *)(y.v_cache + (size_t)j * E + h * 64 + 4 * d4));
+        const size_t voff = on ? (size_t)j * E + h * 64 + 4 * d4 : 0;
+        r.vv[e] = *gl((const f32x4 *)(y.v_cache + voff));
     }
 }
 
@@ -504,9 +517,9 @@ __device__ __forceinline__ void attn_load(int tid, const g2_step_layer &y, att_r
  * position's key and value taken from L; the chunk's (max, sum, o[64]) go
  * to pout[0..65].  `on` is false for a half without a unit; it still takes
  * part in the three barriers. */
-template <bool LOCAL>
+template <bool LOCAL, typename BAR = wg_bar>
 __device__ __forceinline__ void attn_compute(int tid, const ctx &c, float scale, u64 *pout, att_lds &L,
-                                             const att_regs &r, bool on, int ch, int pos, int T)
+                                             const att_regs &r, bool on, int ch, int pos, int T, BAR bar = BAR())
 {
     const int t = tid & 255;
     const int j0 = ch * 64;
@@ -529,7 +542,7 @@ __device__ __forceinline__ void attn_compute(int tid, const ctx &c, float scale,
 #pragma unroll
         for (int e = 0; e < 4; ++e) L.red[dg][4 * pq + e] = s[e];
     }
-    __syncthreads();
+    bar();
     if (on && t < 64) {
         const bool ok = j0 + t < T;
         float s = 0.f;
@@ -542,7 +555,7 @@ __device__ __forceinline__ void attn_compute(int tid, const ctx &c, float scale,
         L.pr[t] = p;
         if (t == 0) { L.stat[0] = m; L.stat[1] = l; }
     }
-    __syncthreads();
+    bar();
     if (on) {
         float o[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -561,7 +574,7 @@ __device__ __forceinline__ void attn_compute(int tid, const ctx &c, float scale,
 #pragma unroll
         for (int f = 0; f < 4; ++f) L.red[jg][4 * d4 + f] = o[f];
     }
-    __syncthreads();
+    bar();
     if (on && t < 64) {
         float o = 0.f;
 #pragma unroll
@@ -581,10 +594,10 @@ __device__ __forceinline__ void attn_compute(int tid, const ctx &c, float scale,
  * taken from the exchange; the chunk's (max, sum, o[64]) go to pout[0..65].
  * `on` is false for a half without a unit; it still takes part in the
  * barriers. */
-template <bool LOCAL>
+template <bool LOCAL, typename BAR = wg_bar>
 __device__ __forceinline__ void attn_chunk(int tid, const ctx &c, float scale, const u64 *src, int qo,
                                            int ko, int vo, u64 *pout, att_lds &L, att_regs &r, bool on,
-                                           int ch, int pos, int T, u64 *trace_slot = nullptr)
+                                           int ch, int pos, int T, u64 *trace_slot = nullptr, BAR bar = BAR())
 {
     const int t = tid & 255;
     /* q, k and v of the head at this position: src[qo + d], src[ko + d],
@@ -597,9 +610,9 @@ __device__ __forceinline__ void attn_chunk(int tid, const ctx &c, float scale, c
         float *dst = part == 0 ? L.q : (part == 1 ? L.kn : L.vn);
         dst[d] = ll_val(v[0]);
     }
-    __syncthreads();
+    bar();
     if (trace_slot && tid == 0) *trace_slot = wall_clock64();
-    attn_compute<LOCAL>(tid, c, scale, pout, L, r, on, ch, pos, T);
+    attn_compute<LOCAL>(tid, c, scale, pout, L, r, on, ch, pos, T, bar);
 }
 
 __device__ __forceinline__ bool am_better2(float v1, int i1, float v2, int i2)
@@ -608,17 +621,18 @@ __device__ __forceinline__ bool am_better2(float v1, int i1, float v2, int i2)
 }
 
 /* First-max over the work-group's (bv, bi); result in amv[0], ami[0]. */
-__device__ __forceinline__ void blk_argmax(int tid, float bv, int bi, float *amv, int *ami)
+template <typename BAR = wg_bar>
+__device__ __forceinline__ void blk_argmax(int tid, float bv, int bi, float *amv, int *ami, BAR bar = BAR())
 {
     amv[tid] = bv;
     ami[tid] = bi;
-    __syncthreads();
+    bar();
     for (int s = NT / 2; s > 0; s >>= 1) {
         if (tid < s && am_better2(amv[tid + s], ami[tid + s], amv[tid], ami[tid])) {
             amv[tid] = amv[tid + s];
             ami[tid] = ami[tid + s];
         }
-        __syncthreads();
+        bar();
     }
 }
 

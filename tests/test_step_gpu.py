@@ -1,8 +1,9 @@
 """GPU parity of the persistent decode-step kernels (one cooperative launch
 per token running every layer, the lm_head and the greedy pick), in both
-forms: all-to-all (the default) and XCD-parallel (G2_STEPX=1: each XCD owns
+forms: all-to-all (the default), XCD-parallel (G2_STEPX=1: each XCD owns
 heads and ffn rows, where the device deals work-groups to XCDs
-round-robin).
+round-robin), two-role (G2_STEP3=1) and loader-ring (G2_STEP4=1: a loader
+wave streams the weight rows through an LDS ring).
 
 The fused path decodes with them by default; these tests pin them against
 the CPU oracle (greedy ids, teacher-forced per-step logits within 2e-3 fp32
@@ -21,10 +22,12 @@ pytestmark = pytest.mark.gpu
 
 SEED = 0x67707432
 KINDS = [pytest.param("a2a", id="all-to-all"), pytest.param("xcd", id="xcd"),
-         pytest.param("two-role", id="two-role")]
-ENV = {"a2a": {"G2_STEPX": "0", "G2_STEP3": "0"}, "xcd": {"G2_STEPX": "1", "G2_STEP3": "0"},
-       "two-role": {"G2_STEPX": "0", "G2_STEP3": "1"}}
-KIND_ID = {"a2a": 1, "xcd": 2, "two-role": 3}
+         pytest.param("two-role", id="two-role"), pytest.param("ring", id="loader-ring")]
+ENV = {"a2a": {"G2_STEPX": "0", "G2_STEP3": "0", "G2_STEP4": "0"},
+       "xcd": {"G2_STEPX": "1", "G2_STEP3": "0", "G2_STEP4": "0"},
+       "two-role": {"G2_STEPX": "0", "G2_STEP3": "1", "G2_STEP4": "0"},
+       "ring": {"G2_STEPX": "0", "G2_STEP3": "0", "G2_STEP4": "1"}}
+KIND_ID = {"a2a": 1, "xcd": 2, "two-role": 3, "ring": 4}
 
 
 @pytest.fixture
@@ -36,8 +39,9 @@ def stepx(request, monkeypatch):
 
 
 def _expect_kind(m, kind, f16=True):
-    """The two-role form runs fp16-weight models; the others run both."""
-    if kind == "two-role" and not f16:
+    """The two-role and loader-ring forms run fp16-weight models; the others
+    run both."""
+    if kind in ("two-role", "ring") and not f16:
         return
     assert m.step_kind() == KIND_ID[kind], f"expected step kernel form {kind}, got {m.step_kind()}"
 
@@ -153,8 +157,8 @@ def test_step_decode_run_matches_generate(g2, stepx):
     m.free()
 
 
-@pytest.mark.parametrize("stepx", [pytest.param("xcd", id="xcd"), pytest.param("two-role", id="two-role")],
-                         indirect=True)
+@pytest.mark.parametrize("stepx", [pytest.param("xcd", id="xcd"), pytest.param("two-role", id="two-role"),
+                                   pytest.param("ring", id="loader-ring")], indirect=True)
 @pytest.mark.parametrize("cfg_args", [(2, 128, 2, 256), (3, 192, 3, 1000), (1, 64, 1, 50257)],
                          ids=["tiny", "3-heads", "1-head"])
 def test_stepx_small_shapes(g2, stepx, cfg_args):
@@ -171,7 +175,7 @@ def test_stepx_small_shapes(g2, stepx, cfg_args):
         ref_ids, top2, ref_lg = om.generate(prompt, 12, logit_steps=4)
         m = g2.Model.from_host(cfg, w, dtype, g2.PATH_FUSED)
         print(f"[step] L{L} E{E} H{H} V{V} {'f16' if f16 else 'f32'} form {m.step_kind()}", flush=True)
-        if stepx == "two-role":
+        if stepx in ("two-role", "ring"):
             _expect_kind(m, stepx, f16)
         ids, _ = m.generate(prompt, 12)
         greedy_agree(ids, ref_ids, top2, 1e-2 if f16 else 1e-4)
