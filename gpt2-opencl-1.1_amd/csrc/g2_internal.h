@@ -60,6 +60,7 @@
     X(HGEMM_STORE, "g2k_hgemm_store") X(HGEMM_GELU, "g2k_hgemm_gelu")         \
     X(HGEMM_RESID, "g2k_hgemm_resid") X(HGEMM_QKV, "g2k_hgemm_qkv")           \
     X(ATTN_PREFILL_MFMA, "g2k_attn_prefill_mfma")                             \
+    X(ATTN_PREFILL_H16, "g2k_attn_prefill_h16")                               \
     X(HGEMM_PARTIAL, "g2k_hgemm_partial") X(SPLITK_RESID, "g2k_splitk_resid") \
     X(HGEMM2_GELU, "g2k_hgemm2_gelu") X(HGEMM2_RESID, "g2k_hgemm2_resid")     \
     X(HGEMM2_QKV, "g2k_hgemm2_qkv") X(HGEMM2_PARTIAL, "g2k_hgemm2_partial")   \

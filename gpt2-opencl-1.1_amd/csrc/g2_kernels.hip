@@ -218,6 +218,15 @@ __device__ __forceinline__ void split_store(uint16_t *hi, uint16_t *lo, size_t i
     lo[i] = __builtin_bit_cast(uint16_t, l);
 }
 
+/* The halves of split_store as values: hi16(v) + lo16(v) represents v to
+ * ~22 significant bits. */
+__device__ __forceinline__ _Float16 hi16(float v) { return (_Float16)v; }
+__device__ __forceinline__ _Float16 lo16(float v)
+{
+#pragma clang fp contract(off)
+    return (_Float16)(v - (float)(_Float16)v);
+}
+
 /* ---- layernorm (math.cl:283-311): one work-group per row, two-pass mean and
  * biased variance, eps 1e-5, out = (x-mean)*inv_std*gamma + beta.  SPLIT:
  * the row is written as fp16 halves (g2_lnsplit_args), same arithmetic. */
@@ -1109,6 +1118,228 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_mfma(const g2
      * staging tiles are free), scaled to the common max */
     __syncthreads();
     float *xw = Kt[0] + (size_t)(rg * 64 + lane) * 24; /* 4 waves x 64 lanes x 24 floats <= 2 tiles */
+    if (hs == 1) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            xw[r] = m[r];
+            xw[4 + r] = l[r];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xw[8 + 4 * t + r] = o[t][r];
+        }
+    }
+    __syncthreads();
+    if (hs == 1) return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float m1 = xw[r], l1 = xw[4 + r];
+        const float mx = fmaxf(m[r], m1);
+        const float f0 = m[r] == -INFINITY ? 0.f : expf(m[r] - mx);
+        const float f1 = m1 == -INFINITY ? 0.f : expf(m1 - mx);
+        l[r] = l[r] * f0 + l1 * f1;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) o[t][r] = o[t][r] * f0 + xw[8 + 4 * t + r] * f1;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int i = i_base + r;
+        if (i >= P) continue;
+        const float inv = 1.0f / l[r];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const size_t idx = (size_t)i * E + h * 64 + 16 * t + lr;
+            if (a.out_hi) split_store(a.out_hi, a.out_lo, idx, o[t][r] * inv);
+            else a.out[idx] = o[t][r] * inv;
+        }
+    }
+}
+
+/* Causal prompt attention on the fp16 matrix cores (same arguments, grid
+ * and results as g2k_attn_prefill_mfma, whose wave layout, online softmax
+ * and half combine it keeps).  Every fp32 operand x is split into fp16
+ * halves hi = fp16(x), lo = fp16(x - hi) (split_store), and each product
+ * of two split operands is hi.hi + hi.lo + lo.hi on v_mfma_f32_16x16x32_f16
+ * (fp32 accumulate; the dropped lo.lo term is below fp32 rounding of the
+ * sum): 48 matrix instructions of 16 cycles per wave and 64-key block
+ * instead of 128 of 32.
+ *
+ * Operand layouts (v_mfma_f32_16x16x32_f16: lane l supplies
+ * A[l%16][8(l/16)..+7] and B[8(l/16)..+7][l%16]; D[4(l/16)+r][l%16]):
+ *   Q  A operand, from global (rows of the block, dims 32s + 8(l/16)..+7);
+ *   K  staged as [key][dim] halves (the B operand of S = Q K^T is 8
+ *      consecutive dims of one key, one 16-byte LDS read);
+ *   V  staged as [dim][key] halves (B of O = P V: 8 consecutive keys of
+ *      one dim);
+ *   P  written in fp32 as [row][key] and read back as the A operand (8
+ *      consecutive keys of one row), split after the read.
+ * Row pitch 72 halves (144 bytes): the 16 lanes of a 16-byte read or write
+ * pass start 36 dwords apart, which covers the 64 banks once. */
+extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_attnp_args a)
+{
+    constexpr int KP = 72, LDP = 68;
+    constexpr int TILE = 64 * KP; /* halves per staged array */
+    /* per half hs: Kh, Kl, Vh, Vl at (4 hs + 0..3) * TILE */
+    __shared__ __attribute__((aligned(16))) _Float16 kvs[8 * TILE];
+    __shared__ __attribute__((aligned(16))) float Ps[8][16 * LDP];
+    const int h = blockIdx.x, qb = blockIdx.y, tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
+    const int rg = wave & 3, hs = wave >> 2;
+    if (h >= a.NH || qb * 64 >= a.P) return;
+    const int E = a.E, P = a.P;
+    f16x8 qh[2], ql[2];
+    {
+        const int i = min(qb * 64 + 16 * rg + lr, P - 1);
+        const float *qp = a.q + (size_t)i * E + h * 64 + 8 * lg;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const f32x4 x0 = *(const f32x4 *)(qp + 32 * s2), x1 = *(const f32x4 *)(qp + 32 * s2 + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                qh[s2][e] = hi16(x0[e]); ql[s2][e] = lo16(x0[e]);
+                qh[s2][4 + e] = hi16(x1[e]); ql[s2][4 + e] = lo16(x1[e]);
+            }
+        }
+    }
+    f32x4 o[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) o[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    float m[4], l[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { m[r] = -INFINITY; l[r] = 0.f; }
+    const int i_base = qb * 64 + 16 * rg + 4 * lg;
+    /* staging (per half, 256 threads): K: key sj = t % 64, dims 16 sc..+15;
+     * V: dim sj, keys 16 sc..+15; 4-byte loads, consecutive lanes read
+     * consecutive words */
+    const int st_ = tid & 255, sj = st_ & 63, sc = st_ >> 6;
+    float kx[16], vx[16];
+    auto kvload = [&](int kb) {
+        const int jb = min(kb, qb) * 64;
+        const float *kp = a.k_cache + (size_t)(h * 64 + 16 * sc) * a.S + min(jb + sj, a.S - 1);
+#pragma unroll
+        for (int d = 0; d < 16; ++d) kx[d] = kp[(size_t)d * a.S];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) vx[k] = a.v_cache[(size_t)min(jb + 16 * sc + k, a.S - 1) * E + h * 64 + sj];
+    };
+    kvload(hs);
+    const int nit = (qb + 2) >> 1;
+    _Float16 *Kh = kvs + (4 * hs + 0) * TILE, *Kl = kvs + (4 * hs + 1) * TILE;
+    _Float16 *Vh = kvs + (4 * hs + 2) * TILE, *Vl = kvs + (4 * hs + 3) * TILE;
+    for (int it = 0; it < nit; ++it) {
+        const int kb = 2 * it + hs, j0 = kb * 64;
+        __syncthreads(); /* the previous blocks have been consumed */
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            f16x8 kh, kl, vh, vl;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                kh[e] = hi16(kx[8 * c + e]); kl[e] = lo16(kx[8 * c + e]);
+                vh[e] = hi16(vx[8 * c + e]); vl[e] = lo16(vx[8 * c + e]);
+            }
+            *(f16x8 *)(Kh + sj * KP + 16 * sc + 8 * c) = kh;
+            *(f16x8 *)(Kl + sj * KP + 16 * sc + 8 * c) = kl;
+            *(f16x8 *)(Vh + sj * KP + 16 * sc + 8 * c) = vh;
+            *(f16x8 *)(Vl + sj * KP + 16 * sc + 8 * c) = vl;
+        }
+        __syncthreads();
+        kvload(kb + 2);
+        if (kb > qb) continue; /* wave-uniform */
+        f32x4 sacc[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) sacc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        {
+            f16x8 bh[4][2], bl[4][2];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int s2 = 0; s2 < 2; ++s2) {
+                    bh[t][s2] = *(const f16x8 *)(Kh + (16 * t + lr) * KP + 32 * s2 + 8 * lg);
+                    bl[t][s2] = *(const f16x8 *)(Kl + (16 * t + lr) * KP + 32 * s2 + 8 * lg);
+                }
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[s2], bh[t][s2], sacc[t], 0, 0, 0);
+                    sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[s2], bl[t][s2], sacc[t], 0, 0, 0);
+                }
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[s2], bh[t][s2], sacc[t], 0, 0, 0);
+        }
+        float alpha[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = i_base + r;
+            float bm = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int j = j0 + 16 * t + lr;
+                const float v = (i < P && j <= i) ? sacc[t][r] * a.scale : -INFINITY;
+                sacc[t][r] = v;
+                bm = fmaxf(bm, v);
+            }
+            bm = row16_max(bm);
+            const float mn = fmaxf(m[r], bm);
+            const float ms = mn == -INFINITY ? 0.f : mn;
+            alpha[r] = expf(m[r] - ms);
+            float ps = 0.f;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float pv = expf(sacc[t][r] - ms);
+                sacc[t][r] = pv;
+                ps += pv;
+            }
+            l[r] = fmaf(l[r], alpha[r], row16_sum(ps));
+            m[r] = mn;
+        }
+        float *pw = Ps[wave];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pw[(4 * lg + r) * LDP + 16 * t + lr] = sacc[t][r];
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[t][r] *= alpha[r];
+        f16x8 ph[2], pl[2];
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+            const f32x4 x0 = *(const f32x4 *)(pw + lr * LDP + 32 * s2 + 8 * lg);
+            const f32x4 x1 = *(const f32x4 *)(pw + lr * LDP + 32 * s2 + 8 * lg + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                ph[s2][e] = hi16(x0[e]); pl[s2][e] = lo16(x0[e]);
+                ph[s2][4 + e] = hi16(x1[e]); pl[s2][4 + e] = lo16(x1[e]);
+            }
+        }
+        {
+            f16x8 bh[4][2], bl[4][2];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int s2 = 0; s2 < 2; ++s2) {
+                    bh[t][s2] = *(const f16x8 *)(Vh + (16 * t + lr) * KP + 32 * s2 + 8 * lg);
+                    bl[t][s2] = *(const f16x8 *)(Vl + (16 * t + lr) * KP + 32 * s2 + 8 * lg);
+                }
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[s2], bh[t][s2], o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s2], bl[t][s2], o[t], 0, 0, 0);
+                }
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s2], bh[t][s2], o[t], 0, 0, 0);
+        }
+    }
+    __syncthreads();
+    float *xw = (float *)kvs + (size_t)(rg * 64 + lane) * 24;
     if (hs == 1) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {

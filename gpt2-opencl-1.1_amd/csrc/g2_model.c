@@ -1009,6 +1009,8 @@ static int fused_prefill(g2_model *m, int P)
     g2_embed_args e = { m->wte, m->wpe, m->hidden, m->ids_dev, NULL, E, P, 0 };
     int rc = g2i_launch(f16 ? G2F_EMBED_F16 : G2F_EMBED_F32, cdivu(E, 256), (unsigned)P, 256, &e);
     int ln1_done = 0; /* the previous layer's fc2 sum already wrote this layer's ln_1 */
+    const char *ea = getenv("G2_PREFILL_ATTN32");
+    const int attn32 = ea && ea[0] == '1'; /* attention on the fp32 matrix cores (reference point) */
     for (int l = 0; l < m->cfg.n_layer && !rc; ++l) {
         g2_layer *y = &m->L[l];
         g2_lnsplit_args ls = { m->hidden, ln_h, ln_l, y->ln1_w, y->ln1_b, E, P };
@@ -1024,7 +1026,7 @@ static int fused_prefill(g2_model *m, int P)
                           : g2i_launch(f_qkv, cdivu(3 * E, 64), cdivu(P, 64), 256, &g);
         g2_attnp_args t = { m->q, y->k_cache, y->v_cache, m->attn, P, E, NH, G2_KV_MAX_SEQ, 1.0f / sqrtf(64.0f),
                             big ? at_h : NULL, big ? at_l : NULL };
-        if (!rc) rc = g2i_launch(G2F_ATTN_PREFILL_MFMA, (unsigned)NH, cdivu(P, 64), 512, &t);
+        if (!rc) rc = g2i_launch(attn32 ? G2F_ATTN_PREFILL_MFMA : G2F_ATTN_PREFILL_H16, (unsigned)NH, cdivu(P, 64), 512, &t);
         memset(&g, 0, sizeof g);
         g.A = m->attn; g.B = y->proj_w; g.bias = y->proj_b; g.C = m->hidden; g.M = P; g.N = E; g.K = E;
         int ln2_done = 0;

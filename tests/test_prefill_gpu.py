@@ -63,3 +63,24 @@ def test_prefill_gemm_tiles_agree(g2, monkeypatch, P):
         out.append(m.logits().copy())
         m.free()
     np.testing.assert_allclose(out[0], out[1], rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("P", [1, 63, 64, 65, 200, 512, 1023])
+def test_prefill_attention_h16_matches_f32(g2, monkeypatch, P):
+    """The prompt attention on the fp16 matrix cores (operands split into
+    fp16 halves, three products per pair) against the same attention on the
+    fp32 matrix cores (G2_PREFILL_ATTN32=1): the logits agree to fp32
+    rounding of the attention output (1e-4); both runs are checked against
+    the oracle elsewhere."""
+    cfg = g2.make_config(2, 1600, 25, vocab_size=50257)
+    w = g2.synth_weights(cfg, SEED, f16_round=True)
+    prompt = random_prompt(P, cfg.vocab_size, 300 + P)
+    print(f"[prefill] XL width L2, P {P}: attention fp16-split vs fp32 matrix cores", flush=True)
+    out = []
+    for v in ("0", "1"):
+        monkeypatch.setenv("G2_PREFILL_ATTN32", v)
+        m = g2.Model.from_host(cfg, w, g2.F16, g2.PATH_FUSED)
+        m.prefill(prompt)
+        out.append(m.logits().copy())
+        m.free()
+    np.testing.assert_allclose(out[0], out[1], rtol=1e-4, atol=1e-4)
