@@ -810,49 +810,69 @@ G2K_HG2 void g2k_hgemm2_partial(const g2_gemm_args a) { hgemm2_impl<GEPI_PARTIAL
  * halves of the next GEMM's operand. */
 G2K void g2k_splitk_resid_ln(const g2_skred_args a)
 {
-    constexpr int PT = G2_SKLN_MAXN / 256;
+    /* thread t owns the 4-column groups t and t + 256 of the row (N % 4 ==
+     * 0, N <= G2_SKLN_MAXN); every load of both groups -- all slices, the
+     * residual, bias and LayerNorm parameters -- is issued before the
+     * first sum (unconditional, clamped into the row), so the row costs
+     * one memory latency instead of one per group */
+    constexpr int PG = G2_SKLN_MAXN / 1024; /* groups per thread */
+    constexpr int ZMAX = 8;                  /* slices read at once (ks <= ZMAX) */
     __shared__ float red4[4];
-    const int m = blockIdx.x, N = a.N;
+    const int m = blockIdx.x, N = a.N, NG = N >> 2;
     if (m >= a.M) return;
     const size_t MN = (size_t)a.M * N, row = (size_t)m * N;
-    constexpr int ZMAX = 8; /* slices read at once (ks <= ZMAX) */
-    float xv[PT];
+    f32x4 pz[PG][ZMAX], cv[PG], bv[PG], gv[PG], ev[PG];
+#pragma unroll
+    for (int k = 0; k < PG; ++k) {
+        const int g = min((int)threadIdx.x + 256 * k, NG - 1);
+#pragma unroll
+        for (int z = 0; z < ZMAX; ++z)
+            pz[k][z] = *(const f32x4 *)(a.part + (size_t)min(z, a.ks - 1) * MN + row + 4 * g);
+        cv[k] = *(const f32x4 *)(a.C + row + 4 * g);
+        bv[k] = a.bias ? *(const f32x4 *)(a.bias + 4 * g) : (f32x4){0.f, 0.f, 0.f, 0.f};
+        gv[k] = *(const f32x4 *)(a.ln_g + 4 * g);
+        ev[k] = *(const f32x4 *)(a.ln_b + 4 * g);
+    }
+    f32x4 xv[PG];
     float s = 0.f;
 #pragma unroll
-    for (int k = 0; k < PT; ++k) {
-        const int n = threadIdx.x + 256 * k;
-        xv[k] = 0.f;
-        if (n < N) {
-            /* every slice's load issued before the first sum */
-            float pz[ZMAX];
+    for (int k = 0; k < PG; ++k) {
+        const int g = (int)threadIdx.x + 256 * k;
+        /* slices in order, then bias, then the residual (the order of the
+         * unfused splitk_resid) */
+        f32x4 v = pz[k][0];
 #pragma unroll
-            for (int z = 0; z < ZMAX; ++z) pz[z] = z < a.ks ? a.part[(size_t)z * MN + row + n] : 0.f;
-            const float c = a.C[row + n];
-            float v = pz[0];
-#pragma unroll
-            for (int z = 1; z < ZMAX; ++z)
-                if (z < a.ks) v += pz[z];
-            if (a.bias) v += a.bias[n];
-            v = v + c;
-            a.C[row + n] = v;
-            xv[k] = v;
-            s += v;
+        for (int z = 1; z < ZMAX; ++z)
+            if (z < a.ks) v += pz[k][z];
+        v += bv[k];
+        v += cv[k];
+        xv[k] = v;
+        if (g < NG) {
+            *(f32x4 *)(a.C + row + 4 * g) = v;
+            s += ((v.x + v.y) + v.z) + v.w;
         }
     }
     const float mean = block_sum(s, red4) / (float)N;
     float q = 0.f;
 #pragma unroll
-    for (int k = 0; k < PT; ++k)
-        if (threadIdx.x + 256 * k < N) {
-            const float d = xv[k] - mean;
-            q = fmaf(d, d, q);
+    for (int k = 0; k < PG; ++k)
+        if ((int)threadIdx.x + 256 * k < NG) {
+            const f32x4 d = xv[k] - mean;
+            q = fmaf(d.x, d.x, q);
+            q = fmaf(d.y, d.y, q);
+            q = fmaf(d.z, d.z, q);
+            q = fmaf(d.w, d.w, q);
         }
     const float var = block_sum(q, red4) / (float)N;
     const float inv = 1.0f / sqrtf(var + 1e-5f);
 #pragma unroll
-    for (int k = 0; k < PT; ++k) {
-        const int n = threadIdx.x + 256 * k;
-        if (n < N) split_store(a.hi, a.lo, row + n, fmaf((xv[k] - mean) * inv, a.ln_g[n], a.ln_b[n]));
+    for (int k = 0; k < PG; ++k) {
+        const int g = (int)threadIdx.x + 256 * k;
+        if (g < NG) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                split_store(a.hi, a.lo, row + 4 * g + e, fmaf((xv[k][e] - mean) * inv, gv[k][e], ev[k][e]));
+        }
     }
 }
 
