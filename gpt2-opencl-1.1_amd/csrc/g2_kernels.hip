@@ -379,6 +379,45 @@ extern "C" __global__ __launch_bounds__(1024) void g2k_attn_out(const g2_attnout
  * ==================================================================== */
 enum { GEPI_STORE = 0, GEPI_GELU = 1, GEPI_RESID = 2, GEPI_QKV = 3, GEPI_PARTIAL = 4, GEPI_GELU_SPLIT = 5 };
 
+/* Bias (and for GEPI_RESID the old C) added to a wave's 32x32 tile in one
+ * branch-free pass before its stores, every load issued before the first
+ * add: a load's wait placed among the stores would also wait for every
+ * store issued before it (stores count in the same counter), once per
+ * element.  mb, nb: the tile's first row and column. */
+template <int EPI>
+__device__ __forceinline__ void epi_add(f32x4 (&acc)[2][2], const g2_gemm_args &a, int mb, int nb, int lane, int M,
+                                        int N)
+{
+    if constexpr (EPI != GEPI_PARTIAL) {
+        float bj[2] = {0.f, 0.f};
+        if (a.bias) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) bj[j] = a.bias[min(nb + j * 16 + (lane & 15), N - 1)];
+        }
+        float rv[2][2][4];
+        if constexpr (EPI == GEPI_RESID) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        rv[i][j][q] = a.C[(size_t)min(mb + i * 16 + 4 * (lane >> 4) + q, M - 1) * N +
+                                          min(nb + j * 16 + (lane & 15), N - 1)];
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    acc[i][j][q] += bj[j];
+                    if constexpr (EPI == GEPI_RESID) acc[i][j][q] += rv[i][j][q];
+                    asm volatile("" : "+v"(acc[i][j][q])); /* not sunk into the stores */
+                }
+    }
+}
+
 template <typename BT, bool BNK, int EPI>
 __device__ void gemm_impl(const g2_gemm_args &a)
 {
@@ -456,6 +495,7 @@ __device__ void gemm_impl(const g2_gemm_args &a)
         __syncthreads();
     }
 
+    epi_add<EPI>(acc, a, m0 + wm * 32, n0 + wn * 32, lane, M, N);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -465,14 +505,13 @@ __device__ void gemm_impl(const g2_gemm_args &a)
                 const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
                 const int n = n0 + wn * 32 + j * 16 + (lane & 15);
                 if (m >= M || n >= N) continue;
-                float v = acc[i][j][r];
-                if (a.bias) v += a.bias[n];
+                const float v = acc[i][j][r];
                 if (EPI == GEPI_STORE) {
                     a.C[(size_t)m * N + n] = v;
                 } else if (EPI == GEPI_GELU) {
                     a.C[(size_t)m * N + n] = gelu_f(v);
                 } else if (EPI == GEPI_RESID) {
-                    a.C[(size_t)m * N + n] = v + a.C[(size_t)m * N + n];
+                    a.C[(size_t)m * N + n] = v;
                 } else {
                     const int E = a.E, pos = a.pos0 + m;
                     if (n < E) a.q_out[(size_t)m * E + n] = v;
@@ -595,6 +634,7 @@ __device__ void hgemm_impl(const g2_gemm_args &a)
         }
     }
 
+    epi_add<EPI>(acc, a, m0 + wm * 32, n0 + wn * 32, lane, M, N);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -604,18 +644,17 @@ __device__ void hgemm_impl(const g2_gemm_args &a)
                 const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + q;
                 const int n = n0 + wn * 32 + j * 16 + (lane & 15);
                 if (m >= M || n >= N) continue;
-                float v = acc[i][j][q];
+                const float v = acc[i][j][q];
                 if (EPI == GEPI_PARTIAL) {
                     a.part[(size_t)blockIdx.z * M * N + (size_t)m * N + n] = v;
                     continue;
                 }
-                if (a.bias) v += a.bias[n];
                 if (EPI == GEPI_STORE) {
                     a.C[(size_t)m * N + n] = v;
                 } else if (EPI == GEPI_GELU) {
                     a.C[(size_t)m * N + n] = gelu_f(v);
                 } else if (EPI == GEPI_RESID) {
-                    a.C[(size_t)m * N + n] = v + a.C[(size_t)m * N + n];
+                    a.C[(size_t)m * N + n] = v;
                 } else {
                     const int E = a.E, pos = a.pos0 + m;
                     if (n < E) a.q_out[(size_t)m * E + n] = v;
@@ -754,6 +793,14 @@ __device__ void hgemm2_impl(const g2_gemm_args &a)
         __builtin_amdgcn_global_load_lds(bsrc + k, (lds_t *)(st + 2 * TB), 16, 0, 0);
     };
 
+    /* the epilogue's bias values (two columns per lane), loaded before the
+     * tiles so they land during the loop (the loop's waits count only the
+     * tile loads issued after them) */
+    float bj[2] = {0.f, 0.f};
+    if (EPI != GEPI_PARTIAL && a.bias) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) bj[j] = a.bias[min(n0 + wn * 32 + j * 16 + (lane & 15), N - 1)];
+    }
     issue(0, 0);
     issue(1, 1);
     int cur = 0;
@@ -767,6 +814,38 @@ __device__ void hgemm2_impl(const g2_gemm_args &a)
     /* no load may land in LDS after the work-group has ended */
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+    /* the residual epilogue's loads, all issued before the first use
+     * (clamped into the matrix) */
+    float rv[2][2][4];
+    if constexpr (EPI == GEPI_RESID) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int m = min(m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + q, M - 1);
+                    const int n = min(n0 + wn * 32 + j * 16 + (lane & 15), N - 1);
+                    rv[i][j][q] = a.C[(size_t)m * N + n];
+                }
+    }
+    /* bias and residual added in one branch-free pass before the first
+     * store: a load's wait placed among the stores would also wait for
+     * every store before it (stores count in the same counter) */
+    if constexpr (EPI != GEPI_PARTIAL) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    acc[i][j][q] += bj[j];
+                    if constexpr (EPI == GEPI_RESID) acc[i][j][q] += rv[i][j][q];
+                    /* keeps the add here (the compiler would sink it, and its
+                     * wait, into the conditional store below) */
+                    asm volatile("" : "+v"(acc[i][j][q]));
+                }
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -776,16 +855,15 @@ __device__ void hgemm2_impl(const g2_gemm_args &a)
                 const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + q;
                 const int n = n0 + wn * 32 + j * 16 + (lane & 15);
                 if (m >= M || n >= N) continue;
-                float v = acc[i][j][q];
+                const float v = acc[i][j][q];
                 if (EPI == GEPI_PARTIAL) {
                     a.part[(size_t)blockIdx.z * M * N + (size_t)m * N + n] = v;
                     continue;
                 }
-                if (a.bias) v += a.bias[n];
                 if (EPI == GEPI_GELU_SPLIT) {
                     split_store(a.Ch, a.Cl, (size_t)m * N + n, gelu_f(v));
                 } else if (EPI == GEPI_RESID) {
-                    a.C[(size_t)m * N + n] = v + a.C[(size_t)m * N + n];
+                    a.C[(size_t)m * N + n] = v;
                 } else {
                     const int E = a.E, pos = a.pos0 + m;
                     if (n < E) a.q_out[(size_t)m * E + n] = v;
