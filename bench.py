@@ -94,9 +94,11 @@ def measured_traffic(kernel, workload):
     return t.get("bytes_per_launch")
 
 
-def cpu_baseline(g2, m, cfg, token, n_steps=4):
-    """Time the oracle on the same workload sample: n_steps decode forwards
-    at positions 512.. over the GPU-prefilled KV cache."""
+def cpu_baseline(g2, m, cfg, token, min_seconds=10.0, max_steps=400):
+    """Time the oracle on a bounded sample of the same workload: decode
+    forwards at positions 513.. over the GPU-prefilled KV cache, as many as
+    fit in min_seconds of CPU work (at most max_steps, and never past the
+    last cache position)."""
     sys.path.insert(0, ROOT)
     from oracle import oracle
     t0 = time.perf_counter()
@@ -109,10 +111,13 @@ def cpu_baseline(g2, m, cfg, token, n_steps=4):
     log(f"cpu oracle ready in {time.perf_counter() - t0:.1f}s")
     om.decode(token, PROMPT_LEN)  # untimed first forward (page-in)
     tok = om.greedy([token], forbid_eos=True)
+    max_steps = min(max_steps, 1022 - PROMPT_LEN)
     t0 = time.perf_counter()
-    for s in range(n_steps):
-        om.decode(tok, PROMPT_LEN + 1 + s)
+    n_steps = 0
+    while n_steps < max_steps and (n_steps == 0 or time.perf_counter() - t0 < min_seconds):
+        om.decode(tok, PROMPT_LEN + 1 + n_steps)
         tok = om.greedy([tok], forbid_eos=True)
+        n_steps += 1
     dt = time.perf_counter() - t0
     cores = oracle.num_threads()
     om.close()
