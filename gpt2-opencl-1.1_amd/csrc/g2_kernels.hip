@@ -1260,6 +1260,10 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_mfma(const g2
  * sum): 48 matrix instructions of 16 cycles per wave and 64-key block
  * instead of 128 of 32.
  *
+ * The online softmax works in base 2 (scores times log2 e, v_exp_f32),
+ * the usual flash-attention form; the probabilities equal exp() of the
+ * natural-base scores to fp32 rounding.
+ *
  * Operand layouts (v_mfma_f32_16x16x32_f16: lane l supplies
  * A[l%16][8(l/16)..+7] and B[8(l/16)..+7][l%16]; D[4(l/16)+r][l%16]):
  *   Q  A operand, from global (rows of the block, dims 32s + 8(l/16)..+7);
@@ -1282,6 +1286,9 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
     const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
     const int rg = wave & 3, hs = wave >> 2;
     if (h >= a.NH || qb * 64 >= a.P) return;
+    /* scores in base-2 units (scaled by log2 e): the softmax's
+     * exponentials are single v_exp_f32 instructions */
+    const float scale2 = a.scale * 1.4426950408889634f;
     const int E = a.E, P = a.P;
     f16x8 qh[2], ql[2];
     {
@@ -1373,18 +1380,18 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const int j = j0 + 16 * t + lr;
-                const float v = (i < P && j <= i) ? sacc[t][r] * a.scale : -INFINITY;
+                const float v = (i < P && j <= i) ? sacc[t][r] * scale2 : -INFINITY;
                 sacc[t][r] = v;
                 bm = fmaxf(bm, v);
             }
             bm = row16_max(bm);
             const float mn = fmaxf(m[r], bm);
             const float ms = mn == -INFINITY ? 0.f : mn;
-            alpha[r] = expf(m[r] - ms);
+            alpha[r] = __builtin_amdgcn_exp2f(m[r] - ms);
             float ps = 0.f;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                const float pv = expf(sacc[t][r] - ms);
+                const float pv = __builtin_amdgcn_exp2f(sacc[t][r] - ms);
                 sacc[t][r] = pv;
                 ps += pv;
             }
@@ -1453,8 +1460,8 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
     for (int r = 0; r < 4; ++r) {
         const float m1 = xw[r], l1 = xw[4 + r];
         const float mx = fmaxf(m[r], m1);
-        const float f0 = m[r] == -INFINITY ? 0.f : expf(m[r] - mx);
-        const float f1 = m1 == -INFINITY ? 0.f : expf(m1 - mx);
+        const float f0 = m[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[r] - mx);
+        const float f1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mx);
         l[r] = l[r] * f0 + l1 * f1;
 #pragma unroll
         for (int t = 0; t < 4; ++t) o[t][r] = o[t][r] * f0 + xw[8 + 4 * t + r] * f1;
