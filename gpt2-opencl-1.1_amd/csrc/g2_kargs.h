@@ -30,6 +30,9 @@ enum {
 
 /* G2S_ERR bits */
 #define G2_ERR_STEP_TIMEOUT 4 /* a step-kernel exchange wait ran out of time */
+/* a plain (not cooperative) launch of the step kernel found its work-groups
+ * not all resident and did nothing; later launches skip until it is cleared */
+#define G2_ERR_STEP_NOT_RESIDENT 8
 
 /* GEMM: C[M,N] = A[M,K] * op(B) with an epilogue.
  * B layout G2_BKN: [K,N] row-major (the reference's device layout);
@@ -236,6 +239,11 @@ typedef struct {
     int L, E, F, NH, V, S;
     int xlayer; /* words per layer region */
     float scale;
+    /* g2k_step_f16/f32 only: 0 cooperative launch; 1 plain launch, so the
+     * kernel checks that all its work-groups are resident before its first
+     * lasting write; 2 as 1 with work-group 1 withholding its arrival (a test
+     * of the not-resident path) */
+    int plain;
 } g2_step_args;
 
 #define G2_TRACE_STRIDE(L) (24 * (L) + 8)
@@ -264,9 +272,13 @@ typedef struct {
 #define G2X_H(E, NH) (G2X_X1(E, NH) + (E))
 #define G2X_X2(E, NH, F) (G2X_H(E, NH) + (F))
 #define G2X_LAYER_WORDS(E, NH, F) ((G2X_X2(E, NH, F) + (E) + 31) & ~31)
-/* Total words: header, L layer regions, 2 argmax words per work-group. */
+/* Total words: header, L layer regions, 2 argmax words per work-group, 32
+ * spare words, 1 arrival word per work-group. */
 #define G2X_TOTAL_WORDS(L, E, NH, F, nwg) \
-    ((long)G2X_HEAD + (long)(L) * G2X_LAYER_WORDS(E, NH, F) + 2L * (nwg) + 32)
+    ((long)G2X_HEAD + (long)(L) * G2X_LAYER_WORDS(E, NH, F) + 3L * (nwg) + 32)
+/* after the layers: 2 argmax words per work-group, 32 spare words, then one
+ * arrival word per work-group (plain launches) */
+#define G2X_ARRIVE(L, xlayer, nwg) ((long)G2X_HEAD + (long)(L) * (xlayer) + 2L * (nwg) + 32)
 
 /* XCD-parallel decode step (same arguments as g2_step_args; layout below).
  * A work-group reads its XCD from the hardware; its rank within the XCD is

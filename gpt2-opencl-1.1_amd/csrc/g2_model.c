@@ -60,6 +60,8 @@ struct g2_model {
     int stepx;     /* ... in its XCD-parallel form */
     int step3;     /* ... in its two-role form */
     int step4;     /* ... in its loader-wave form */
+    int plain;     /* the all-to-all form's launches are plain, not cooperative (2: test
+                      hook, work-group 1 withholds its arrival) */
     int step_ran;  /* a step kernel ran since the last error check */
     const char *step_why; /* why the step kernel cannot run this model */
     unsigned long long *trace; /* phase timestamps, when G2_STEP_TRACE names a file */
@@ -310,6 +312,11 @@ static int step_setup(g2_model *m)
     m->stepx = envx && envx[0] == '1' && g2i_stepx_ok() && stepx_supported(m, nwg);
     const char *env4 = getenv("G2_STEP4");
     m->step4 = !m->step3 && !m->stepx && env4 && env4[0] == '1' && g2i_step4_ok() && step4_supported(m, nwg);
+    /* A cooperative launch costs ~17 us more than a plain one between
+     * back-to-back steps (1.4% of an XL token); the all-to-all kernel checks
+     * residency itself, so it is launched plain unless G2_STEP_COOP=1. */
+    const char *envc = getenv("G2_STEP_COOP"), *envw = getenv("G2_STEP_TEST_WITHHOLD");
+    m->plain = envc && envc[0] == '1' ? 0 : (envw && envw[0] == '1' ? 2 : 1);
     const long w1 = G2X_TOTAL_WORDS(L, c->n_embd, c->n_head, c->ffn_dim, nwg);
     const int HX = (c->n_head + G2_NXCD - 1) / G2_NXCD, FX = (c->ffn_dim + G2_NXCD - 1) / G2_NXCD;
     const long w2 = G2XX_TOTAL_WORDS(L, HX, c->n_embd, FX, nwg);
@@ -851,26 +858,41 @@ static int step_launch(g2_model *m)
     }
     a.xlayer = G2X_LAYER_WORDS(c->n_embd, c->n_head, c->ffn_dim);
     if (m->step4) return g2i_coop_launch(G2F_STEP4_F16, (unsigned)m->step_wgs, G2_STEP4_THREADS, &a);
-    return g2i_coop_launch(m->dtype == G2_F16 ? G2F_STEP_F16 : G2F_STEP_F32, (unsigned)m->step_wgs,
-                           G2_STEP_THREADS, &a);
+    const int fid = m->dtype == G2_F16 ? G2F_STEP_F16 : G2F_STEP_F32;
+    if (m->plain) {
+        a.plain = m->plain;
+        return g2i_launch(fid, (unsigned)m->step_wgs, 1, G2_STEP_THREADS, &a);
+    }
+    return g2i_coop_launch(fid, (unsigned)m->step_wgs, G2_STEP_THREADS, &a);
 }
 
-/* After step kernels ran: fail if one of them abandoned a hand-off (its
- * outputs are then invalid) and clear the exchange area for the next run. */
-static int step_check(g2_model *m, const int *state_words)
+static int fused_step(g2_model *m);
+
+/* After step kernels ran, ngen_target = state[G2S_NGEN] once the run is
+ * complete.  A plain launch that found its grid not resident did nothing
+ * and made the later launches of the run skip: clear the flag and the
+ * exchange area, switch this model to cooperative launches and run the
+ * missing steps.  Fail if a step abandoned a hand-off (its outputs are
+ * then invalid) and clear the exchange area for the next run. */
+static int step_check(g2_model *m, int ngen_target)
 {
     if (!m->step_ran) return G2_OK;
     m->step_ran = 0;
-    int err = 0, rc = G2_OK;
-    if (state_words) err = state_words[G2S_ERR];
-    else {
-        rc = g2i_hip(hipMemcpyAsync(&err, m->state + G2S_ERR, sizeof err, hipMemcpyDeviceToHost,
-                                    g2i_stream()), "step check");
-        if (!rc) rc = g2i_hip(hipStreamSynchronize(g2i_stream()), "step check sync");
-        if (rc) return rc;
+    int w[G2S_SEQ + 1];
+    int rc = g2i_hip(hipMemcpyAsync(w, m->state, sizeof w, hipMemcpyDeviceToHost, g2i_stream()), "step check");
+    if (!rc) rc = g2i_hip(hipStreamSynchronize(g2i_stream()), "step check sync");
+    if (rc) return rc;
+    const int err = w[G2S_ERR], zero = 0;
+    if (err & G2_ERR_STEP_NOT_RESIDENT) {
+        rc = g2i_hip(hipMemsetAsync(m->xbuf, 0, m->xbuf_bytes, g2i_stream()), "exchange clear");
+        if (!rc) rc = up(m->state + G2S_ERR, &zero, sizeof zero);
+        m->plain = 0;
+        fprintf(stderr, "g2: decode step kernel: work-groups of a plain launch were not all resident; "
+                        "resuming with cooperative launches\n");
+        for (int s = w[G2S_NGEN]; s < ngen_target && !rc; ++s) rc = fused_step(m);
+        return rc ? rc : step_check(m, ngen_target);
     }
     if (!(err & G2_ERR_STEP_TIMEOUT)) return G2_OK;
-    const int zero = 0;
     rc = g2i_hip(hipMemsetAsync(m->xbuf, 0, m->xbuf_bytes, g2i_stream()), "exchange clear");
     if (!rc) rc = up(m->state + G2S_ERR, &zero, sizeof zero);
     if (rc) return rc;
@@ -1081,7 +1103,7 @@ int g2_decode(g2_model *m, int token, int pos)
     }
     int rc = set_state(m, pos, token, 0, 0);
     if (!rc) rc = fused_step(m);
-    return rc ? rc : step_check(m, NULL);
+    return rc ? rc : step_check(m, 1);
 }
 
 int g2_read_logits(g2_model *m, float *host, int n)
@@ -1186,13 +1208,13 @@ int g2_generate(g2_model *m, const int *prompt, int n_prompt, int max_new, int m
     if (m->events_ok) hipEventRecord(m->ev[1], g2i_stream());
     for (int s = 0; s < n_dec && !rc; ++s) rc = fused_step(m);
     if (m->events_ok) hipEventRecord(m->ev[2], g2i_stream());
+    if (!rc) rc = step_check(m, 1 + n_dec); /* the prefill's pick + n_dec steps */
     if (rc) return rc;
     int *st = malloc((size_t)G2S_WORDS * sizeof(int));
     if (!st) return g2i_err(G2_E_NOMEM, "state readback");
     rc = g2i_hip(hipMemcpyAsync(st, m->state, (size_t)G2S_WORDS * sizeof(int), hipMemcpyDeviceToHost,
                                 g2i_stream()), "state readback");
     if (!rc) rc = g2i_hip(hipStreamSynchronize(g2i_stream()), "state sync");
-    if (!rc) rc = step_check(m, st);
     int gen = 0;
     if (!rc) {
         const int total = 1 + n_dec;
@@ -1220,7 +1242,7 @@ int g2_decode_run(g2_model *m, int token, int start_pos, int n_steps, int forbid
     for (int s = 0; s < n_steps && !rc; ++s) rc = fused_step(m);
     if (m->events_ok) hipEventRecord(m->ev[1], g2i_stream());
     if (!rc) rc = g2i_hip(hipStreamSynchronize(g2i_stream()), "decode run sync");
-    if (!rc) rc = step_check(m, NULL);
+    if (!rc) rc = step_check(m, n_steps);
     if (!rc) rc = step_trace_dump(m);
     if (rc) return rc;
     if (elapsed_ms) *elapsed_ms = ev_ms(m, 0, 1);

@@ -41,8 +41,14 @@
  * Every wait is bounded in time: a wait that runs out (100 ms) sets
  * G2_ERR_STEP_TIMEOUT in the state and raises the abort word, after which
  * every wait of every work-group returns at once, so the grid always
- * drains.  The launch is cooperative (all work-groups co-resident), so no
- * wait depends on a work-group that has not started.
+ * drains.  No wait may depend on a work-group that has not started, so all
+ * work-groups must be resident at once.  A cooperative launch guarantees
+ * that; a plain launch (a.plain, ~17 us less between back-to-back steps)
+ * is checked instead: each work-group posts an arrival word at its start
+ * and, before its first lasting write, confirms that every work-group has
+ * arrived and none gave up (grid_resident); otherwise the launch writes
+ * nothing, sets G2_ERR_STEP_NOT_RESIDENT and the host resumes the run with
+ * cooperative launches.
  */
 
 namespace g2step {
@@ -654,6 +660,47 @@ __device__ __forceinline__ int fresh_tid()
     return t;
 }
 
+/* Plain launches (not cooperative): before its first lasting write (the
+ * K/V cache entries of layer 0), a work-group checks that every work-group
+ * of the grid has posted its arrival word, i.e. is resident at the same
+ * time, and that none has given up.  A work-group that waits longer than
+ * RESIDENT_LIMIT gives up: it sets G2_ERR_STEP_NOT_RESIDENT, raises the
+ * abort word and exits, and so does every work-group that sees the abort
+ * word after its own arrivals were complete (a work-group that only got a
+ * CU when another exited finds all arrival words posted, but the abort word
+ * raised before that exit).  No work-group of such a launch writes the
+ * caches, the logits or the state.  Returns false for such a launch; all
+ * threads take part and get the same answer. */
+constexpr unsigned long long RESIDENT_LIMIT = 100000ull; /* 1 ms */
+
+__device__ __forceinline__ bool grid_resident(int tid, const ctx &c, const u64 *arr, int nwg, lds_flag *flag)
+{
+    if (tid == 0) *flag = 0;
+    __syncthreads();
+    for (int w = tid; w < nwg; w += NT) {
+        u64 v = ll_get(arr + w);
+        const u64 t0 = wall_clock64();
+        while (ll_tag(v) != c.tag) {
+            if (wall_clock64() - t0 > RESIDENT_LIMIT) { *flag = 1; break; }
+            __builtin_amdgcn_s_sleep(4);
+            v = ll_get(arr + w);
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        if (!*flag && ll_tag(ll_get(c.abort_w)) == c.tag) *flag = 1;
+        if (*flag) {
+            atomicOr(c.state + G2S_ERR, G2_ERR_STEP_NOT_RESIDENT);
+            ll_put(c.abort_w, 0.f, c.tag);
+            /* a read of the same word after the store: the abort is visible
+             * before this work-group exits and frees its CU */
+            if (ll_tag(ll_get(c.abort_w)) != c.tag) *flag = 2;
+        }
+    }
+    __syncthreads();
+    return *flag == 0;
+}
+
 /* LM head and greedy pick, the end of every step kernel: X2 of the last
  * layer (xlast: E words from nwg producers) -> LayerNorm_f -> logits of the
  * work-group's head rows -> first-max per work-group (argmax words AM) ->
@@ -743,6 +790,9 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     const int tok = clampi(a.state[G2S_TOK], 0, V - 1);
     const int ngen = a.state[G2S_NGEN], min_new = a.state[G2S_MIN_NEW];
     const unsigned seq = (unsigned)a.state[G2S_SEQ];
+    /* a plain launch earlier in this run found the grid not resident: skip
+     * until the host has resumed the run */
+    if (a.plain && (a.state[G2S_ERR] & G2_ERR_STEP_NOT_RESIDENT)) return;
     ctx c;
     c.tag = seq + 1u;
     c.abort_w = a.xbuf;
@@ -758,7 +808,11 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     {
         const G2_CONST g2_step_layer *LT0 = (const G2_CONST g2_step_layer *)a.layers;
         const int tid = fresh_tid();
-        if (tid == 0) dead = 0;
+        if (tid == 0) {
+            dead = 0;
+            if (a.plain && !(a.plain == 2 && wg == 1))
+                ll_put(a.xbuf + G2X_ARRIVE(a.L, a.xlayer, nwg) + wg, 0.f, c.tag);
+        }
         load_set<UMAX>(tid, wa, make_plan<WT>(LT0->qkv_w, 3 * E, E), 0);
         load_set<UPROJ>(tid, wp, make_plan<WT>(LT0->proj_w, E, E), 0);
         /* embedding of the token at its position (embed, math.cl:333-350) */
@@ -787,6 +841,9 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             TRACE(11);
             matvec<WT, UMAX>(tid, wa, p, xin, part);
             TRACE(12);
+            if (l == 0 && a.plain &&
+                !grid_resident(tid, c, a.xbuf + G2X_ARRIVE(a.L, a.xlayer, nwg), nwg, (lds_flag *)&flag))
+                return;
             if (tid < p.nrows) {
                 const int r = p.r0 + tid;
                 float v = row_sum(p, part, tid);

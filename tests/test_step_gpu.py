@@ -157,6 +157,50 @@ def test_step_decode_run_matches_generate(g2, stepx):
     m.free()
 
 
+def test_step_plain_launch_not_resident_resumes(g2, monkeypatch, capfd):
+    """The all-to-all kernel is launched plain (not cooperatively) and
+    checks that all its work-groups are resident before its first lasting
+    write.  Forced failure from the host (G2_STEP_TEST_WITHHOLD=1:
+    work-group 1 withholds its arrival word, so every work-group gives up
+    after 1 ms and writes nothing): the host resumes the run with
+    cooperative launches, and generate, a second generate and a single
+    decode give ids and logits bit-identical to cooperative launches only
+    (G2_STEP_COOP=1) and to plain launches."""
+    cfg = g2.make_config(3, 256, 4, vocab_size=1000)
+    w = g2.synth_weights(cfg, SEED, f16_round=True)
+    prompt = random_prompt(120, cfg.vocab_size, 31)
+    for k, v in ENV["a2a"].items():
+        monkeypatch.setenv(k, v)
+    outs = []
+    for env in ({"G2_STEP_COOP": "1"}, {"G2_STEP_TEST_WITHHOLD": "1"}, {}):
+        for k in ("G2_STEP_COOP", "G2_STEP_TEST_WITHHOLD"):
+            monkeypatch.delenv(k, raising=False)
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        print(f"[step] launch mode {env or 'plain'}", flush=True)
+        run = []
+        for _ in range(2):
+            m = g2.Model.from_host(cfg, w, g2.F16, g2.PATH_FUSED)
+            assert m.step_kind() == KIND_ID["a2a"]
+            if not run:
+                for _ in range(2):
+                    ids, _ = m.generate(prompt, 30, min_new=30)
+                    run += [ids.copy(), m.logits().copy()]
+            else:
+                m.prefill(prompt)
+                m.decode(int(run[0][0]), len(prompt))
+                run.append(m.logits().copy())
+            m.free()
+        err = capfd.readouterr().err
+        resumed = err.count("resuming with cooperative launches")
+        assert resumed == (2 if "G2_STEP_TEST_WITHHOLD" in env else 0), err
+        outs.append(run)
+    assert len(outs[0][0]) == 30
+    for o in outs[1:]:
+        for a, b in zip(outs[0], o):
+            np.testing.assert_array_equal(a, b)
+
+
 @pytest.mark.parametrize("stepx", [pytest.param("xcd", id="xcd"), pytest.param("two-role", id="two-role"),
                                    pytest.param("ring", id="loader-ring")], indirect=True)
 @pytest.mark.parametrize("cfg_args", [(2, 128, 2, 256), (3, 192, 3, 1000), (1, 64, 1, 50257)],
