@@ -209,7 +209,9 @@ int g2_model_uses_graph(const g2_model *m);
 /* Fused path decode engine.  By default (when the device supports
  * cooperative launch and the model fits the kernel: n_embd <= 1600, ffn <=
  * 6400) every decode forward is ONE launch of a persistent kernel that runs
- * all layers, the lm_head and the greedy pick; the environment variable
+ * all layers, the lm_head and the greedy pick (a plain launch that checks
+ * in the kernel that its work-groups are resident, else resumes the call
+ * with cooperative launches; G2_STEP_COOP=1 forces those); the variable
  * G2_STEP=0 or g2_model_set_step(m, 0) selects the per-operator kernels
  * instead.  Replaces the reference's per-op enqueue loop of decode()
  * (main.c:1792-1833) with no counterpart there.  The default is the
