@@ -883,7 +883,9 @@ static int step_check(g2_model *m, int ngen_target)
     if (!rc) rc = g2i_hip(hipStreamSynchronize(g2i_stream()), "step check sync");
     if (rc) return rc;
     const int err = w[G2S_ERR], zero = 0;
-    if (err & G2_ERR_STEP_NOT_RESIDENT) {
+    /* a timed-out hand-off (outputs invalid) is reported even if a later
+     * launch of the call also found its grid not resident */
+    if ((err & G2_ERR_STEP_NOT_RESIDENT) && !(err & G2_ERR_STEP_TIMEOUT)) {
         rc = g2i_hip(hipMemsetAsync(m->xbuf, 0, m->xbuf_bytes, g2i_stream()), "exchange clear");
         if (!rc) rc = up(m->state + G2S_ERR, &zero, sizeof zero);
         m->plain = 0;
