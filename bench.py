@@ -142,9 +142,9 @@ def main():
         return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} (WORLD_SIZE {world}) is not "
-              f"supported. The batch-1 decode shards by output columns across GPUs only in design "
-              f"(see DESIGN.md); run with --gpus 1.", file=sys.stderr)
+        print(f"bench.py: this library runs on one GPU only; --gpus {args.gpus} (WORLD_SIZE {world}) is not "
+              f"supported. Sharding the batch-1 decode by output columns across GPUs is designed but not "
+              f"built; run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import g2hip as g2
