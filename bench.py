@@ -192,7 +192,7 @@ def main():
     achieved = bytes_step / (step_ms_events * 1e-3) / 1e9
 
     kind = m.step_kind()
-    kname = ({1: "g2k_step", 2: "g2k_stepx", 3: "g2k_step3"}.get(kind, "") + ("_f16" if f16 else "_f32")) if kind else ""
+    kname = ("g2k_step_f16" if f16 else "g2k_step_f32") if kind else ""
     workload = (f"GPT-2 {args.config.upper()} {'fp16' if f16 else 'fp32'}-weight batch-1 greedy decode: {P}-token "
                 f"random prompt, {n_dec} decode forwards (positions {P}..{P + n_dec - 1})")
     result = {

@@ -53,10 +53,6 @@
     X(GEMM_NK_F16_QKV, "g2k_gemm_nk_f16_qkv")                                 \
     X(ATTN_PREFILL, "g2k_attn_prefill")                                       \
     X(STEP_F32, "g2k_step_f32") X(STEP_F16, "g2k_step_f16")                   \
-    X(STEPX_F32, "g2k_stepx_f32") X(STEPX_F16, "g2k_stepx_f16")               \
-    X(XCC_PROBE, "g2k_xcc_probe") X(STEP3_F16, "g2k_step3_f16")               \
-    X(STEP4_F16, "g2k_step4_f16")                                             \
-    X(TRANSPOSE16, "g2k_transpose16")                                         \
     X(HGEMM_STORE, "g2k_hgemm_store") X(HGEMM_GELU, "g2k_hgemm_gelu")         \
     X(HGEMM_RESID, "g2k_hgemm_resid") X(HGEMM_QKV, "g2k_hgemm_qkv")           \
     X(ATTN_PREFILL_MFMA, "g2k_attn_prefill_mfma")                             \
@@ -95,11 +91,6 @@ int g2i_coop_launch(int fid, unsigned gx, unsigned bx, void *args);
 int g2i_step_wgs(void);
 /* compute units of the device (after g2_init) */
 int g2i_cus(void);
-/* 1 if the XCD-parallel step kernel may run: its occupancy fits and a probe
- * launch found work-group w on XCD w % G2_NXCD for every w of the grid. */
-int g2i_stepx_ok(void);
-int g2i_step3_ok(void);
-int g2i_step4_ok(void);
 int g2i_device_alloc(void **p, size_t bytes);
 /* Launch a packed-matvec kernel: fid_f32_64 is the epilogue's first table
  * entry (f32, 64-lane shape); the lane shape and grid follow from K. */

@@ -216,9 +216,6 @@ typedef struct {
 typedef struct {
     const float *ln1_w, *ln1_b, *qkv_b, *proj_b, *ln2_w, *ln2_b, *fc_b, *fc2_b;
     const void *qkv_w, *proj_w, *fc_w, *fc2_w;
-    /* fc2 weights input-major [F][E] (the two-role kernel's K-split); NULL
-     * when that kernel is not set up */
-    const void *fc2_wt;
     float *k_cache, *v_cache;
 } g2_step_layer;
 
@@ -254,14 +251,6 @@ typedef struct {
 #define G2_STEP_MAXUNITS 512 /* (row, segment) units per work-group and phase */
 #define G2_STEP_MAXCH 16    /* 64-position key chunks per head */
 #define G2X_HEAD 64         /* words before the first layer region (word 0: abort) */
-/* Loader-wave decode step (g2k_step4_f16, same arguments and exchange
- * layout): 8 computing waves + 4 loader waves; weight rows pass through an
- * LDS ring of 1 KB blocks; lm_head rows go through it G2_STEP4_LM_ROWS at a
- * time.  Every matrix share must fit the ring. */
-#define G2_STEP4_THREADS 768
-#define G2_STEP4_RING_BLOCKS 104
-#define G2_STEP4_LM_ROWS 16
-
 /* Word offsets inside one layer region (E = n_embd, NH heads, F = ffn):
  * QKV outputs [3E], attention chunk partials [NH][G2_STEP_MAXCH][66],
  * merged attention O [E], X1 = x + proj [E], H = gelu(fc) [F],
@@ -279,55 +268,6 @@ typedef struct {
 /* after the layers: 2 argmax words per work-group, 32 spare words, then one
  * arrival word per work-group (plain launches) */
 #define G2X_ARRIVE(L, xlayer, nwg) ((long)G2X_HEAD + (long)(L) * (xlayer) + 2L * (nwg) + 32)
-
-/* XCD-parallel decode step (same arguments as g2_step_args; layout below).
- * A work-group reads its XCD from the hardware; its rank within the XCD is
- * w / G2_NXCD (distinct under the dispatcher's round-robin).  XCD x
- * owns heads [NH*x/8, NH*(x+1)/8) and ffn rows [F*x/8, F*(x+1)/8); proj and
- * fc2 are computed as per-XCD partial products over those K-slices and
- * summed across XCDs.  Hand-offs inside an XCD go through its L2; only the
- * two partial sums per layer cross XCDs.
- * Exchange words per layer: G2_NXCD local regions of G2XL_WORDS each
- * (qkv of the XCD's heads, attention partials, merged o, X1, H slice, X2),
- * then two global regions of G2_NXCD*E partial sums (proj, fc2). */
-#define G2_NXCD 8
-#define G2XL_QKV 0
-#define G2XL_ATT(HX) (192 * (HX))
-#define G2XL_O(HX) (G2XL_ATT(HX) + (HX) * G2_STEP_MAXCH * 66)
-#define G2XL_X1(HX) (G2XL_O(HX) + 64 * (HX))
-#define G2XL_H(HX, E) (G2XL_X1(HX) + (E))
-#define G2XL_X2(HX, E, FX) (G2XL_H(HX, E) + (FX))
-#define G2XL_WORDS(HX, E, FX) ((G2XL_X2(HX, E, FX) + (E) + 63) & ~63)
-#define G2XX_LAYER_WORDS(HX, E, FX) (G2_NXCD * G2XL_WORDS(HX, E, FX) + 2 * G2_NXCD * (E))
-#define G2XX_TOTAL_WORDS(L, HX, E, FX, nwg) \
-    ((long)G2X_HEAD + (long)(L) * G2XX_LAYER_WORDS(HX, E, FX) + 2L * (nwg) + 32)
-
-/* 16-bit matrix transpose: dst[c*R + r] = src[r*C + c]; grid (ceil(C/32),
- * ceil(R/32)) of 256 threads. */
-typedef struct {
-    const uint16_t *src;
-    uint16_t *dst;
-    int R, C;
-} g2_transpose_args;
-
-/* Two-role decode step (g2k_step3_f16, same arguments as g2_step_args).
- * Exchange words per layer: QKV outputs [3E], attention chunk partials
- * [NH][G2_STEP_MAXCH][66], merged attention O [E], X1 [E], X2 [E], then
- * the partial fc2 products blocked by reader: work-group p's partial of
- * output row n goes to word ((k * nwg) + p) * 8 + r, where work-group k
- * sums rows [E k / nwg, E (k+1) / nwg) and n is its row r, so a reader's
- * words are contiguous and a writer's rows of one reader share a 64-byte
- * line; regions are padded to 64 words. */
-#define G3X_ATT(E) (3 * (E))
-#define G3X_O(E, NH) (G3X_ATT(E) + (NH) * G2_STEP_MAXCH * 66)
-#define G3X_X1(E, NH) (G3X_O(E, NH) + (E))
-#define G3X_X2(E, NH) (G3X_X1(E, NH) + (E))
-#define G3X_P2(E, NH) (G3X_X2(E, NH) + (E))
-#define G3X_LAYER_WORDS(E, NH, nwg) ((G3X_P2(E, NH) + 8L * (nwg) * (nwg) + 63) & ~63L)
-#define G3X_TOTAL_WORDS(L, E, NH, nwg) \
-    ((long)G2X_HEAD + (long)(L) * G3X_LAYER_WORDS(E, NH, nwg) + 2L * (nwg) + 32)
-#define G3_MAXWG 256   /* work-groups of the two-role kernel (4 per exchange lane) */
-#define G3_MAXROWS 8   /* X2 rows a work-group sums (n_embd / nwg, rounded up) */
 
 /* Causal attention over a prompt block: rows i < P of q[P,E]; keys/values
  * j <= i from the transposed K cache and the V cache; head dim 64. */

@@ -1485,24 +1485,3 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
 
 /* The persistent decode step (one cooperative launch per token). */
 #include "g2_step.hip"
-#include "g2_stepx.hip"
-#include "g2_step3.hip"
-#include "g2_step4.hip"
-
-/* dst = transpose of the 16-bit [R][C] matrix src, 32x32 tiles through LDS
- * (the step kernels' input-major fc2 copy). */
-G2K void g2k_transpose16(const g2_transpose_args a)
-{
-    __shared__ unsigned short t[32][33];
-    const int c0 = blockIdx.x * 32, r0 = blockIdx.y * 32;
-    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
-    for (int k = ty; k < 32; k += 8) {
-        const int r = r0 + k, c = c0 + tx;
-        if (r < a.R && c < a.C) t[k][tx] = a.src[(size_t)r * a.C + c];
-    }
-    __syncthreads();
-    for (int k = ty; k < 32; k += 8) {
-        const int c = c0 + k, r = r0 + tx;
-        if (c < a.C && r < a.R) a.dst[(size_t)c * a.R + r] = t[tx][k];
-    }
-}

@@ -30,7 +30,6 @@
 typedef struct {
     float *ln1_w, *ln1_b, *qkv_b, *proj_b, *ln2_w, *ln2_b, *fc_b, *fc2_b;
     void *qkv_w, *proj_w, *fc_w, *fc2_w;
-    void *fc2_wt; /* fc2 input-major [F][E] (two-role step kernel), or NULL */
     float *k_cache, *v_cache;
 } g2_layer;
 
@@ -57,9 +56,6 @@ struct g2_model {
     size_t xbuf_bytes;
     int step_wgs;  /* grid of the step kernel, 0 if this model cannot use it */
     int step_on;   /* decode steps run the step kernel */
-    int stepx;     /* ... in its XCD-parallel form */
-    int step3;     /* ... in its two-role form */
-    int step4;     /* ... in its loader-wave form */
     int plain;     /* the all-to-all form's launches are plain, not cooperative (2: test
                       hook, work-group 1 withholds its arrival) */
     int step_ran;  /* a step kernel ran since the last error check */
@@ -198,90 +194,6 @@ static int step_supported(const g2_model *m, int nwg, const char **why)
     return 1;
 }
 
-static int step_nseg(int C)
-{
-    const int cpl = C <= 64 ? 1 : (C <= 128 ? 2 : 4);
-    const int need = (C + 64 * cpl - 1) / (64 * cpl);
-    return need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : (need <= 8 ? 8 : 1 << 20)));
-}
-
-/* Whether the XCD-parallel step kernel can run this model on a grid of nwg
- * work-groups (G2_NXCD XCDs of nwg/G2_NXCD): the ffn slice of an XCD must
- * start on a 16-byte chunk, every work-group's share of every matrix must
- * fit its units and threads, and the reduce-scatter of E rows over the
- * ranks of an XCD must fit one read per thread. */
-static int stepx_supported(const g2_model *m, int nwg)
-{
-    const g2_config *c = &m->cfg;
-    const int ve = m->dtype == G2_F16 ? 8 : 4;
-    const int E = c->n_embd, F = c->ffn_dim, V = c->vocab_size, NH = c->n_head;
-    if (nwg <= 0 || nwg % G2_NXCD) return 0;
-    const int G = nwg / G2_NXCD;
-    const int HX = (NH + G2_NXCD - 1) / G2_NXCD, FX = (F + G2_NXCD - 1) / G2_NXCD;
-    if (F % G2_NXCD || (F / G2_NXCD) % ve) return 0;
-    if (G2_NXCD * ((E + G - 1) / G) > G2_STEP_THREADS) return 0;
-    const int rows[5] = { (192 * HX + G - 1) / G, (FX + G - 1) / G, (E + G - 1) / G, (E + G - 1) / G,
-                          (V + nwg - 1) / nwg };
-    const int chunks[5] = { E / ve, E / ve, 64 * HX / ve, FX / ve, E / ve };
-    for (int i = 0; i < 5; ++i) {
-        if (rows[i] > G2_STEP_THREADS) return 0;
-        if ((long)rows[i] * step_nseg(chunks[i]) > G2_STEP_MAXUNITS) return 0;
-    }
-    return 1;
-}
-
-/* Whether the two-role step kernel (g2k_step3_f16) can run this model on a
- * grid of nwg work-groups: fp16 weights; every matrix share within the
- * compute waves' register sets (qkv rows <= 21, fc rows <= 28, proj rows
- * <= 7 per work-group, fc2 rows per thread group <= 13); the X2 rows a
- * work-group sums <= G3_MAXROWS; at most two attention units per
- * work-group (n_head * 16 <= 2 nwg). */
-static int step3_supported(const g2_model *m, int nwg)
-{
-    const g2_config *c = &m->cfg;
-    const int E = c->n_embd, F = c->ffn_dim, NH = c->n_head;
-    if (m->dtype != G2_F16 || nwg <= 0 || nwg > G3_MAXWG || E > G2_STEP_MAXE || E % 8) return 0;
-    const int NC = E / 8, JG = 448 / NC;
-    if (JG < 1 || NC > 256) return 0;
-    if ((3 * E + nwg - 1) / nwg > 21 || (F + nwg - 1) / nwg > 28 || (E + nwg - 1) / nwg > 7) return 0;
-    if (((F + nwg - 1) / nwg + JG - 1) / JG > 13) return 0;
-    if ((E + nwg - 1) / nwg > G3_MAXROWS) return 0;
-    if (NH * G2_STEP_MAXCH > 2 * nwg) return 0;
-    return 1;
-}
-
-/* Whether the loader-wave step kernel (g2k_step4_f16) can run this model on
- * a grid of nwg work-groups: fp16 weights, and every work-group's share of
- * every matrix (and G2_STEP4_LM_ROWS lm_head rows) fits its LDS ring. */
-static int step4_supported(const g2_model *m, int nwg)
-{
-    const g2_config *c = &m->cfg;
-    const long E = c->n_embd, F = c->ffn_dim;
-    if (m->dtype != G2_F16 || nwg <= 0) return 0;
-    const long ring = (long)G2_STEP4_RING_BLOCKS * 1024;
-    const long share[5] = { (3 * E + nwg - 1) / nwg * E * 2, (E + nwg - 1) / nwg * E * 2,
-                            (F + nwg - 1) / nwg * E * 2, (E + nwg - 1) / nwg * F * 2, G2_STEP4_LM_ROWS * E * 2 };
-    for (int i = 0; i < 5; ++i)
-        if (share[i] > ring) return 0;
-    return 1;
-}
-
-/* The input-major copy of every layer's fc2 weights for the two-role kernel
- * (a device transpose of the packed [E][F] matrix). */
-static int step3_fc2_copies(g2_model *m)
-{
-    const int E = m->cfg.n_embd, F = m->cfg.ffn_dim;
-    for (int l = 0; l < m->cfg.n_layer; ++l) {
-        g2_layer *y = &m->L[l];
-        int rc = dev_alloc(m, &y->fc2_wt, (size_t)F * E * 2, 0);
-        if (rc) return rc;
-        g2_transpose_args t = { (const uint16_t *)y->fc2_w, (uint16_t *)y->fc2_wt, E, F };
-        rc = g2i_launch(G2F_TRANSPOSE16, (unsigned)((F + 31) / 32), (unsigned)((E + 31) / 32), 256, &t);
-        if (rc) return rc;
-    }
-    return G2_OK;
-}
-
 /* Device tables of the step kernel (after the weights are uploaded). */
 static int step_setup(g2_model *m)
 {
@@ -289,12 +201,6 @@ static int step_setup(g2_model *m)
     if (!step_supported(m, nwg, &m->step_why)) return G2_OK;
     const g2_config *c = &m->cfg;
     const int L = c->n_layer;
-    const char *env3 = getenv("G2_STEP3");
-    m->step3 = env3 && env3[0] == '1' && g2i_step3_ok() && step3_supported(m, nwg);
-    if (m->step3) {
-        int rc3 = step3_fc2_copies(m);
-        if (rc3) return rc3;
-    }
     g2_step_layer *t = calloc((size_t)L, sizeof *t);
     if (!t) return g2i_err(G2_E_NOMEM, "step layer table");
     for (int l = 0; l < L; ++l) {
@@ -302,28 +208,17 @@ static int step_setup(g2_model *m)
         t[l].ln1_w = y->ln1_w; t[l].ln1_b = y->ln1_b; t[l].qkv_b = y->qkv_b; t[l].proj_b = y->proj_b;
         t[l].ln2_w = y->ln2_w; t[l].ln2_b = y->ln2_b; t[l].fc_b = y->fc_b; t[l].fc2_b = y->fc2_b;
         t[l].qkv_w = y->qkv_w; t[l].proj_w = y->proj_w; t[l].fc_w = y->fc_w; t[l].fc2_w = y->fc2_w;
-        t[l].fc2_wt = y->fc2_wt;
         t[l].k_cache = y->k_cache; t[l].v_cache = y->v_cache;
     }
     int rc = dev_alloc(m, (void **)&m->step_layers, (size_t)L * sizeof *t, 0);
     if (!rc) rc = up(m->step_layers, t, (size_t)L * sizeof *t);
     free(t);
-    const char *envx = getenv("G2_STEPX");
-    m->stepx = envx && envx[0] == '1' && g2i_stepx_ok() && stepx_supported(m, nwg);
-    const char *env4 = getenv("G2_STEP4");
-    m->step4 = !m->step3 && !m->stepx && env4 && env4[0] == '1' && g2i_step4_ok() && step4_supported(m, nwg);
     /* A cooperative launch costs ~17 us more than a plain one between
      * back-to-back steps (1.4% of an XL token); the all-to-all kernel checks
      * residency itself, so it is launched plain unless G2_STEP_COOP=1. */
     const char *envc = getenv("G2_STEP_COOP"), *envw = getenv("G2_STEP_TEST_WITHHOLD");
     m->plain = envc && envc[0] == '1' ? 0 : (envw && envw[0] == '1' ? 2 : 1);
-    const long w1 = G2X_TOTAL_WORDS(L, c->n_embd, c->n_head, c->ffn_dim, nwg);
-    const int HX = (c->n_head + G2_NXCD - 1) / G2_NXCD, FX = (c->ffn_dim + G2_NXCD - 1) / G2_NXCD;
-    const long w2 = G2XX_TOTAL_WORDS(L, HX, c->n_embd, FX, nwg);
-    const long w3 = m->step3 ? G3X_TOTAL_WORDS(L, c->n_embd, c->n_head, nwg) : 0;
-    long wmax = w1 > w2 ? w1 : w2;
-    if (w3 > wmax) wmax = w3;
-    m->xbuf_bytes = (size_t)wmax * 8;
+    m->xbuf_bytes = (size_t)G2X_TOTAL_WORDS(L, c->n_embd, c->n_head, c->ffn_dim, nwg) * 8;
     if (!rc) rc = dev_alloc(m, (void **)&m->xbuf, m->xbuf_bytes, 0);
     if (!rc) rc = g2i_hip(hipMemsetAsync(m->xbuf, 0, m->xbuf_bytes, g2i_stream()), "exchange clear");
     if (rc) return rc;
@@ -408,7 +303,7 @@ int g2_model_free(g2_model *m)
     for (int l = 0; l < m->cfg.n_layer; ++l) {
         g2_layer *y = &m->L[l];
         void *lb[] = { y->ln1_w, y->ln1_b, y->qkv_b, y->proj_b, y->ln2_w, y->ln2_b, y->fc_b,
-                       y->fc2_b, y->qkv_w, y->proj_w, y->fc_w, y->fc2_w, y->fc2_wt, y->k_cache, y->v_cache };
+                       y->fc2_b, y->qkv_w, y->proj_w, y->fc_w, y->fc2_w, y->k_cache, y->v_cache };
         for (size_t i = 0; i < sizeof lb / sizeof lb[0]; ++i)
             if (lb[i]) hipFree(lb[i]);
     }
@@ -686,7 +581,7 @@ int g2_model_set_step(g2_model *m, int on)
 int g2_model_uses_step(const g2_model *m)
 {
     if (!m) return g2i_err(G2_E_ARG, "NULL model");
-    return m->step_on ? (m->step3 ? 3 : (m->stepx ? 2 : (m->step4 ? 4 : 1))) : 0;
+    return m->step_on ? 1 : 0;
 }
 
 int g2_model_uses_graph(const g2_model *m)
@@ -846,18 +741,7 @@ static int step_launch(g2_model *m)
     a.S = G2_KV_MAX_SEQ;
     a.scale = 1.0f / sqrtf(64.0f);
     m->step_ran = 1;
-    if (m->step3) {
-        a.xlayer = (int)G3X_LAYER_WORDS(c->n_embd, c->n_head, m->step_wgs);
-        return g2i_coop_launch(G2F_STEP3_F16, (unsigned)m->step_wgs, G2_STEP_THREADS, &a);
-    }
-    if (m->stepx) {
-        const int HX = (c->n_head + G2_NXCD - 1) / G2_NXCD, FX = (c->ffn_dim + G2_NXCD - 1) / G2_NXCD;
-        a.xlayer = G2XX_LAYER_WORDS(HX, c->n_embd, FX);
-        return g2i_coop_launch(m->dtype == G2_F16 ? G2F_STEPX_F16 : G2F_STEPX_F32, (unsigned)m->step_wgs,
-                               G2_STEP_THREADS, &a);
-    }
     a.xlayer = G2X_LAYER_WORDS(c->n_embd, c->n_head, c->ffn_dim);
-    if (m->step4) return g2i_coop_launch(G2F_STEP4_F16, (unsigned)m->step_wgs, G2_STEP4_THREADS, &a);
     const int fid = m->dtype == G2_F16 ? G2F_STEP_F16 : G2F_STEP_F32;
     if (m->plain) {
         a.plain = m->plain;
@@ -898,12 +782,6 @@ static int step_check(g2_model *m, int ngen_target)
     rc = g2i_hip(hipMemsetAsync(m->xbuf, 0, m->xbuf_bytes, g2i_stream()), "exchange clear");
     if (!rc) rc = up(m->state + G2S_ERR, &zero, sizeof zero);
     if (rc) return rc;
-    if (m->stepx) {
-        m->stepx = 0; /* later steps use the all-to-all step kernel */
-        return g2i_err(G2_E_HIP, "XCD-parallel decode step kernel: a hand-off between work-groups timed out "
-                                 "(work-groups not where expected?); the step's outputs are invalid and later "
-                                 "steps use the all-to-all step kernel");
-    }
     return g2i_err(G2_E_HIP, "decode step kernel: a hand-off between work-groups timed out; "
                              "the step's outputs are invalid");
 }

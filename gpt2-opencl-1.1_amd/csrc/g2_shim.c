@@ -33,9 +33,6 @@ static const char *const g2_kernel_names[G2F_COUNT] = { G2_KERNEL_LIST(G2_NAME_E
 static struct {
     int ready, device, cus;
     int step_wgs; /* work-groups of a cooperative step launch (0: unsupported) */
-    int stepx_ok; /* the XCD-parallel step kernel may run */
-    int step3_ok; /* the two-role step kernel may run */
-    int step4_ok; /* the loader-wave step kernel may run */
     char name[256];
     hipModule_t module;
     hipStream_t stream;
@@ -94,45 +91,6 @@ int g2i_coop_launch(int fid, unsigned gx, unsigned bx, void *args)
 
 int g2i_step_wgs(void) { return G.step_wgs; }
 int g2i_cus(void) { return G.cus > 0 ? G.cus : 1; }
-int g2i_stepx_ok(void) { return G.stepx_ok; }
-int g2i_step3_ok(void) { return G.step3_ok; }
-int g2i_step4_ok(void) { return G.step4_ok; }
-
-/* The XCD-parallel step kernel hands data between work-groups through the
- * L2 of their XCD and gives the work-groups of one XCD the ranks w / 8,
- * which are distinct if consecutive work-groups go to consecutive XCDs (the
- * dispatcher's round-robin, whatever XCD it starts from).  Check that with
- * a probe launch of the same shape; 1 if it holds for every work-group, 0
- * if not, -1 if the cooperative launch itself is refused (*err: its error). */
-static int xcd_mapping_holds(int nwg, hipError_t *err)
-{
-    int ok = 0, nb = 0, *d = NULL;
-    *err = hipSuccess;
-    if (nwg <= 0 || nwg % G2_NXCD) return 0;
-    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, G.fn[G2F_STEPX_F16], G2_STEP_THREADS, 0) != hipSuccess || nb < 1)
-        return 0;
-    if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, G.fn[G2F_STEPX_F32], G2_STEP_THREADS, 0) != hipSuccess || nb < 1)
-        return 0;
-    int *h = malloc((size_t)nwg * sizeof(int));
-    if (!h) return 0;
-    if (hipMalloc((void **)&d, (size_t)nwg * sizeof(int)) == hipSuccess &&
-        hipMemsetAsync(d, 0xff, (size_t)nwg * sizeof(int), G.stream) == hipSuccess) {
-        void *params[1] = { &d };
-        *err = hipModuleLaunchCooperativeKernel(G.fn[G2F_XCC_PROBE], (unsigned)nwg, 1, 1, G2_STEP_THREADS, 1, 1, 0,
-                                                G.stream, params);
-        if (*err != hipSuccess) ok = -1;
-        else if (hipMemcpyAsync(h, d, (size_t)nwg * sizeof(int), hipMemcpyDeviceToHost, G.stream) == hipSuccess &&
-            hipStreamSynchronize(G.stream) == hipSuccess) {
-            ok = h[0] >= 0 && h[0] < G2_NXCD;
-            for (int w = 0; w < nwg && ok; ++w)
-                if (h[w] != (h[0] + w) % G2_NXCD) ok = 0;
-        }
-    }
-    if (d) hipFree(d);
-    free(h);
-    (void)hipGetLastError();
-    return ok;
-}
 
 int g2i_device_alloc(void **p, size_t bytes)
 {
@@ -245,29 +203,7 @@ int g2_init(int device)
                     rtv, coop, (int)ea, nb[0], nb[1], (int)eo[0], (int)eo[1], fa.numRegs, fa.sharedSizeBytes,
                     fa.maxThreadsPerBlock);
         }
-        int nb3 = 0;
-        G.step3_ok = G.step_wgs && G.step_wgs <= G3_MAXWG &&
-                     hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb3, G.fn[G2F_STEP3_F16], G2_STEP_THREADS, 0) ==
-                         hipSuccess && nb3 >= 1;
-        int nb4 = 0;
-        G.step4_ok = G.step_wgs &&
-                     hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb4, G.fn[G2F_STEP4_F16], G2_STEP4_THREADS, 0) ==
-                         hipSuccess && nb4 >= 1;
         (void)hipGetLastError();
-        hipError_t ec = hipSuccess;
-        const int xm = G.step_wgs ? xcd_mapping_holds(G.step_wgs, &ec) : 0;
-        G.stepx_ok = xm == 1;
-        if (xm < 0) {
-            /* A device grants cooperative launches to one process at a time:
-             * a second process on the same GPU is refused them. */
-            fprintf(stderr, "g2hip: cooperative launch refused (HIP error %d: %s; another process on this GPU "
-                            "may hold it); decode uses per-operator kernels\n", (int)ec, hipGetErrorString(ec));
-            G.step_wgs = 0;
-            G.step3_ok = 0;
-            G.step4_ok = 0;
-        } else if (G.step_wgs && !G.stepx_ok)
-            fprintf(stderr, "g2hip: work-groups are not dealt to XCDs round-robin on this device; "
-                            "decode uses the all-to-all step kernel\n");
     }
     G.device = device;
     G.ready = 1;

@@ -394,8 +394,7 @@ class Model:
         return _lib.g2_model_uses_step(self.h) >= 1
 
     def step_kind(self):
-        """3: two-role step kernel, 2: XCD-parallel step kernel, 1: all-to-all step kernel,
-        0: per-operator kernels."""
+        """1: persistent step kernel, 0: per-operator kernels."""
         return _lib.g2_model_uses_step(self.h)
 
     def prefill(self, ids):

@@ -214,17 +214,9 @@ int g2_model_uses_graph(const g2_model *m);
  * with cooperative launches; G2_STEP_COOP=1 forces those); the variable
  * G2_STEP=0 or g2_model_set_step(m, 0) selects the per-operator kernels
  * instead.  Replaces the reference's per-op enqueue loop of decode()
- * (main.c:1792-1833) with no counterpart there.  The default is the
- * all-to-all form; G2_STEPX=1 selects the XCD-parallel form (each XCD owns
- * heads and ffn rows) on a device whose work-groups are dealt to its 8 XCDs
- * round-robin (checked at g2_init); G2_STEP3=1 selects the two-role form
- * (fp16 weights: one wave per work-group does every hand-off, the others
- * keep the weights of the next matrices in flight); G2_STEP4=1 the
- * loader-ring form (fp16 weights: loader waves stream the weight rows
- * through an LDS ring).  set_step returns G2_E_ARG if on=1 and the model
- * cannot use the kernel; uses_step returns 4 (loader-ring step kernel), 3
- * (two-role), 2 (XCD-parallel), 1 (all-to-all) or 0 (per-operator
- * kernels). */
+ * (main.c:1792-1833) with no counterpart there.  set_step returns G2_E_ARG
+ * if on=1 and the model cannot use the kernel; uses_step returns 1 (step
+ * kernel) or 0 (per-operator kernels). */
 int g2_model_set_step(g2_model *m, int on);
 int g2_model_uses_step(const g2_model *m);
 

@@ -1,9 +1,5 @@
-"""GPU parity of the persistent decode-step kernels (one cooperative launch
-per token running every layer, the lm_head and the greedy pick), in both
-forms: all-to-all (the default), XCD-parallel (G2_STEPX=1: each XCD owns
-heads and ffn rows, where the device deals work-groups to XCDs
-round-robin), two-role (G2_STEP3=1) and loader-ring (G2_STEP4=1: a loader
-wave streams the weight rows through an LDS ring).
+"""GPU parity of the persistent decode-step kernel (one launch per token
+running every layer, the lm_head and the greedy pick).
 
 The fused path decodes with them by default; these tests pin them against
 the CPU oracle (greedy ids, teacher-forced per-step logits within 2e-3 fp32
@@ -21,31 +17,6 @@ from parity import greedy_agree, random_prompt
 pytestmark = pytest.mark.gpu
 
 SEED = 0x67707432
-KINDS = [pytest.param("a2a", id="all-to-all"), pytest.param("xcd", id="xcd"),
-         pytest.param("two-role", id="two-role"), pytest.param("ring", id="loader-ring")]
-ENV = {"a2a": {"G2_STEPX": "0", "G2_STEP3": "0", "G2_STEP4": "0"},
-       "xcd": {"G2_STEPX": "1", "G2_STEP3": "0", "G2_STEP4": "0"},
-       "two-role": {"G2_STEPX": "0", "G2_STEP3": "1", "G2_STEP4": "0"},
-       "ring": {"G2_STEPX": "0", "G2_STEP3": "0", "G2_STEP4": "1"}}
-KIND_ID = {"a2a": 1, "xcd": 2, "two-role": 3, "ring": 4}
-
-
-@pytest.fixture
-def stepx(request, monkeypatch):
-    """Selects the step-kernel form for models created in the test."""
-    for k, v in ENV[request.param].items():
-        monkeypatch.setenv(k, v)
-    return request.param
-
-
-def _expect_kind(m, kind, f16=True):
-    """The two-role and loader-ring forms run fp16-weight models; the others
-    run both."""
-    if kind in ("two-role", "ring") and not f16:
-        return
-    assert m.step_kind() == KIND_ID[kind], f"expected step kernel form {kind}, got {m.step_kind()}"
-
-
 def _check(got, ref, f16):
     tol = 5e-2 if f16 else 2e-3
     np.testing.assert_allclose(got, ref, rtol=tol if f16 else 1e-3, atol=tol)
@@ -66,18 +37,15 @@ def test_step_kernel_is_default(g2):
     m.free()
 
 
-@pytest.mark.parametrize("stepx", KINDS, indirect=True)
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
-def test_step_matches_operator_kernels(g2, stepx, dtype):
+def test_step_matches_operator_kernels(g2, dtype):
     """Same model, same prompt: the step kernel and the per-operator decode
     kernels give the same greedy ids and logits within the parity bound."""
     cfg = g2.preset("small")
     dt = g2.F16 if dtype == "f16" else g2.F32
     m = g2.Model.synth(cfg, SEED, dt, g2.PATH_FUSED)
     prompt = random_prompt(48, cfg.vocab_size, 11)
-    print(f"[step] small {dtype} form {m.step_kind()}: step kernel vs operator kernels", flush=True)
-    if stepx != "xcd":
-        _expect_kind(m, stepx, dtype == "f16")
+    print(f"[step] small {dtype}: step kernel vs operator kernels", flush=True)
     m.set_step(True)
     ids_s, _ = m.generate(prompt, 20)
     lg_s = m.logits()
@@ -99,8 +67,7 @@ def test_step_matches_operator_kernels(g2, stepx, dtype):
     m.free()
 
 
-@pytest.mark.parametrize("stepx", KINDS, indirect=True)
-def test_step_xl_width_to_end_of_context(g2, stepx):
+def test_step_xl_width_to_end_of_context(g2):
     """Two layers at GPT-2 XL width (n_embd 1600, 25 heads, ffn 6400, vocab
     50257, fp16 weights): teacher-forced decode logits at positions
     1000..1022 (16 key chunks per head) against the oracle."""
@@ -110,11 +77,9 @@ def test_step_xl_width_to_end_of_context(g2, stepx):
     om = oracle.Model(cfg, w, kslice=4)
     m = g2.Model.from_host(cfg, w, g2.F16, g2.PATH_FUSED)
     assert m.uses_step()
-    if stepx != "xcd":
-        _expect_kind(m, stepx)
     P = 1000
     prompt = random_prompt(P, cfg.vocab_size, 77)
-    print(f"[step] XL width L2 form {m.step_kind()}, prompt {P}", flush=True)
+    print(f"[step] XL width L2, prompt {P}", flush=True)
     om.prefill(prompt)
     m.prefill(prompt)
     _check(m.logits(), om.logits(), True)
@@ -129,8 +94,7 @@ def test_step_xl_width_to_end_of_context(g2, stepx):
     om.close()
 
 
-@pytest.mark.parametrize("stepx", KINDS, indirect=True)
-def test_step_deterministic(g2, stepx):
+def test_step_deterministic(g2):
     """Two identical runs produce bit-identical ids and logits."""
     cfg = g2.preset("small")
     m = g2.Model.synth(cfg, SEED, g2.F16, g2.PATH_FUSED)
@@ -144,8 +108,7 @@ def test_step_deterministic(g2, stepx):
     m.free()
 
 
-@pytest.mark.parametrize("stepx", KINDS, indirect=True)
-def test_step_decode_run_matches_generate(g2, stepx):
+def test_step_decode_run_matches_generate(g2):
     """decode_run (the bench's loop) continues a prefilled cache exactly as
     generate does."""
     cfg = g2.make_config(3, 256, 4, vocab_size=1000)
@@ -158,7 +121,7 @@ def test_step_decode_run_matches_generate(g2, stepx):
 
 
 def test_step_plain_launch_not_resident_resumes(g2, monkeypatch, capfd):
-    """The all-to-all kernel is launched plain (not cooperatively) and
+    """The step kernel is launched plain (not cooperatively) and
     checks that all its work-groups are resident before its first lasting
     write.  Forced failure from the host (G2_STEP_TEST_WITHHOLD=1:
     work-group 1 withholds its arrival word, so every work-group gives up
@@ -169,8 +132,6 @@ def test_step_plain_launch_not_resident_resumes(g2, monkeypatch, capfd):
     cfg = g2.make_config(3, 256, 4, vocab_size=1000)
     w = g2.synth_weights(cfg, SEED, f16_round=True)
     prompt = random_prompt(120, cfg.vocab_size, 31)
-    for k, v in ENV["a2a"].items():
-        monkeypatch.setenv(k, v)
     outs = []
     for env in ({"G2_STEP_COOP": "1"}, {"G2_STEP_TEST_WITHHOLD": "1"}, {}):
         for k in ("G2_STEP_COOP", "G2_STEP_TEST_WITHHOLD"):
@@ -181,7 +142,7 @@ def test_step_plain_launch_not_resident_resumes(g2, monkeypatch, capfd):
         run = []
         for _ in range(2):
             m = g2.Model.from_host(cfg, w, g2.F16, g2.PATH_FUSED)
-            assert m.step_kind() == KIND_ID["a2a"]
+            assert m.step_kind() == 1
             if not run:
                 for _ in range(2):
                     ids, _ = m.generate(prompt, 30, min_new=30)
@@ -199,33 +160,3 @@ def test_step_plain_launch_not_resident_resumes(g2, monkeypatch, capfd):
     for o in outs[1:]:
         for a, b in zip(outs[0], o):
             np.testing.assert_array_equal(a, b)
-
-
-@pytest.mark.parametrize("stepx", [pytest.param("xcd", id="xcd"), pytest.param("two-role", id="two-role"),
-                                   pytest.param("ring", id="loader-ring")], indirect=True)
-@pytest.mark.parametrize("cfg_args", [(2, 128, 2, 256), (3, 192, 3, 1000), (1, 64, 1, 50257)],
-                         ids=["tiny", "3-heads", "1-head"])
-def test_stepx_small_shapes(g2, stepx, cfg_args):
-    """The XCD-parallel and two-role kernels on small shapes: some XCDs own
-    no head (n_head < 8), most work-groups own no ffn or output rows, ffn
-    slices are a few chunks.  Greedy ids and logits vs the oracle."""
-    L, E, H, V = cfg_args
-    cfg = g2.make_config(L, E, H, vocab_size=V)
-    for dtype in (g2.F32, g2.F16):
-        f16 = dtype == g2.F16
-        w = g2.synth_weights(cfg, SEED, f16_round=f16)
-        om = oracle.Model(cfg, w)
-        prompt = random_prompt(30, V, 4)
-        ref_ids, top2, ref_lg = om.generate(prompt, 12, logit_steps=4)
-        m = g2.Model.from_host(cfg, w, dtype, g2.PATH_FUSED)
-        print(f"[step] L{L} E{E} H{H} V{V} {'f16' if f16 else 'f32'} form {m.step_kind()}", flush=True)
-        if stepx in ("two-role", "ring"):
-            _expect_kind(m, stepx, f16)
-        ids, _ = m.generate(prompt, 12)
-        greedy_agree(ids, ref_ids, top2, 1e-2 if f16 else 1e-4)
-        m.prefill(prompt)
-        for k in range(3):
-            m.decode(ref_ids[k], 30 + k)
-            _check(m.logits(), ref_lg[k + 1], f16)
-        m.free()
-        om.close()
