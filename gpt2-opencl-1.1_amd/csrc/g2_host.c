@@ -27,7 +27,10 @@ static int json_int(const char *json, const char *const *keys, int nkeys, int de
         if (!p) continue;
         ++p;
         while (*p == ' ' || *p == '\t' || *p == '\n' || *p == '\r') ++p;
-        return atoi(p);
+        /* atoi's value, with out-of-range numbers clamped (they then fail the
+         * ceilings instead of overflowing) */
+        const long long v = strtoll(p, NULL, 10);
+        return v > (1 << 28) ? (1 << 28) : (v < -(1 << 28) ? -(1 << 28) : (int)v);
     }
     return defval;
 }
@@ -325,6 +328,13 @@ int g2h_st_open(const char *path, g2h_st *st)
     }
     h[hlen] = 0;
     st->data_start = 8 + (int64_t)hlen;
+    /* every tensor's bytes must lie inside the file */
+    int64_t fsize = -1;
+    if (fseeko(st->fp, 0, SEEK_END) == 0) fsize = (int64_t)ftello(st->fp);
+    if (fsize < st->data_start) {
+        free(h); g2h_st_close(st);
+        return g2i_err(G2_E_FORMAT, "%s: file shorter than its header", path);
+    }
     const char *p = h, *end = h + hlen;
     int cap = 64;
     st->t = calloc((size_t)cap, sizeof *st->t);
@@ -389,10 +399,19 @@ int g2h_st_open(const char *path, g2h_st *st)
                 p = skip_ws(p, end);
                 if (p < end && *p == ',') ++p;
             }
+            /* element count with every dimension and the product bounded (no
+             * int64 overflow), byte range consistent with it and inside the file */
+            const int64_t lim = (int64_t)1 << 40;
             int64_t nel = 1;
-            for (int i = 0; i < t->ndim; ++i) nel *= t->shape[i];
-            if (t->dtype < 0 || t->end < t->begin || t->begin < 0 ||
-                (t->esize && nel * t->esize != t->end - t->begin)) {
+            int bad = t->dtype < 0;
+            for (int i = 0; i < t->ndim && !bad; ++i) {
+                if (t->shape[i] < 0 || t->shape[i] > lim) bad = 1;
+                else if (t->shape[i] > 0 && nel > lim / t->shape[i]) bad = 1;
+                else nel *= t->shape[i];
+            }
+            if (!bad && (t->begin < 0 || t->end < t->begin || t->end > fsize - st->data_start)) bad = 1;
+            if (!bad && t->esize && nel * t->esize != t->end - t->begin) bad = 1;
+            if (bad) {
                 rc = g2i_err(G2_E_FORMAT, "%s: inconsistent entry for %s", path, t->name);
                 goto done;
             }
@@ -426,11 +445,15 @@ const g2h_tensor *g2h_st_find(const g2h_st *st, const char *name)
     return NULL;
 }
 
-/* Read a tensor as fp32 (F32 copied, F16/BF16 widened). */
-int g2h_st_read_f32(const g2h_st *st, const g2h_tensor *t, float *dst)
+/* Read a tensor as fp32 (F32 copied, F16/BF16 widened) into dst, which
+ * holds cap floats. */
+int g2h_st_read_f32(const g2h_st *st, const g2h_tensor *t, float *dst, int64_t cap)
 {
     if (t->dtype == G2H_ST_OTHER)
         return g2i_err(G2_E_FORMAT, "tensor %s has unsupported dtype %s", t->name, t->dtype_name);
+    if (t->numel > cap || t->numel * t->esize != t->end - t->begin)
+        return g2i_err(G2_E_FORMAT, "tensor %s: %lld elements do not fit the %lld expected", t->name,
+                       (long long)t->numel, (long long)cap);
     const size_t bytes = (size_t)(t->end - t->begin);
     if (fseeko(st->fp, (off_t)(st->data_start + t->begin), SEEK_SET) != 0)
         return g2i_err(G2_E_IO, "seek to %s failed", t->name);

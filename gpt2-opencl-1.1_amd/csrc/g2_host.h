@@ -30,7 +30,7 @@ char *g2h_slurp(const char *path, size_t *size);
 int g2h_st_open(const char *path, g2h_st *st);
 void g2h_st_close(g2h_st *st);
 const g2h_tensor *g2h_st_find(const g2h_st *st, const char *name);
-int g2h_st_read_f32(const g2h_st *st, const g2h_tensor *t, float *dst);
+int g2h_st_read_f32(const g2h_st *st, const g2h_tensor *t, float *dst, int64_t cap);
 float g2h_f16_to_f32(uint16_t h);
 
 #endif /* G2_HOST_H */

@@ -429,15 +429,21 @@ static int read_linear(const g2h_st *st, const char *name, int in, int out, int 
 {
     const g2h_tensor *t = g2h_st_find(st, name);
     if (!t) return g2i_err(G2_E_FORMAT, "tensor '%s' not found", name);
-    const int r = t->ndim == 2 ? (int)t->shape[0] : -1, c = t->ndim == 2 ? (int)t->shape[1] : -1;
+    /* shapes compared as int64 (a dimension of 2^32 + n must not pass as n) */
+    const int64_t r = t->ndim == 2 ? t->shape[0] : -1, c = t->ndim == 2 ? t->shape[1] : -1;
+    const int64_t n = (int64_t)in * out;
     if (conv1d) {
-        if (r != in || c != out) return g2i_err(G2_E_FORMAT, "tensor '%s': expected [%d,%d], got [%d,%d]", name, in, out, r, c);
-        return g2h_st_read_f32(st, t, dst);
+        if (r != in || c != out || t->numel != n)
+            return g2i_err(G2_E_FORMAT, "tensor '%s': expected [%d,%d], got [%lld,%lld]", name, in, out,
+                           (long long)r, (long long)c);
+        return g2h_st_read_f32(st, t, dst, n);
     }
-    if (r != out || c != in) return g2i_err(G2_E_FORMAT, "tensor '%s': expected [%d,%d], got [%d,%d]", name, out, in, r, c);
+    if (r != out || c != in || t->numel != n)
+        return g2i_err(G2_E_FORMAT, "tensor '%s': expected [%d,%d], got [%lld,%lld]", name, out, in,
+                       (long long)r, (long long)c);
     float *tmp = malloc((size_t)in * out * sizeof(float));
     if (!tmp) return g2i_err(G2_E_NOMEM, "staging %s", name);
-    int rc = g2h_st_read_f32(st, t, tmp);
+    int rc = g2h_st_read_f32(st, t, tmp, n);
     if (!rc)
         for (int o = 0; o < out; ++o)
             for (int i = 0; i < in; ++i) dst[(size_t)i * out + o] = tmp[(size_t)o * in + i];
@@ -450,7 +456,7 @@ static int read_vec(const g2h_st *st, const char *name, int64_t n, float *dst)
     const g2h_tensor *t = g2h_st_find(st, name);
     if (!t) return g2i_err(G2_E_FORMAT, "tensor '%s' not found", name);
     if (t->numel != n) return g2i_err(G2_E_FORMAT, "tensor '%s': %lld elements, expected %lld", name, (long long)t->numel, (long long)n);
-    return g2h_st_read_f32(st, t, dst);
+    return g2h_st_read_f32(st, t, dst, n);
 }
 
 int g2_model_load(const char *dir, int weight_dtype, int path, g2_model **out)
@@ -499,7 +505,7 @@ int g2_model_load(const char *dir, int weight_dtype, int path, g2_model **out)
         const g2h_tensor *t = g2h_st_find(&st, "wpe.weight");
         if (!t) rc = g2i_err(G2_E_FORMAT, "tensor 'wpe.weight' not found");
         else if (t->numel % E || t->numel / E > G2_KV_MAX_SEQ) rc = g2i_err(G2_E_FORMAT, "wpe.weight has a bad shape");
-        else rc = g2h_st_read_f32(&st, t, wpe);
+        else rc = g2h_st_read_f32(&st, t, wpe, (int64_t)G2_KV_MAX_SEQ * E);
     }
     if (!rc) rc = read_vec(&st, "ln_f.weight", E, lnf_w);
     if (!rc) rc = read_vec(&st, "ln_f.bias", E, lnf_b);
@@ -511,9 +517,10 @@ int g2_model_load(const char *dir, int weight_dtype, int path, g2_model **out)
         if (lm) {
             lmh = malloc((size_t)V * E * sizeof(float));
             if (!lmh) rc = g2i_err(G2_E_NOMEM, "lm_head staging");
-            else if (lm->ndim == 2 && lm->shape[0] == V && lm->shape[1] == E) rc = g2h_st_read_f32(&st, lm, lmh);
+            else if (lm->ndim == 2 && lm->shape[0] == V && lm->shape[1] == E)
+                rc = g2h_st_read_f32(&st, lm, lmh, (int64_t)V * E);
             else if (lm->ndim == 2 && lm->shape[0] == E && lm->shape[1] == V) {
-                rc = g2h_st_read_f32(&st, lm, buf);
+                rc = g2h_st_read_f32(&st, lm, buf, (int64_t)V * E);
                 if (!rc)
                     for (int v = 0; v < V; ++v)
                         for (int k = 0; k < E; ++k) lmh[(size_t)v * E + k] = buf[(size_t)k * V + v];
