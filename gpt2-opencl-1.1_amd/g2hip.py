@@ -299,29 +299,74 @@ def convert_f16(x):
     return out
 
 
-def synth_weights(cfg, seed, f16_round=False):
+LAYER_SLOTS = ("ln1_w", "ln1_b", "qkv_w", "qkv_b", "proj_w", "proj_b", "ln2_w", "ln2_b", "fc_w", "fc_b",
+               "fc2_w", "fc2_b")
+
+# Scales of the affine parameters synth_weights(affine=True) draws: biases
+# N(0, AFFINE_BIAS_STD), LayerNorm gamma 1 + N(0, AFFINE_LN_STD), beta N(0, AFFINE_LN_STD).
+AFFINE_BIAS_STD = 0.02
+AFFINE_LN_STD = 0.1
+
+
+def synth_weights(cfg, seed, f16_round=False, affine=False):
     """Host copy of the synthetic random-init weights g2_model_synth builds:
     dict with wte [V,E], wpe [1024,E], lnf_w, lnf_b and `layers`, a list of
-    12-tuples (ln1_w, ln1_b, qkv_w, qkv_b, proj_w, proj_b, ln2_w, ln2_b, fc_w,
-    fc_b, fc2_w, fc2_b) with matrices in the Conv1D [in,out] layout.  With
-    f16_round the matrices and embeddings are rounded to fp16 values (kept
-    as float32), i.e. what the fp16 weight format stores."""
+    12-tuples in LAYER_SLOTS order (ln1_w, ln1_b, qkv_w, qkv_b, proj_w,
+    proj_b, ln2_w, ln2_b, fc_w, fc_b, fc2_w, fc2_b) with matrices in the
+    Conv1D [in,out] layout.  With f16_round the matrices and embeddings are
+    rounded to fp16 values (kept as float32), i.e. what the fp16 weight
+    format stores.  With affine, every bias vector and LayerNorm gamma/beta
+    (ln_1, ln_2, ln_f) is drawn at random instead of 0 / 1 / 0 (biases
+    N(0, 0.02), gamma 1 + N(0, 0.1), beta N(0, 0.1), from a numpy generator
+    seeded with `seed`), so each of them has a distinct, visible effect."""
     E, F, V = cfg.n_embd, cfg.ffn_dim, cfg.vocab_size
 
     def rnd(a):
         return a.astype(np.float16).astype(np.float32) if f16_round else a
 
+    rng = np.random.default_rng(seed ^ 0x5A17) if affine else None
+
+    def bias(n):
+        if not affine:
+            return np.zeros(n, np.float32)
+        return (rng.standard_normal(n) * AFFINE_BIAS_STD).astype(np.float32)
+
+    def gamma():
+        if not affine:
+            return np.ones(E, np.float32)
+        return (1.0 + rng.standard_normal(E) * AFFINE_LN_STD).astype(np.float32)
+
+    def beta():
+        if not affine:
+            return np.zeros(E, np.float32)
+        return (rng.standard_normal(E) * AFFINE_LN_STD).astype(np.float32)
+
     wte = rnd(synth_normal(V * E, seed, synth_tensor_id(-1, 1)).reshape(V, E))
     wpe = rnd(synth_normal(MAX_SEQ * E, seed, synth_tensor_id(-1, 2)).reshape(MAX_SEQ, E))
-    ones_e, zeros_e = np.ones(E, np.float32), np.zeros(E, np.float32)
     layers = []
     for l in range(cfg.n_layer):
         mats = []
         for w, (i, o) in enumerate([(E, 3 * E), (E, E), (E, F), (F, E)]):
             mats.append(rnd(synth_normal(i * o, seed, synth_tensor_id(l, w)).reshape(i, o)))
-        layers.append((ones_e, zeros_e, mats[0], np.zeros(3 * E, np.float32), mats[1], zeros_e,
-                       ones_e, zeros_e, mats[2], np.zeros(F, np.float32), mats[3], zeros_e))
-    return {"wte": wte, "wpe": wpe, "lnf_w": ones_e, "lnf_b": zeros_e, "layers": layers}
+        layers.append((gamma(), beta(), mats[0], bias(3 * E), mats[1], bias(E),
+                       gamma(), beta(), mats[2], bias(F), mats[3], bias(E)))
+    return {"wte": wte, "wpe": wpe, "lnf_w": gamma(), "lnf_b": beta(), "layers": layers}
+
+
+def swap_slots(weights, a, b, layer=None):
+    """Copy of a synth_weights dict with layer slots a and b (LAYER_SLOTS
+    names) exchanged in one layer (all layers if layer is None): a planted
+    wiring mistake for checking that a parity test notices it."""
+    ia, ib = LAYER_SLOTS.index(a), LAYER_SLOTS.index(b)
+    out = dict(weights)
+    layers = []
+    for l, lw in enumerate(weights["layers"]):
+        lw = list(lw)
+        if layer is None or l == layer:
+            lw[ia], lw[ib] = lw[ib], lw[ia]
+        layers.append(tuple(lw))
+    out["layers"] = layers
+    return out
 
 
 # ---------------------------------------------------------------- model

@@ -373,6 +373,18 @@ or_model *or_model_create(int n_layer, int n_embd, int n_head, int vocab,
     return m;
 }
 
+/* A separate lm_head [vocab, n_embd] instead of the tied wte (main.c:1374-1405:
+ * lm_head.weight present in the file): padded and transposed the same way. */
+void or_model_set_lm_head(or_model *m, const float *lm)
+{
+    const size_t E = (size_t)m->n_embd, V = (size_t)m->padded_vocab;
+    memset(m->lm_head, 0, E * V * sizeof(float));
+    #pragma omp parallel for schedule(static)
+    for (int k = 0; k < (int)E; ++k)
+        for (int n = 0; n < m->vocab; ++n)
+            m->lm_head[(size_t)k * V + n] = lm[(size_t)n * E + k];
+}
+
 void or_model_destroy(or_model *m)
 {
     if (!m) return;

@@ -44,6 +44,7 @@ for _n, _a, _r in [
     ("or_attn_out_1q", [_vp, _vp, _vp, _i, _i, _i, _i, _i], None),
     ("or_model_create", [_i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp], _vp),
     ("or_model_destroy", [_vp], None),
+    ("or_model_set_lm_head", [_vp, _vp], None),
     ("or_prefill", [_vp, _vp, _i], None),
     ("or_decode", [_vp, _i, _i], None),
     ("or_logits", [_vp], C.POINTER(C.c_float)),
@@ -170,7 +171,8 @@ def attn_out_1q(scores, v_cache, T_kv, D, DH, out_base, out_len, row_stride=1024
 
 class Model:
     """Oracle GPT-2 over host weights in the Conv1D [in,out] layout (the dict
-    of g2hip.synth_weights).  kslice pins the split-K slice count of the
+    of g2hip.synth_weights; an optional "lm_head" [V, E] entry replaces the
+    tied head).  kslice pins the split-K slice count of the
     attn_proj / ffn2 matvecs (the reference tunes it at start-up)."""
 
     def __init__(self, cfg, weights, kslice=4):
@@ -190,6 +192,8 @@ class Model:
         self.h = _lib.or_model_create(cfg.n_layer, cfg.n_embd, cfg.n_head, cfg.vocab_size,
                                       cfg.ffn_dim, kslice, ptr(weights["wte"]), ptr(weights["wpe"]),
                                       ptr(weights["lnf_w"]), ptr(weights["lnf_b"]), flat)
+        if weights.get("lm_head") is not None:  # separate [V, E] head instead of the tied wte
+            _lib.or_model_set_lm_head(self.h, ptr(weights["lm_head"]))
         self.padded_vocab = (cfg.vocab_size + 3) & ~3
 
     def close(self):

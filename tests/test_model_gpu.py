@@ -3,15 +3,16 @@
 Both execution paths (the reference operator sequence and the fused gfx950
 path), fp32 and fp16 weights, on the same synthetic random-init weights and
 random prompts.  Greedy ids must be identical (tests/parity.py allows a
-parting only at a reference near-tie), and per-step logits under teacher
-forcing must stay within max-abs 2e-3 / rel 1e-3 (fp32) and 5e-2 (fp16
+parting only where the oracle's own top-2 gap is below 1e-4), and every
+step teacher-forced along the oracle's ids must give the oracle's greedy
+choice and logits within max-abs 2e-3 / rel 1e-3 (fp32) and 5e-2 (fp16
 weights) of the oracle's.
 """
 import numpy as np
 import pytest
 
 from oracle import oracle
-from parity import greedy_agree, random_prompt
+from parity import TIE_TOL, greedy_agree, masked_first_max, random_prompt
 
 pytestmark = pytest.mark.gpu
 
@@ -28,26 +29,36 @@ def check_logits(got, ref, f16):
     np.testing.assert_allclose(got, ref, rtol=rtol, atol=atol)
 
 
-def run_parity(g2, cfg, path, dtype, P, n_new, tf_steps, seed=SEED, kslice=4):
+def run_parity(g2, cfg, path, dtype, P, n_new, seed=SEED, kslice=4):
+    """Free-running greedy generation against the oracle's ids, then every
+    step teacher-forced along the oracle's ids: logits within the parity
+    bound and the greedy choice equal to the oracle's (near ties aside)."""
     f16 = dtype == g2.F16
     w = g2.synth_weights(cfg, seed, f16_round=f16)
     om = oracle.Model(cfg, w, kslice=kslice)
     prompt = random_prompt(P, cfg.vocab_size, seed + P)
     print(f"[model] L{cfg.n_layer} E{cfg.n_embd} V{cfg.vocab_size} path {path} dtype {dtype} P {P} new {n_new}",
           flush=True)
-    ref_ids, top2, ref_lg = om.generate(prompt, n_new, logit_steps=tf_steps + 1)
+    ref_ids, top2, _ = om.generate(prompt, n_new, min_new=n_new)
+    ref_lg = om.teacher_forced(prompt, ref_ids[:-1])
+    gaps = top2[:, 0] - top2[:, 1]
     m = g2.Model.synth(cfg, seed, dtype, path)
     if path == g2.PATH_REFERENCE:
         m.set_kslice(kslice)
-    ids, timing = m.generate(prompt, n_new)
-    agree = greedy_agree(ids, ref_ids, top2, tie_tol=1e-2 if f16 else 1e-4)
-    assert agree == len(ref_ids) or agree > 0
-    # teacher-forced per-step logits along the oracle's own ids
+    ids, timing = m.generate(prompt, n_new, min_new=n_new)
+    agree = greedy_agree(ids, ref_ids, top2)
     m.prefill(prompt)
-    check_logits(m.logits(), ref_lg[0], f16)
-    for k in range(tf_steps):
-        m.decode(ref_ids[k], P + k)
-        check_logits(m.logits(), ref_lg[k + 1], f16)
+    max_err = 0.0
+    for k in range(len(ref_ids)):
+        if k > 0:
+            m.decode(int(ref_ids[k - 1]), P + k - 1)
+        lg = m.logits()
+        check_logits(lg, ref_lg[k], f16)
+        max_err = max(max_err, float(np.abs(lg - ref_lg[k]).max()))
+        c = masked_first_max(lg)
+        assert c == ref_ids[k] or gaps[k] < TIE_TOL, f"teacher-forced step {k}: {c} vs {ref_ids[k]}"
+    print(f"[model] free-running ids agree for {agree} of {len(ref_ids)}; teacher-forced max logit error "
+          f"{max_err:.3e}", flush=True)
     m.free()
     om.close()
     return ids, ref_ids, timing
@@ -55,22 +66,23 @@ def run_parity(g2, cfg, path, dtype, P, n_new, tf_steps, seed=SEED, kslice=4):
 
 @pytest.mark.parametrize("path", [0, 1], ids=["reference", "fused"])
 def test_tiny_fp32(g2, path):
-    ids, ref_ids, _ = run_parity(g2, tiny_cfg(g2), path, g2.F32, P=17, n_new=40, tf_steps=8)
+    ids, ref_ids, _ = run_parity(g2, tiny_cfg(g2), path, g2.F32, P=17, n_new=40)
     np.testing.assert_array_equal(ids, ref_ids)
 
 
 def test_tiny_fp16_fused(g2):
-    run_parity(g2, tiny_cfg(g2), g2.PATH_FUSED, g2.F16, P=17, n_new=40, tf_steps=8)
+    run_parity(g2, tiny_cfg(g2), g2.PATH_FUSED, g2.F16, P=17, n_new=40)
 
 
 @pytest.mark.parametrize("path", [0, 1], ids=["reference", "fused"])
 def test_small_fp32(g2, path):
-    """GPT-2 small shape (12 layers, 768, 12 heads, vocab 50257)."""
-    run_parity(g2, g2.preset("small"), path, g2.F32, P=64, n_new=24, tf_steps=4)
+    """GPT-2 small shape (12 layers, 768, 12 heads, vocab 50257); the full
+    255-forward run is in test_full_depth_gpu.py."""
+    run_parity(g2, g2.preset("small"), path, g2.F32, P=64, n_new=24)
 
 
 def test_small_fp16_fused(g2):
-    run_parity(g2, g2.preset("small"), g2.PATH_FUSED, g2.F16, P=64, n_new=24, tf_steps=4)
+    run_parity(g2, g2.preset("small"), g2.PATH_FUSED, g2.F16, P=64, n_new=24)
 
 
 def test_prompt_edges(g2):
@@ -85,7 +97,7 @@ def test_prompt_edges(g2):
         ref_ids, top2, _ = om.generate(prompt, n_new)
         ids, _ = m.generate(prompt, n_new)
         assert len(ids) == min(n_new, 1024 - P)
-        greedy_agree(ids, ref_ids, top2, 1e-4)
+        greedy_agree(ids, ref_ids, top2)
 
 
 def test_eos_stop(g2):

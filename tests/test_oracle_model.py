@@ -32,13 +32,16 @@ def _torch():
 def hf_model(cfg, w):
     transformers = pytest.importorskip("transformers")
     torch = _torch()
+    tied = w.get("lm_head") is None
     hc = transformers.GPT2Config(vocab_size=cfg.vocab_size, n_positions=1024, n_embd=cfg.n_embd,
                                  n_layer=cfg.n_layer, n_head=cfg.n_head, n_inner=cfg.ffn_dim,
                                  activation_function="gelu_new", resid_pdrop=0.0, embd_pdrop=0.0,
-                                 attn_pdrop=0.0, layer_norm_epsilon=1e-5, bos_token_id=0, eos_token_id=0)
+                                 attn_pdrop=0.0, layer_norm_epsilon=1e-5, bos_token_id=0, eos_token_id=0,
+                                 tie_word_embeddings=tied)
     m = transformers.GPT2LMHeadModel(hc).eval().double()
     sd = {"transformer.wte.weight": w["wte"], "transformer.wpe.weight": w["wpe"],
-          "transformer.ln_f.weight": w["lnf_w"], "transformer.ln_f.bias": w["lnf_b"], "lm_head.weight": w["wte"]}
+          "transformer.ln_f.weight": w["lnf_w"], "transformer.ln_f.bias": w["lnf_b"],
+          "lm_head.weight": w["wte"] if tied else w["lm_head"]}
     for l, lw in enumerate(w["layers"]):
         for n, a in zip(NAMES, lw):
             sd[f"transformer.h.{l}.{n}"] = a
@@ -66,10 +69,14 @@ def hf_logits(m, ids):
         return m(torch.tensor(np.asarray(ids, np.int64)[None])).logits[0].numpy()
 
 
+@pytest.mark.parametrize("affine", [False, True], ids=["plain", "affine"])
 @pytest.mark.parametrize("L,E,H,V", [(2, 128, 2, 256), (3, 192, 3, 1000)])
-def test_prefill_decode_vs_transformers(L, E, H, V):
+def test_prefill_decode_vs_transformers(L, E, H, V, affine):
+    """affine: every bias and LayerNorm gamma/beta random (ln_1, ln_2, ln_f,
+    c_attn, attn.c_proj, c_fc, mlp.c_proj: main.c:1752-1828 order), so each
+    parameter's slot in the composition is pinned against transformers."""
     cfg = g2hip.make_config(L, E, H, vocab_size=V)
-    w = g2hip.synth_weights(cfg, 11)
+    w = g2hip.synth_weights(cfg, 11, affine=affine)
     om = oracle.Model(cfg, w)
     hf = hf_model(cfg, w)
     prompt = random_prompt(21, V, 2)
@@ -84,9 +91,29 @@ def test_prefill_decode_vs_transformers(L, E, H, V):
         np.testing.assert_allclose(om.logits(), hf_logits(hf, ids)[-1], rtol=1e-5, atol=2e-6)
 
 
-def test_generate_vs_transformers_greedy():
+def test_separate_lm_head_vs_transformers():
+    """A file with its own lm_head.weight (main.c:1374-1405): the oracle's
+    head replaces the tied wte; pinned against an untied transformers model."""
+    cfg = g2hip.make_config(2, 128, 2, vocab_size=256)
+    w = g2hip.synth_weights(cfg, 21, affine=True)
+    w["lm_head"] = (np.random.default_rng(4).standard_normal((256, 128)) * 0.02).astype(np.float32)
+    om = oracle.Model(cfg, w)
+    hf = hf_model(cfg, w)
+    assert hf.lm_head.weight.data_ptr() != hf.transformer.wte.weight.data_ptr()
+    prompt = random_prompt(15, 256, 8)
+    om.prefill(prompt)
+    np.testing.assert_allclose(om.logits(), hf_logits(hf, prompt)[-1], rtol=1e-5, atol=2e-6)
+    w_tied = dict(w)
+    w_tied["lm_head"] = None
+    om2 = oracle.Model(cfg, w_tied)
+    om2.prefill(prompt)
+    assert np.abs(om2.logits() - om.logits()).max() > 1e-2  # the separate head is really used
+
+
+@pytest.mark.parametrize("affine", [False, True], ids=["plain", "affine"])
+def test_generate_vs_transformers_greedy(affine):
     cfg = g2hip.make_config(2, 128, 2, vocab_size=512)
-    w = g2hip.synth_weights(cfg, 12)
+    w = g2hip.synth_weights(cfg, 12, affine=affine)
     om = oracle.Model(cfg, w)
     hf = hf_model(cfg, w)
     prompt = random_prompt(9, 512, 3)
@@ -164,3 +191,37 @@ def test_generation_protocol_lengths():
     assert len(ids) == 1
     ids, top2, _ = om.generate(random_prompt(10, 128, 2), 7)
     assert len(ids) == 7 and np.all(top2[:, 0] >= top2[:, 1])
+
+
+SWAPS = [("ln1_b", "proj_b"), ("proj_b", "fc2_b"), ("ln1_w", "ln2_w"), ("ln1_b", "ln2_b"), ("ln2_b", "fc2_b")]
+
+
+@pytest.mark.parametrize("a,b", SWAPS, ids=[f"{a}-{b}" for a, b in SWAPS])
+def test_planted_slot_swap_fails_the_pin(a, b):
+    """A mistake planted in the oracle's input: two same-sized parameter
+    slots exchanged in one layer.  The transformers pin above must reject it
+    (its tolerance is 1e-5), and so must the GPU model tests that use the
+    same affine weights, whose logits tolerance is 2e-3: every planted swap
+    moves some logit by more than that, at the first and the last layer."""
+    cfg = g2hip.make_config(3, 192, 3, vocab_size=1000)
+    w = g2hip.synth_weights(cfg, 11, affine=True)
+    prompt = random_prompt(21, cfg.vocab_size, 2)
+    hf = hf_model(cfg, w)
+    ref = hf_logits(hf, prompt)[-1]
+    for layer in (0, cfg.n_layer - 1):
+        om = oracle.Model(cfg, g2hip.swap_slots(w, a, b, layer))
+        om.prefill(prompt)
+        d = float(np.abs(om.logits() - ref).max())
+        om.close()
+        assert d > 2e-3, f"swap {a}<->{b} in layer {layer} moved the logits by only {d:.2e}"
+        with pytest.raises(AssertionError):
+            np.testing.assert_allclose(om_logits_of(cfg, g2hip.swap_slots(w, a, b, layer), prompt), ref,
+                                       rtol=1e-5, atol=2e-6)
+
+
+def om_logits_of(cfg, w, prompt):
+    om = oracle.Model(cfg, w)
+    om.prefill(prompt)
+    out = om.logits()
+    om.close()
+    return out
