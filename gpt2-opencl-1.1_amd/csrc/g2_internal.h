@@ -15,6 +15,10 @@
 #include "g2hip.h"
 #include "g2_kargs.h"
 
+#ifdef __cplusplus
+extern "C" {
+#endif
+
 /* Packed-matvec kernels of one epilogue: f32/f16 twins of the four lane
  * shapes (see g2_decode.hip and rows_shape in g2_shim.c). */
 #define G2_ROWS_LIST(X, E, s)                                                 \
@@ -102,5 +106,17 @@ int g2i_attn_launch(g2_attn1q_args *a, unsigned chunks);
 
 /* host helpers (g2_host.c) */
 void g2i_f32_to_f16(uint16_t *dst, const float *src, size_t n);
+
+/* Static device scratch of g2_attn_1q_noalloc (g2_noalloc.hip): the chunk
+ * partials of up to 64 heads x G2_ATTN_MAX_CHUNKS chunks, 66 floats each.
+ * setup resolves its address on a device (the device current); scratch
+ * returns it, or NULL before setup. */
+#define G2_NOALLOC_SCRATCH_FLOATS (64 * G2_ATTN_MAX_CHUNKS * 66)
+int g2i_noalloc_setup(int device);
+float *g2i_noalloc_scratch(int device);
+
+#ifdef __cplusplus
+}
+#endif
 
 #endif /* G2_INTERNAL_H */

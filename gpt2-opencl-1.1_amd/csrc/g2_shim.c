@@ -39,6 +39,8 @@ static struct {
     hipFunction_t fn[G2F_COUNT];
     float *scratch;
     float *attn_part;
+    int noalloc_rc;         /* g2i_noalloc_setup result at g2_init */
+    char noalloc_err[256];
 } G;
 
 static char g_errbuf[512] = "no error";
@@ -205,6 +207,10 @@ int g2_init(int device)
         }
         (void)hipGetLastError();
     }
+    /* the allocation-free entry point's scratch: resolve its address on this
+     * device now; a failure only disables that entry point */
+    G.noalloc_rc = g2i_noalloc_setup(device);
+    if (G.noalloc_rc) snprintf(G.noalloc_err, sizeof G.noalloc_err, "%s", g2_last_error());
     G.device = device;
     G.ready = 1;
     (void)g2_hsaco_end;
@@ -504,6 +510,34 @@ int g2_attn_1q(const float *qkv, const float *k_cache, const float *v_cache, flo
     memset(&a, 0, sizeof a);
     a.q = qkv + q_base; a.k_cache = k_cache; a.v_cache = v_cache; a.out = out + out_base;
     a.part = G.attn_part;
+    a.T_fixed = T_kv; a.D = D; a.NH = NH; a.S = max_seq; a.max_chunks = G2_ATTN_MAX_CHUNKS;
+    a.scale = scale;
+    return g2i_attn_launch(&a, cdiv(T_kv, G2_ATTN_CHUNK));
+}
+
+/* g2_attn_1q without allocation: the chunk partials go to the static device
+ * scratch resolved at g2_init (g2_noalloc.hip), not to a library buffer.
+ * Nothing is allocated or freed here; every partial the merge reads is
+ * written by the same call, so no clearing is needed. */
+int g2_attn_1q_noalloc(const float *qkv, const float *k_cache, const float *v_cache, float *out,
+                       int q_base, int T_kv, int D, int NH, int max_seq, int out_base, float scale)
+{
+    NEED_READY();
+    if (NH > 0 && (long)NH * G2_ATTN_MAX_CHUNKS * 66 > G2_NOALLOC_SCRATCH_FLOATS)
+        return g2i_err(G2_E_LIMIT, "g2_attn_1q_noalloc: %d heads need %ld scratch floats, the static scratch "
+                       "holds %d (64 heads)", NH, (long)NH * G2_ATTN_MAX_CHUNKS * 66, G2_NOALLOC_SCRATCH_FLOATS);
+    if (G.noalloc_rc) return g2i_err(G2_E_HIP, "g2_attn_1q_noalloc: no static scratch: %s", G.noalloc_err);
+    if (!qkv || !k_cache || !v_cache || !out) return g2i_err(G2_E_ARG, "g2_attn_1q_noalloc: NULL buffer");
+    if (NH <= 0 || NH * 64 != D)
+        return g2i_err(G2_E_ARG, "g2_attn_1q_noalloc: needs head dim 64 (D=%d NH=%d)", D, NH);
+    if (T_kv <= 0 || T_kv > max_seq || max_seq > G2_MAX_SEQ || q_base < 0 || out_base < 0)
+        return g2i_err(G2_E_ARG, "g2_attn_1q_noalloc: bad sizes");
+    float *part = g2i_noalloc_scratch(G.device);
+    if (!part) return g2i_err(G2_E_STATE, "g2_attn_1q_noalloc: static scratch not resolved on device %d", G.device);
+    g2_attn1q_args a;
+    memset(&a, 0, sizeof a);
+    a.q = qkv + q_base; a.k_cache = k_cache; a.v_cache = v_cache; a.out = out + out_base;
+    a.part = part;
     a.T_fixed = T_kv; a.D = D; a.NH = NH; a.S = max_seq; a.max_chunks = G2_ATTN_MAX_CHUNKS;
     a.scale = scale;
     return g2i_attn_launch(&a, cdiv(T_kv, G2_ATTN_CHUNK));

@@ -91,6 +91,7 @@ for _n, _a in {
     "g2_attn_scores_1q": [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f],
     "g2_attn_softmax_1q": [_vp, _i, _i], "g2_attn_out_1q": [_vp, _vp, _vp, _i, _i, _i, _i],
     "g2_attn_1q": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f],
+    "g2_attn_1q_noalloc": [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _f],
     "g2_matvec_rows": [_vp, _vp, _i, _vp, _vp, _vp, _i, _i, _i],
     "g2_model_uses_graph": [_vp], "g2_read_kv": [_vp, _i, _vp, _vp],
     "g2_config_load": [C.c_char_p, C.POINTER(Config)], "g2_config_parse": [C.c_char_p, C.POINTER(Config)],
@@ -220,6 +221,12 @@ def matvec(A, B, bias, residual, Cb, N, K, apply_gelu=0, f16=False):
 def matvec_sk(A, B, partial, N, K, kslice, f16=False):
     fn = _lib.g2_matvec_sk_f16 if f16 else _lib.g2_matvec_sk
     check(fn(_p(A), _p(B), _p(partial), N, K, kslice))
+
+
+def attn_1q_noalloc(qkv, k_cache, v_cache, out, q_base, T_kv, D, NH, max_seq, out_base, scale):
+    """attn_1q with its chunk partials in the library's static device scratch."""
+    check(_lib.g2_attn_1q_noalloc(_p(qkv), _p(k_cache), _p(v_cache), _p(out), q_base, T_kv, D, NH,
+                                  max_seq, out_base, scale))
 
 
 def matvec_rows(x, W, w_dtype, bias, residual, y, N, K, apply_gelu=0):

@@ -134,6 +134,18 @@ int g2_attn_out_1q(const float *scores, const float *v_cache, float *out,
 int g2_attn_1q(const float *qkv, const float *k_cache, const float *v_cache,
                float *out, int q_base, int T_kv, int D, int NH, int max_seq,
                int out_base, float scale);
+/* g2_attn_1q that allocates nothing (no counterpart in the reference): for
+ * callers that cannot allocate device memory -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  Same
+ * arguments and results as g2_attn_1q; its chunk partials go to a static
+ * device array of 64 heads x 16 chunks x 66 floats (270 KB per GPU, held
+ * until the process ends) instead of a library buffer.  More than 64 heads:
+ * G2_E_LIMIT.  Every call on a GPU shares that array, so calls that overlap
+ * on one GPU (other streams or threads of the process) race; calls on the
+ * library stream run one after another. */
+int g2_attn_1q_noalloc(const float *qkv, const float *k_cache, const float *v_cache,
+                       float *out, int q_base, int T_kv, int D, int NH, int max_seq,
+                       int out_base, float scale);
 
 /* launch_matvec over the output-major weight layout the fused model uses:
  * y[n] = sum_k W[n*K + k] x[k] (+ bias[n]) (+ y[n] when residual == y);
