@@ -21,6 +21,7 @@
  */
 #include <hip/hip_runtime.h>
 #include "g2_kargs.h"
+#include "g2_step_plan.h"
 
 #define G2K extern "C" __global__ __launch_bounds__(256)
 

@@ -26,6 +26,7 @@
 
 #include "g2_internal.h"
 #include "g2_host.h"
+#include "g2_step_plan.h"
 
 typedef struct {
     float *ln1_w, *ln1_b, *qkv_b, *proj_b, *ln2_w, *ln2_b, *fc_b, *fc2_b;
@@ -163,35 +164,15 @@ static int check_model_config(const g2_config *c, int dtype, int path)
     return G2_OK;
 }
 
-/* (row, segment) units one work-group of the step kernel takes for an
- * N x K packed matrix: rows split evenly, each row in 1, 2, 4 or 8
- * segments of at most 256 16-byte chunks (more is not supported). */
-static int step_units(int N, int K, int elems_per_chunk, int nwg)
-{
-    const int C = K / elems_per_chunk, need = (C + 255) / 256;
-    if (need > 8) return 1 << 30;
-    const int nseg = need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : 8));
-    return ((N + nwg - 1) / nwg) * nseg;
-}
-
 /* Whether the persistent step kernel can run this model: fused path, a
- * device grid, the kernel's LDS ceilings (n_embd <= G2_STEP_MAXE, ffn <=
- * G2_STEP_MAXF) and at most G2_STEP_MAXUNITS units per work-group in every
- * matrix.  On refusal `why` names the reason. */
+ * device grid and the kernel's own limits (g2p_step_refusal, shared with
+ * the kernel's CPU address check).  On refusal `why` names the reason. */
 static int step_supported(const g2_model *m, int nwg, const char **why)
 {
     const g2_config *c = &m->cfg;
-    const int ve = m->dtype == G2_F16 ? 8 : 4;
-    const int E = c->n_embd, F = c->ffn_dim, V = c->vocab_size;
     if (m->path != G2_PATH_FUSED) { *why = "not the fused path"; return 0; }
-    if (nwg <= 0 || nwg > G2_STEP_THREADS) { *why = "no cooperative step grid (unsupported, or refused at g2_init)"; return 0; }
-    if (E > G2_STEP_MAXE || F > G2_STEP_MAXF) { *why = "n_embd or ffn above the step kernel's ceilings"; return 0; }
-    if (E % ve || F % ve || E != 64 * c->n_head) { *why = "sizes not multiples of the weight chunk or head dim not 64"; return 0; }
-    const int dims[5][2] = { { 3 * E, E }, { E, E }, { F, E }, { E, F }, { V, E } };
-    for (int i = 0; i < 5; ++i)
-        if (step_units(dims[i][0], dims[i][1], ve, nwg) > G2_STEP_MAXUNITS) { *why = "a matrix exceeds the units per work-group"; return 0; }
-    *why = NULL;
-    return 1;
+    *why = g2p_step_refusal(c->n_embd, c->n_head, c->ffn_dim, c->vocab_size, m->dtype == G2_F16 ? 8 : 4, nwg);
+    return *why == NULL;
 }
 
 /* Device tables of the step kernel (after the weights are uploaded). */

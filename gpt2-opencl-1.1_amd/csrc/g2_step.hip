@@ -347,25 +347,16 @@ __device__ __forceinline__ void layernorm(int tid, const float *x, float *xin, c
  * lanes x up to 4 chunks).  With
  * a register set of UM units per wave, unit u belongs to wave u % NW, slot
  * (u / NW) % UM, batch u / (NW * UM). */
-struct plan {
+struct plan : g2p_rows {
     const u32x4 *W;
-    int C, nseg, SL, r0, nrows, nunits;
 };
 
 template <typename WT>
 __device__ __forceinline__ plan make_plan(const void *W, int N, int K)
 {
-    constexpr int VE = chunk_t<WT>::V;
     plan p;
+    static_cast<g2p_rows &>(p) = g2p_rows_plan(N, K, chunk_t<WT>::V, blockIdx.x, gridDim.x);
     p.W = (const u32x4 *)W;
-    p.C = K / VE;
-    const int need = (p.C + SEGC - 1) / SEGC;
-    p.nseg = need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : 8));
-    p.SL = (p.C + p.nseg - 1) / p.nseg;
-    const long nwg = gridDim.x, wg = blockIdx.x;
-    p.r0 = (int)(((long)N * wg) / nwg);
-    p.nrows = (int)(((long)N * (wg + 1)) / nwg) - p.r0;
-    p.nunits = p.nrows * p.nseg;
     return p;
 }
 
@@ -382,16 +373,11 @@ __device__ __forceinline__ void load_set(int tid, u32x4 (&w)[UM][4], const plan 
     const int wave = tid >> 6, lane = tid & 63;
 #pragma unroll
     for (int j = 0; j < UM; ++j) {
-        const int u = batch * NW * UM + wave + NW * j;
-        const bool uv = u < p.nunits;
-        const int row = p.r0 + (uv ? u / p.nseg : 0);
-        const int c0 = (uv ? u % p.nseg : 0) * p.SL;
-        const int c1 = min(p.C, c0 + p.SL);
+        const g2p_unit un = g2p_unit_at(&p, UM, batch, wave, j);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             /* a unit past the share reads one chunk with every lane (one line) */
-            const int cc = uv ? min(c0 + lane + 64 * i, c1 - 1) : 0;
-            w[j][i] = __builtin_nontemporal_load(gl(p.W) + (size_t)row * p.C + cc);
+            w[j][i] = __builtin_nontemporal_load(gl(p.W) + g2p_unit_chunk(&un, lane, i));
         }
     }
 }
@@ -405,17 +391,15 @@ __device__ __forceinline__ void dot_set(int tid, const u32x4 (&w)[UM][4], const 
 {
     constexpr int VE = chunk_t<WT>::V;
     const int wave = tid >> 6, lane = tid & 63;
-    const int c0 = (wave % p.nseg) * p.SL;
-    const int c1 = min(p.C, c0 + p.SL);
     if (batch * NW * UM + wave >= p.nunits) return; /* wave-uniform */
     float xv[4][VE];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int cc = c0 + lane + 64 * i;
+        const int cc = g2p_dot_chunk(&p, wave, lane, i);
 #pragma unroll
         for (int e = 0; e < VE; e += 4) {
             f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
-            if (cc < c1) v = *(const f32x4 *)(xin + cc * VE + e);
+            if (cc >= 0) v = *(const f32x4 *)(xin + cc * VE + e);
             xv[i][e] = v.x; xv[i][e + 1] = v.y; xv[i][e + 2] = v.z; xv[i][e + 3] = v.w;
         }
     }
@@ -504,17 +488,15 @@ __device__ __forceinline__ void attn_load(int tid, const g2_step_layer &y, att_r
      * without a unit points every lane at the first 16 bytes of the caches,
      * so its loads cost one line each instead of 32 KB of memory traffic
      * queued in front of the work-group's later reads. */
-    (void)T; (void)pos;
-    const size_t koff = on ? (size_t)(h * 64 + 4 * dg) * S + jk : 0, kstr = on ? (size_t)(S / 4) : 0;
+    (void)T; (void)pos; (void)j0; (void)pq; (void)dg; (void)jk; (void)d4; (void)jg;
+    long koff, voff[4];
+    g2p_attn_offsets(t, on, h, ch, E, S, &koff, voff);
+    const size_t kstr = on ? (size_t)(S / 4) : 0;
     const G2_GLOBAL f32x4 *kb = gl((const f32x4 *)(y.k_cache + koff));
 #pragma unroll
     for (int d = 0; d < 4; ++d) r.kv[d] = kb[(size_t)d * kstr];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int j = j0 + 4 * jg + e;
-        const size_t voff = on ? (size_t)j * E + h * 64 + 4 * d4 : 0;
-        r.vv[e] = *gl((const f32x4 *)(y.v_cache + voff));
-    }
+    for (int e = 0; e < 4; ++e) r.vv[e] = *gl((const f32x4 *)(y.v_cache + voff[e]));
 }
 
 /* The attention of one 64-position chunk once L.q, L.kn and L.vn hold the
@@ -862,7 +844,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             const int rounds = (nunits + 2 * nwg - 1) / (2 * nwg);
             const int hf = tid >> 8;
             for (int rd = 0; rd < rounds; ++rd) {
-                const int u = wg + nwg * (2 * rd + hf);
+                const int u = g2p_attn_unit(wg, nwg, rd, hf);
                 const bool on = u < nunits;
                 const int h = on ? u / nch : 0, ch = on ? u % nch : 0;
                 attn_load(tid, y, ar[0], on, h, ch, pos, T, E, S);

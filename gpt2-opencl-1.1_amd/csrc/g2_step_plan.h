@@ -1,0 +1,132 @@
+/*
+ * g2_step_plan.h -- index arithmetic of the persistent decode-step kernel
+ * (g2_step.hip): which rows and 16-byte chunks of each packed matrix a
+ * work-group and lane load, and which KV-cache entries an attention unit
+ * reads.  Plain integer functions, compiled both into the kernel and into
+ * the CPU address check (tests/native/step_addr.cpp), so the check runs the
+ * kernel's own address computations.
+ */
+#ifndef G2_STEP_PLAN_H
+#define G2_STEP_PLAN_H
+
+#include "g2_kargs.h"
+
+#if defined(__HIPCC__) || defined(__HIP__)
+#define G2P_FN __host__ __device__ __forceinline__
+#else
+#define G2P_FN static inline
+#endif
+
+#define G2P_NW (G2_STEP_THREADS / 64) /* waves per work-group */
+#define G2P_SEGC 256                  /* chunks per (row, segment) unit: 64 lanes x 4 */
+
+G2P_FN int g2p_min(int a, int b) { return a < b ? a : b; }
+
+/* A work-group's share of one packed matrix W[N,K] (output-major, K / VE
+ * 16-byte chunks per row of VE elements each): rows [r0, r0 + nrows), split
+ * evenly over the nwg work-groups; each row in nseg (1, 2, 4 or 8: a divisor
+ * of the wave count) segments of SL <= 256 chunks; a (row, segment) unit is
+ * one wave's job, 64 lanes x up to 4 chunks. */
+typedef struct {
+    int C, nseg, SL, r0, nrows, nunits;
+} g2p_rows;
+
+G2P_FN g2p_rows g2p_rows_plan(int N, int K, int VE, long wg, long nwg)
+{
+    g2p_rows p;
+    p.C = K / VE;
+    const int need = (p.C + G2P_SEGC - 1) / G2P_SEGC;
+    p.nseg = need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : 8));
+    p.SL = (p.C + p.nseg - 1) / p.nseg;
+    p.r0 = (int)(((long)N * wg) / nwg);
+    p.nrows = (int)(((long)N * (wg + 1)) / nwg) - p.r0;
+    p.nunits = p.nrows * p.nseg;
+    return p;
+}
+
+/* Unit j of a register set of UM units per wave, for the batch `batch` of
+ * the share, as loaded by wave `wave`: unit u = batch*NW*UM + wave + NW*j,
+ * its row's first chunk (base = row * C) and its column chunks [c0, clast].
+ * Every load is unconditional: a unit past the share (uv = 0) reads chunk 0
+ * of the share's first row with every lane. */
+typedef struct {
+    long base;
+    int c0, clast, uv;
+} g2p_unit;
+
+G2P_FN g2p_unit g2p_unit_at(const g2p_rows *p, int UM, int batch, int wave, int j)
+{
+    g2p_unit a;
+    const int u = batch * G2P_NW * UM + wave + G2P_NW * j;
+    a.uv = u < p->nunits;
+    const int row = p->r0 + (a.uv ? u / p->nseg : 0);
+    a.c0 = (a.uv ? u % p->nseg : 0) * p->SL;
+    a.clast = g2p_min(p->C, a.c0 + p->SL) - 1;
+    a.base = (long)row * p->C;
+    return a;
+}
+
+/* The chunk (row * C + column chunk) that lane `lane` loads into slot i of
+ * unit a: a lane past the segment's end reads the segment's last chunk
+ * (which the same instruction fetches anyway). */
+G2P_FN long g2p_unit_chunk(const g2p_unit *a, int lane, int i)
+{
+    return a->base + (a->uv ? g2p_min(a->c0 + lane + 64 * i, a->clast) : 0);
+}
+
+/* The x chunk lane `lane` of wave `wave` multiplies in slot i of the dot
+ * products (every unit of a wave has segment wave % nseg); -1 when the slot
+ * lies past the segment (its product is skipped). */
+G2P_FN int g2p_dot_chunk(const g2p_rows *p, int wave, int lane, int i)
+{
+    const int c0 = (wave % p->nseg) * p->SL;
+    const int c1 = g2p_min(p->C, c0 + p->SL);
+    const int cc = c0 + lane + 64 * i;
+    return cc < c1 ? cc : -1;
+}
+
+/* Attention unit (head h, 64-position chunk ch) by the 256 threads of one
+ * half of a work-group, thread t: the K-cache floats it loads are
+ * koff + d*S .. + 3 for d < 4 (transposed cache [E][S]: dims 4dg..4dg+3 of
+ * the head at positions j0+4pq..+3), the V-cache floats voff[e] .. + 3 for
+ * e < 4 (cache [S][E]: position j0+4jg+e, dims 4d4..+3).  A half without a
+ * unit (on = 0) points every lane at the caches' first 16 bytes. */
+G2P_FN void g2p_attn_offsets(int t, int on, int h, int ch, int E, int S, long *koff, long *voff)
+{
+    const int j0 = ch * 64;
+    const int pq = t & 15, dg = t >> 4, jk = j0 + 4 * pq;
+    const int d4 = t & 15, jg = t >> 4;
+    *koff = on ? (long)(h * 64 + 4 * dg) * S + jk : 0;
+    for (int e = 0; e < 4; ++e) {
+        const int jj = j0 + 4 * jg + e;
+        voff[e] = on ? (long)jj * E + h * 64 + 4 * d4 : 0;
+    }
+}
+
+/* Whether the step kernel can run a model of n_embd E (NH heads of 64),
+ * ffn F and vocabulary V with VE weight elements per 16-byte chunk on a grid
+ * of nwg work-groups: E and F within its LDS buffers, whole chunks, and for
+ * every matrix at most G2_STEP_MAXUNITS (row, segment) units per work-group
+ * (hence at most that many rows: one epilogue thread per row) and at most 8
+ * segments per row.  Returns NULL if it can, else the reason. */
+G2P_FN const char *g2p_step_refusal(int E, int NH, int F, int V, int VE, int nwg)
+{
+    if (nwg <= 0 || nwg > G2_STEP_THREADS) return "no step grid";
+    if (E > G2_STEP_MAXE || F > G2_STEP_MAXF) return "n_embd or ffn above the step kernel's ceilings";
+    if (E % VE || F % VE || E != 64 * NH) return "sizes not multiples of the weight chunk or head dim not 64";
+    const int dims[5][2] = { { 3 * E, E }, { E, E }, { F, E }, { E, F }, { V, E } };
+    for (int i = 0; i < 5; ++i) {
+        const int C = dims[i][1] / VE, need = (C + G2P_SEGC - 1) / G2P_SEGC;
+        if (need > 8) return "a matrix row exceeds 8 segments";
+        const int nseg = need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : 8));
+        if ((long)((dims[i][0] + nwg - 1) / nwg) * nseg > G2_STEP_MAXUNITS)
+            return "a matrix exceeds the units per work-group";
+    }
+    return 0;
+}
+
+/* Attention unit u of a layer: work-group, half and round it runs in
+ * (unit u -> work-group u % nwg, half (u / nwg) % 2, round u / (2 nwg)). */
+G2P_FN int g2p_attn_unit(int wg, int nwg, int round, int half) { return wg + nwg * (2 * round + half); }
+
+#endif /* G2_STEP_PLAN_H */

@@ -1,0 +1,203 @@
+/*
+ * step_addr.cpp -- CPU address check of the persistent decode-step kernel
+ * (gpt2-opencl-1.1_amd/csrc/g2_step.hip).  Test infrastructure, compiled
+ * with g++ by tests/test_step_addresses.py.
+ *
+ * For one model shape, weight element size and position, every work-group
+ * and thread of the launch (G2_STEP_THREADS threads, nwg work-groups) is
+ * walked through the kernel's phases, and every global address it would
+ * load or store is checked against the allocation it points into:
+ *   weights   qkv [3E][K], proj [E][E], fc [F][E], fc2 [E][F], lm_head [V][E]
+ *             (16-byte chunks from g2_step_plan.h, the kernel's own code),
+ *             biases and LayerNorm parameters, the embedding rows;
+ *   KV cache  the attention units' 16-byte loads of K [E][S] and V [S][E]
+ *             and the current position's K/V stores;
+ *   exchange  every tagged word read or written: q/k/v, chunk partials,
+ *             merged O, X1, H, X2, the argmax words, the arrival words;
+ *   LDS       the dot products' x reads and the partial-sum slots.
+ * Prints one line of counts; exits 1 if any access is out of bounds, 3 if
+ * the host refuses the shape (g2p_step_refusal: it then never launches it).
+ *
+ * Usage: step_addr L E NH V F VE POS NWG [plant]
+ *   VE: elements per 16-byte chunk (8 fp16, 4 fp32); plant=1 replaces the
+ *   clamped chunk of g2p_unit_chunk by the unclamped one (a planted mistake
+ *   the check must catch).
+ */
+#include <cstdio>
+#include <cstdlib>
+
+#include "g2_step_plan.h"
+
+static long n_checked, n_bad;
+static const char *first_bad;
+
+static void chk(const char *what, long lo, long hi_excl, long lim)
+{
+    ++n_checked;
+    if (lo < 0 || hi_excl > lim) {
+        if (!n_bad) {
+            first_bad = what;
+            fprintf(stderr, "out of bounds: %s [%ld, %ld) of %ld\n", what, lo, hi_excl, lim);
+        }
+        ++n_bad;
+    }
+}
+
+static int plant = 0;
+
+/* load_set<UM>(batch) of a work-group: every lane's 16-byte chunk loads */
+static void load_set(const char *what, const g2p_rows &p, int UM, int batch, long N, long VE)
+{
+    const long chunks = N * p.C; /* 16-byte chunks in the matrix */
+    for (int tid = 0; tid < G2_STEP_THREADS; ++tid) {
+        const int wave = tid >> 6, lane = tid & 63;
+        for (int j = 0; j < UM; ++j) {
+            const g2p_unit un = g2p_unit_at(&p, UM, batch, wave, j);
+            for (int i = 0; i < 4; ++i) {
+                long c = g2p_unit_chunk(&un, lane, i);
+                if (plant && un.uv) c = un.base + un.c0 + lane + 64 * i;
+                chk(what, c, c + 1, chunks);
+            }
+        }
+    }
+    (void)VE;
+}
+
+/* dot_set's LDS reads of x (K floats written) and its partial-sum writes */
+static void dot_set(const char *what, const g2p_rows &p, int UM, int batch, int VE, long K)
+{
+    for (int tid = 0; tid < G2_STEP_THREADS; ++tid) {
+        const int wave = tid >> 6, lane = tid & 63;
+        if (batch * G2P_NW * UM + wave >= p.nunits) continue;
+        for (int i = 0; i < 4; ++i) {
+            const int cc = g2p_dot_chunk(&p, wave, lane, i);
+            if (cc >= 0) {
+                chk(what, (long)cc * VE, (long)cc * VE + VE, K);
+                chk("LDS x", (long)cc * VE, (long)cc * VE + VE, G2_STEP_MAXF);
+            }
+        }
+        for (int j = 0; j < UM; ++j) {
+            const int u = batch * G2P_NW * UM + wave + G2P_NW * j;
+            if (u < p.nunits) chk("LDS partial sums", u, u + 1, G2_STEP_MAXUNITS);
+        }
+    }
+}
+
+/* a whole matrix share as matvec<UM> runs it (batch 0 preloaded, later
+ * batches loaded on demand), its bias load and the row sums */
+static void matrix(const char *what, const void *bias_tag, int N, int K, int VE, int UM, long wg, long nwg)
+{
+    const g2p_rows p = g2p_rows_plan(N, K, VE, wg, nwg);
+    chk("rows per work-group", 0, p.nrows, G2_STEP_THREADS);
+    for (int b = 0; b == 0 || b * G2P_NW * UM < p.nunits; ++b) {
+        load_set(what, p, UM, b, N, VE);
+        dot_set(what, p, UM, b, VE, K);
+    }
+    if (bias_tag)
+        for (int tid = 0; tid < G2_STEP_THREADS; ++tid) {
+            const int r = g2p_min(p.r0 + tid, N - 1);
+            chk("bias", r, r + 1, N);
+        }
+    for (int t = 0; t < p.nrows; ++t)
+        for (int s = 0; s < p.nseg; ++s) chk("LDS partial sums", (long)t * p.nseg + s, (long)t * p.nseg + s + 1,
+                                             G2_STEP_MAXUNITS);
+}
+
+int main(int argc, char **argv)
+{
+    if (argc < 9) return 2;
+    const int L = atoi(argv[1]), E = atoi(argv[2]), NH = atoi(argv[3]), V = atoi(argv[4]), F = atoi(argv[5]);
+    const int VE = atoi(argv[6]), pos = atoi(argv[7]), nwg = atoi(argv[8]);
+    plant = argc > 9 ? atoi(argv[9]) : 0;
+    const int S = G2_KV_MAX_SEQ, NT = G2_STEP_THREADS;
+    const long xlayer = G2X_LAYER_WORDS(E, NH, F);
+    const long xtotal = G2X_TOTAL_WORDS(L, E, NH, F, nwg);
+    const int T = pos + 1, nch = (T + 63) / 64;
+    const int NPE = (G2_STEP_MAXE + NT - 1) / NT;
+    if (nch > G2_STEP_MAXCH) {
+        fprintf(stderr, "position beyond the cache\n");
+        return 1;
+    }
+    /* the host never launches the kernel on a shape it refuses */
+    const char *why = g2p_step_refusal(E, NH, F, V, VE, nwg);
+    if (why) {
+        printf("refused: %s\n", why);
+        return 3;
+    }
+    for (long wg = 0; wg < nwg; ++wg) {
+        /* embedding of the token at pos, LayerNorm parameters */
+        for (int tid = 0; tid < NT; ++tid) {
+            for (int d = tid; d < E; d += NT) {
+                chk("wte row", (long)(V - 1) * E + d, (long)(V - 1) * E + d + 1, (long)V * E);
+                chk("wpe row", (long)pos * E + d, (long)pos * E + d + 1, (long)S * E);
+            }
+            for (int k = 0; k < NPE; ++k) {
+                const int i = g2p_min(tid + NT * k, E - 1);
+                chk("LayerNorm parameters", i, i + 1, E);
+            }
+            chk("arrival word", G2X_ARRIVE(L, xlayer, nwg) + wg, G2X_ARRIVE(L, xlayer, nwg) + wg + 1, xtotal);
+        }
+        for (int l = 0; l < L; ++l) {
+            const long R = G2X_HEAD + (long)l * xlayer;
+            /* QKV: rows, K/V cache stores at pos, q/k/v words */
+            matrix("qkv weights", "b", 3 * E, E, VE, 4, wg, nwg);
+            const g2p_rows pq = g2p_rows_plan(3 * E, E, VE, wg, nwg);
+            for (int t = 0; t < pq.nrows; ++t) {
+                const int r = pq.r0 + t;
+                chk("qkv word", R + r, R + r + 1, R + G2X_ATT(E));
+                if (r >= 2 * E) chk("V cache store", (long)pos * E + (r - 2 * E), (long)pos * E + (r - 2 * E) + 1, (long)S * E);
+                else if (r >= E) chk("K cache store", (long)(r - E) * S + pos, (long)(r - E) * S + pos + 1, (long)E * S);
+            }
+            if (l > 0)
+                for (int w = 0; w < E; ++w) chk("X2 word", R - xlayer + G2X_X2(E, NH, F) + w, R - xlayer + G2X_X2(E, NH, F) + w + 1, R);
+            /* ATTN units */
+            const int nunits = NH * nch, rounds = (nunits + 2 * nwg - 1) / (2 * nwg);
+            for (int rd = 0; rd < rounds; ++rd)
+                for (int tid = 0; tid < NT; ++tid) {
+                    const int hf = tid >> 8, t = tid & 255;
+                    const int u = g2p_attn_unit((int)wg, nwg, rd, hf);
+                    const int on = u < nunits;
+                    const int h = on ? u / nch : 0, ch = on ? u % nch : 0;
+                    long koff, voff[4];
+                    g2p_attn_offsets(t, on, h, ch, E, S, &koff, voff);
+                    for (int d = 0; d < 4; ++d) chk("K cache load", koff + (long)d * S, koff + (long)d * S + 4, (long)E * S);
+                    for (int e = 0; e < 4; ++e) chk("V cache load", voff[e], voff[e] + 4, (long)S * E);
+                    if (on && t < 192) {
+                        const int part = t >> 6, d = t & 63;
+                        const long w = (part == 0 ? 0 : (part == 1 ? E : 2 * E)) + h * 64 + d;
+                        chk("q/k/v word of a unit", R + w, R + w + 1, R + G2X_ATT(E));
+                    }
+                    if (on && t < 66) {
+                        const long pw = R + G2X_ATT(E) + ((long)h * G2_STEP_MAXCH + ch) * 66 + t;
+                        chk("chunk partial word", pw, pw + 1, R + G2X_O(E, NH));
+                    }
+                }
+            /* MERGE of head h by work-group h */
+            for (int h = (int)wg; h < NH; h += nwg) {
+                const long hp = R + G2X_ATT(E) + (long)h * G2_STEP_MAXCH * 66;
+                chk("merge partial reads", hp, hp + (long)nch * 66, R + G2X_O(E, NH));
+                chk("O words", R + G2X_O(E, NH) + h * 64, R + G2X_O(E, NH) + h * 64 + 64, R + G2X_X1(E, NH));
+            }
+            /* PROJ, FC, FC2 */
+            matrix("proj weights", "b", E, E, VE, 1, wg, nwg);
+            const g2p_rows pp = g2p_rows_plan(E, E, VE, wg, nwg);
+            chk("X1 words", R + G2X_X1(E, NH) + pp.r0, R + G2X_X1(E, NH) + pp.r0 + pp.nrows, R + G2X_H(E, NH));
+            matrix("fc weights", "b", F, E, VE, 4, wg, nwg);
+            const g2p_rows pf = g2p_rows_plan(F, E, VE, wg, nwg);
+            chk("H words", R + G2X_H(E, NH) + pf.r0, R + G2X_H(E, NH) + pf.r0 + pf.nrows, R + G2X_X2(E, NH, F));
+            matrix("fc2 weights", "b", E, F, VE, 4, wg, nwg);
+            const g2p_rows p2 = g2p_rows_plan(E, F, VE, wg, nwg);
+            chk("X2 words", R + G2X_X2(E, NH, F) + p2.r0, R + G2X_X2(E, NH, F) + p2.r0 + p2.nrows, R + xlayer);
+            chk("fetched vector in LDS", 0, F, G2_STEP_MAXF);
+        }
+        /* LM head rows, logits, argmax words */
+        matrix("lm_head weights", nullptr, V, E, VE, 4, wg, nwg);
+        const g2p_rows pl = g2p_rows_plan(V, E, VE, wg, nwg);
+        chk("logits", pl.r0, pl.r0 + pl.nrows, V);
+        const long AM = G2X_HEAD + (long)L * xlayer;
+        chk("argmax words", AM + 2 * wg, AM + 2 * wg + 2, G2X_ARRIVE(L, xlayer, nwg));
+    }
+    printf("checked %ld accesses, %ld out of bounds%s%s\n", n_checked, n_bad, n_bad ? "; first: " : "",
+           n_bad ? first_bad : "");
+    return n_bad ? 1 : 0;
+}
