@@ -238,8 +238,9 @@ typedef struct {
     float scale;
     /* g2k_step_f16/f32 only: 0 cooperative launch; 1 plain launch, so the
      * kernel checks that all its work-groups are resident before its first
-     * lasting write; 2 as 1 with work-group 1 withholding its arrival (a test
-     * of the not-resident path) */
+     * lasting write; tests of that check: 2 as 1 with work-group 1
+     * withholding its arrival, 3 with it arriving 0.5 ms late (within the
+     * limit), 4 with it arriving 2 ms late (after the others gave up) */
     int plain;
 } g2_step_args;
 
@@ -251,6 +252,7 @@ typedef struct {
 #define G2_STEP_MAXUNITS 512 /* (row, segment) units per work-group and phase */
 #define G2_STEP_MAXCH 16    /* 64-position key chunks per head */
 #define G2X_HEAD 64         /* words before the first layer region (word 0: abort) */
+#define G2X_DECISION 1      /* header word: a plain launch's residency verdict */
 /* Word offsets inside one layer region (E = n_embd, NH heads, F = ffn):
  * QKV outputs [3E], attention chunk partials [NH][G2_STEP_MAXCH][66],
  * merged attention O [E], X1 = x + proj [E], H = gelu(fc) [F],

@@ -57,8 +57,8 @@ struct g2_model {
     size_t xbuf_bytes;
     int step_wgs;  /* grid of the step kernel, 0 if this model cannot use it */
     int step_on;   /* decode steps run the step kernel */
-    int plain;     /* the all-to-all form's launches are plain, not cooperative (2: test
-                      hook, work-group 1 withholds its arrival) */
+    int plain;     /* launches are plain, not cooperative (2-4: test modes of the
+                      residency check, see g2_step_args.plain) */
     int step_ran;  /* a step kernel ran since the last error check */
     const char *step_why; /* why the step kernel cannot run this model */
     unsigned long long *trace; /* phase timestamps, when G2_STEP_TRACE names a file */
@@ -198,7 +198,10 @@ static int step_setup(g2_model *m)
      * back-to-back steps (1.4% of an XL token); the all-to-all kernel checks
      * residency itself, so it is launched plain unless G2_STEP_COOP=1. */
     const char *envc = getenv("G2_STEP_COOP"), *envw = getenv("G2_STEP_TEST_WITHHOLD");
-    m->plain = envc && envc[0] == '1' ? 0 : (envw && envw[0] == '1' ? 2 : 1);
+    /* G2_STEP_TEST_WITHHOLD (tests of the residency check): 1 work-group 1
+     * never arrives, 2 arrives 0.5 ms late, 3 arrives 2 ms late */
+    const int tw = envw && envw[0] >= '1' && envw[0] <= '3' ? envw[0] - '0' : 0;
+    m->plain = envc && envc[0] == '1' ? 0 : (tw ? 1 + tw : 1);
     m->xbuf_bytes = (size_t)G2X_TOTAL_WORDS(L, c->n_embd, c->n_head, c->ffn_dim, nwg) * 8;
     if (!rc) rc = dev_alloc(m, (void **)&m->xbuf, m->xbuf_bytes, 0);
     if (!rc) rc = g2i_hip(hipMemsetAsync(m->xbuf, 0, m->xbuf_bytes, g2i_stream()), "exchange clear");

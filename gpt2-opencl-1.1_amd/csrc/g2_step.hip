@@ -645,17 +645,22 @@ __device__ __forceinline__ int fresh_tid()
 /* Plain launches (not cooperative): before its first lasting write (the
  * K/V cache entries of layer 0), a work-group checks that every work-group
  * of the grid has posted its arrival word, i.e. is resident at the same
- * time, and that none has given up.  A work-group that waits longer than
- * RESIDENT_LIMIT gives up: it sets G2_ERR_STEP_NOT_RESIDENT, raises the
- * abort word and exits, and so does every work-group that sees the abort
- * word after its own arrivals were complete (a work-group that only got a
- * CU when another exited finds all arrival words posted, but the abort word
- * raised before that exit).  No work-group of such a launch writes the
- * caches, the logits or the state.  Returns false for such a launch; all
- * threads take part and get the same answer. */
+ * time.  The launch's verdict is one word decided once, by compare-and-swap
+ * on the decision word (its high half the launch's tag): GO by the first
+ * work-group that saw every arrival, ABORT by the first whose wait ran out
+ * (RESIDENT_LIMIT).  Every work-group follows the stored verdict, so either
+ * all of them go on or none writes anything.  GO is safe for a work-group
+ * whose own wait ran out: a GO proves every work-group arrived, and none
+ * leaves before the verdict, so all were resident together.  On ABORT the
+ * work-groups set G2_ERR_STEP_NOT_RESIDENT, raise the abort word and exit;
+ * a work-group that only got a CU when another exited finds the verdict
+ * already stored.  Returns false for an aborted launch; all threads take
+ * part and get the same answer. */
 constexpr unsigned long long RESIDENT_LIMIT = 100000ull; /* 1 ms */
+constexpr unsigned VERDICT_GO = 1u, VERDICT_ABORT = 2u;
 
-__device__ __forceinline__ bool grid_resident(int tid, const ctx &c, const u64 *arr, int nwg, lds_flag *flag)
+__device__ __forceinline__ bool grid_resident(int tid, const ctx &c, const u64 *arr, u64 *decision, int nwg,
+                                              lds_flag *flag)
 {
     if (tid == 0) *flag = 0;
     __syncthreads();
@@ -670,14 +675,20 @@ __device__ __forceinline__ bool grid_resident(int tid, const ctx &c, const u64 *
     }
     __syncthreads();
     if (tid == 0) {
-        if (!*flag && ll_tag(ll_get(c.abort_w)) == c.tag) *flag = 1;
-        if (*flag) {
+        const unsigned mine = *flag ? VERDICT_ABORT : VERDICT_GO;
+        u64 cur = ll_get(decision);
+        while (ll_tag(cur) != c.tag) {
+            const u64 want = ((u64)c.tag << 32) | mine;
+            const u64 prev = atomicCAS((unsigned long long *)decision, cur, want);
+            cur = prev == cur ? want : prev;
+        }
+        const bool go = (unsigned)cur == VERDICT_GO;
+        if (!go) {
             atomicOr(c.state + G2S_ERR, G2_ERR_STEP_NOT_RESIDENT);
             ll_put(c.abort_w, 0.f, c.tag);
-            /* a read of the same word after the store: the abort is visible
-             * before this work-group exits and frees its CU */
-            if (ll_tag(ll_get(c.abort_w)) != c.tag) *flag = 2;
+            *c.dead = 1;
         }
+        *flag = go ? 0 : 1;
     }
     __syncthreads();
     return *flag == 0;
@@ -729,6 +740,7 @@ __device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, con
     /* ---- greedy pick (g2k_argmax_merge with advance) */
     __syncthreads();
     fetch<2>(tid, c, AM, 2 * nwg, nwg, xin, flag);
+    const u64 abort_seen = tid == 0 ? ll_get(c.abort_w) : 0; /* issued ahead of the merge */
     bv = -INFINITY;
     bi = 0x7fffffff;
     for (int b = tid; b < nwg; b += NT) {
@@ -737,7 +749,9 @@ __device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, con
         if (am_better2(v, i, bv, bi)) { bv = v; bi = i; }
     }
     blk_argmax(tid, bv, bi, amv, ami);
-    if (tid == 0) {
+    /* a launch that gave up a wait (its words may be stale) leaves the state
+     * as it was; the host reports the failed step */
+    if (tid == 0 && !*c.dead && ll_tag(abort_seen) != c.tag) {
         const int tk = (ami[0] >= 0 && ami[0] < V) ? ami[0] : 0;
         const int ng = clampi(ngen, 0, G2S_WORDS - G2S_IDS - 1);
         a.state[G2S_IDS + ng] = tk;
@@ -792,6 +806,13 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         const int tid = fresh_tid();
         if (tid == 0) {
             dead = 0;
+            /* test modes of a.plain (work-group 1 only): 2 never posts its
+             * arrival, 3 posts it 0.5 ms late (within the limit), 4 posts it
+             * 2 ms late (after the others gave up) */
+            if (a.plain && wg == 1 && a.plain >= 3) {
+                const u64 t0 = wall_clock64(), d = a.plain == 3 ? 50000ull : 200000ull;
+                while (wall_clock64() - t0 < d) __builtin_amdgcn_s_sleep(8);
+            }
             if (a.plain && !(a.plain == 2 && wg == 1))
                 ll_put(a.xbuf + G2X_ARRIVE(a.L, a.xlayer, nwg) + wg, 0.f, c.tag);
         }
@@ -824,7 +845,8 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             matvec<WT, UMAX>(tid, wa, p, xin, part);
             TRACE(12);
             if (l == 0 && a.plain &&
-                !grid_resident(tid, c, a.xbuf + G2X_ARRIVE(a.L, a.xlayer, nwg), nwg, (lds_flag *)&flag))
+                !grid_resident(tid, c, a.xbuf + G2X_ARRIVE(a.L, a.xlayer, nwg), a.xbuf + G2X_DECISION, nwg,
+                               (lds_flag *)&flag))
                 return;
             if (tid < p.nrows) {
                 const int r = p.r0 + tid;

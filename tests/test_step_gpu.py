@@ -119,20 +119,25 @@ def test_step_decode_run_matches_generate(g2):
     m.free()
 
 
-def test_step_plain_launch_not_resident_resumes(g2, monkeypatch, capfd):
-    """The step kernel is launched plain (not cooperatively) and
-    checks that all its work-groups are resident before its first lasting
-    write.  Forced failure from the host (G2_STEP_TEST_WITHHOLD=1:
-    work-group 1 withholds its arrival word, so every work-group gives up
-    after 1 ms and writes nothing): the host resumes the run with
-    cooperative launches, and generate, a second generate and a single
-    decode give ids and logits bit-identical to cooperative launches only
-    (G2_STEP_COOP=1) and to plain launches."""
+@pytest.mark.parametrize("late", ["never", "0.5ms", "2ms"])
+def test_step_plain_launch_not_resident_resumes(g2, monkeypatch, capfd, late):
+    """The step kernel is launched plain (not cooperatively) and all its
+    work-groups agree on one verdict, by compare-and-swap on a decision
+    word, before their first lasting write: GO once one has seen every
+    arrival word, ABORT once one has waited 1 ms.  Forced from the host
+    (G2_STEP_TEST_WITHHOLD): work-group 1 never posts its arrival (every
+    launch aborts), posts it 0.5 ms late (within the limit: no abort), or
+    2 ms late (the others give up first; work-group 1 then finds ABORT
+    stored).  After an abort nothing was written: the host resumes the run
+    with cooperative launches.  In every mode generate, a second generate
+    and a single decode give ids and logits bit-identical to cooperative
+    launches only (G2_STEP_COOP=1) and to plain launches."""
     cfg = g2.make_config(3, 256, 4, vocab_size=1000)
     w = g2.synth_weights(cfg, SEED, f16_round=True)
     prompt = random_prompt(120, cfg.vocab_size, 31)
+    mode = {"never": "1", "0.5ms": "2", "2ms": "3"}[late]
     outs = []
-    for env in ({"G2_STEP_COOP": "1"}, {"G2_STEP_TEST_WITHHOLD": "1"}, {}):
+    for env in ({"G2_STEP_COOP": "1"}, {"G2_STEP_TEST_WITHHOLD": mode}, {}):
         for k in ("G2_STEP_COOP", "G2_STEP_TEST_WITHHOLD"):
             monkeypatch.delenv(k, raising=False)
         for k, v in env.items():
@@ -153,7 +158,8 @@ def test_step_plain_launch_not_resident_resumes(g2, monkeypatch, capfd):
             m.free()
         err = capfd.readouterr().err
         resumed = err.count("resuming with cooperative launches")
-        assert resumed == (2 if "G2_STEP_TEST_WITHHOLD" in env else 0), err
+        expect = 2 if ("G2_STEP_TEST_WITHHOLD" in env and late != "0.5ms") else 0
+        assert resumed == expect, err
         outs.append(run)
     assert len(outs[0][0]) == 30
     for o in outs[1:]:
