@@ -22,17 +22,22 @@ launches, bytes per token from the formula
 parameters, embedding rows, K/V writes), against MI355X's 8 TB/s HBM peak.
 
 cpu_baseline: the CPU oracle (a C restatement of the reference kernels with
-their accumulation order) on the host's cores, decoding a bounded sample of
-the same workload -- a few forwards at positions 512.. over the KV cache the
-GPU prefill produced.
+their accumulation order) on the host's cores, decoding a fixed sample of
+the same workload -- 100 greedy forwards at positions P+1.. over the KV
+cache the GPU prefill produced -- with the CPU model and thread placement.
 
 traffic: HBM bytes per launch of that kernel from rocprofv3 counter runs
 (FETCH_SIZE and WRITE_SIZE, one run each), each scaled by what the same
 counter reads for a plain device copy of known size (`--copy-probe`); the
-figures are read from profiles/g2k_step_f16_xl_traffic.json when it exists
-and matches this workload, else traffic is null.
+figures are read from profiles/<kernel>_<config>_traffic.json when it
+exists and matches this workload, else traffic is null.
+
+Other configurations of the workload list (each with its own prompt and
+decode length: small fp32 64+255, medium fp32 128+511, large fp32 and
+fp16-weight 256+511) run with --config; the headline is XL.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+                       [--config small|medium|large|large16|xl]
        python bench.py --copy-probe   (device copies of 1 GiB, for counter calibration)
 """
 import argparse
@@ -48,8 +53,13 @@ sys.path.insert(0, os.path.join(ROOT, "gpt2-opencl-1.1_amd"))
 
 METRIC = "batch-1 decode tok/s + % HBM roofline (GPT-2 XL fp16); prefill tok/s"
 SEED = 0x67707432
-PROMPT_LEN = 512
 HBM_PEAK_GBS = 8000.0
+# name: (preset, fp16 weights, prompt tokens); decode forwards fill the
+# context to 1024 positions, except GPT-2 small (255 forwards)
+CONFIGS = {"small": ("small", False, 64, 255), "medium": ("medium", False, 128, 511),
+           "large": ("large", False, 256, 511), "large16": ("large", True, 256, 511),
+           "xl": ("xl", True, 512, 511)}
+CPU_SAMPLE_FORWARDS = 100
 
 
 def step_bytes(cfg, w_bytes, kv_bytes, positions):
@@ -65,7 +75,10 @@ def log(msg):
 
 
 COPY_BYTES = 1 << 30
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "g2k_step_f16_xl_traffic.json")
+
+
+def traffic_file(kernel, config):
+    return os.path.join(ROOT, "profiles", f"{kernel}_{config}_traffic.json")
 
 
 def copy_probe():
@@ -81,11 +94,11 @@ def copy_probe():
     print(json.dumps({"copy_bytes": COPY_BYTES, "copies": 5}), flush=True)
 
 
-def measured_traffic(kernel, workload):
+def measured_traffic(kernel, config, workload):
     """HBM bytes per launch from the committed counter summary, if it was
     taken on this kernel and workload."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(traffic_file(kernel, config)) as f:
             t = json.load(f)
     except (OSError, ValueError):
         return None
@@ -94,37 +107,58 @@ def measured_traffic(kernel, workload):
     return t.get("bytes_per_launch")
 
 
-def cpu_baseline(g2, m, cfg, token, min_seconds=10.0, max_steps=400):
-    """Time the oracle on a bounded sample of the same workload: decode
-    forwards at positions 513.. over the GPU-prefilled KV cache, as many as
-    fit in min_seconds of CPU work (at most max_steps, and never past the
-    last cache position)."""
+def cpu_description():
+    """CPU model, logical CPUs this process may run on, and their list."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        allowed = sorted(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = list(range(os.cpu_count() or 1))
+    return model, allowed
+
+
+def cpu_baseline(g2, m, cfg, f16, P, token, n_forwards=CPU_SAMPLE_FORWARDS):
+    """Time the oracle on a fixed sample of the same workload: n_forwards
+    greedy decode forwards at positions P+1.. over the GPU-prefilled KV
+    cache (the reference's timing method, main.c:2106-2170: wall clock
+    around the decode loop, sampling included, no printing)."""
     sys.path.insert(0, ROOT)
     from oracle import oracle
     t0 = time.perf_counter()
-    w = g2.synth_weights(cfg, SEED, f16_round=True)
+    w = g2.synth_weights(cfg, SEED, f16_round=f16)
     om = oracle.Model(cfg, w, kslice=4)
     del w
     for l in range(cfg.n_layer):
         k, v = m.read_kv(l)
         om.set_kv(l, k, v)
     log(f"cpu oracle ready in {time.perf_counter() - t0:.1f}s")
-    om.decode(token, PROMPT_LEN)  # untimed first forward (page-in)
+    om.decode(token, P)  # untimed first forward (page-in)
     tok = om.greedy([token], forbid_eos=True)
-    max_steps = min(max_steps, 1022 - PROMPT_LEN)
+    n = min(n_forwards, 1022 - P)
     t0 = time.perf_counter()
-    n_steps = 0
-    while n_steps < max_steps and (n_steps == 0 or time.perf_counter() - t0 < min_seconds):
-        om.decode(tok, PROMPT_LEN + 1 + n_steps)
+    for i in range(n):
+        om.decode(tok, P + 1 + i)
         tok = om.greedy([tok], forbid_eos=True)
-        n_steps += 1
     dt = time.perf_counter() - t0
-    cores = oracle.num_threads()
+    threads = oracle.num_threads()
     om.close()
-    return {"value": round(n_steps / dt, 3), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{n_steps} greedy decode forwards of GPT-2 XL (fp16-rounded weights held as fp32) at "
-                      f"positions {PROMPT_LEN + 1}..{PROMPT_LEN + n_steps} over the GPU-prefilled KV cache, "
-                      f"{cores} OpenMP threads, {dt:.2f} s"}
+    model, allowed = cpu_description()
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "cpu": model, "logical_cpus_allowed": len(allowed),
+            "pinning": (f"OpenMP threads {threads} (OMP_NUM_THREADS={os.environ.get('OMP_NUM_THREADS', 'unset')}), "
+                        f"no explicit binding; process affinity CPUs {allowed[0]}-{allowed[-1]}"
+                        if allowed else "none"),
+            "sample": f"{n} greedy decode forwards of GPT-2 {cfg.n_layer}-layer E{cfg.n_embd} "
+                      f"({'fp16-rounded weights held as fp32' if f16 else 'fp32 weights'}) at positions "
+                      f"{P + 1}..{P + n} over the GPU-prefilled KV cache, {threads} OpenMP threads, {dt:.2f} s"}
 
 
 def main():
@@ -133,8 +167,9 @@ def main():
     ap.add_argument("--steps", type=int, default=3)
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--config", default="xl", choices=["small", "medium", "large", "xl"])
-    ap.add_argument("--fp32", action="store_true", help="fp32 weights instead of fp16")
+    ap.add_argument("--config", default="xl", choices=list(CONFIGS),
+                    help="xl: XL fp16 512+511 (default, the headline); small/medium/large: fp32 weights; "
+                         "large16: large with fp16 weights")
     ap.add_argument("--copy-probe", action="store_true", help="device copies of 1 GiB for counter calibration")
     args = ap.parse_args()
     if args.copy_probe:
@@ -149,17 +184,24 @@ def main():
 
     import g2hip as g2
     g2.init(0)
+    try:
+        run(args, g2)
+    finally:
+        # release the model and the library before the interpreter exits, so
+        # no HIP stream, module or buffer is left to the runtime's exit path
+        g2.shutdown()
+
+
+def run(args, g2):
     name, cus = g2.device_name()
-    cfg = g2.preset(args.config)
-    f16 = not args.fp32
+    preset, f16, P, n_dec = CONFIGS[args.config]
+    cfg = g2.preset(preset)
     wdtype = g2.F16 if f16 else g2.F32
     t0 = time.perf_counter()
     m = g2.Model.synth(cfg, SEED, wdtype, g2.PATH_FUSED)
     log(f"{args.config} model on {name} ({cus} CUs) in {time.perf_counter() - t0:.1f}s, "
         f"{m.weight_bytes() / 2**20:.0f} MiB of weights")
-    prompt = np.random.default_rng(SEED).integers(0, cfg.vocab_size, PROMPT_LEN).astype(np.int32)
-    P = PROMPT_LEN
-    n_dec = 1023 - P
+    prompt = np.random.default_rng(SEED).integers(0, cfg.vocab_size, P).astype(np.int32)
 
     # prefill: prompt -> first token (device-selected), timed by HIP events
     ids, _ = m.generate(prompt, 2)  # warm-up, builds the decode graph
@@ -193,7 +235,7 @@ def main():
 
     kind = m.step_kind()
     kname = ("g2k_step_f16" if f16 else "g2k_step_f32") if kind else ""
-    workload = (f"GPT-2 {args.config.upper()} {'fp16' if f16 else 'fp32'}-weight batch-1 greedy decode: {P}-token "
+    workload = (f"GPT-2 {preset.upper()} {'fp16' if f16 else 'fp32'}-weight batch-1 greedy decode: {P}-token "
                 f"random prompt, {n_dec} decode forwards (positions {P}..{P + n_dec - 1})")
     result = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
@@ -209,13 +251,13 @@ def main():
         "decode_ms_per_token": round(step_ms_events / n_dec, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(kname, workload) if kname else None,
+                     "traffic": measured_traffic(kname, args.config, workload) if kname else None,
                      "kernel": (f"{kname} (one launch per decode token)" if kname
                                 else "decode step (per-operator kernels)"),
                      "bytes_per_launch": round(bytes_step / n_dec)},
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(g2, m, cfg, first_tok)
+        result["cpu_baseline"] = cpu_baseline(g2, m, cfg, f16, P, first_tok)
     print(json.dumps(result), flush=True)
     m.free()
 

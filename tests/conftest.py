@@ -24,3 +24,7 @@ def g2():
     print(f"\n[g2] device {name} with {cus} CUs", flush=True)
     yield g2hip
     g2hip.sync()
+    import gc
+
+    gc.collect()  # models and buffers the tests dropped are freed while the library is up
+    g2hip.shutdown()
