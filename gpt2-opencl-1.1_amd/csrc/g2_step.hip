@@ -304,16 +304,19 @@ template <int NE, typename BAR = wg_bar>
 __device__ __forceinline__ void layernorm(int tid, const float *x, float *xin, const ln_params<NE> &lp,
                                           int E, float *red, BAR bar = BAR())
 {
+    /* every LDS read issued at once, at a clamped index (a read under a
+     * lane condition would be waited for one at a time); entries past E
+     * contribute exact zeros */
     const float x0 = x[0];
+    float xv[NE];
+#pragma unroll
+    for (int k = 0; k < NE; ++k) xv[k] = x[min(tid + NT * k, E - 1)];
     float s = 0.f, q = 0.f;
 #pragma unroll
     for (int k = 0; k < NE; ++k) {
-        const int i = tid + NT * k;
-        if (i < E) {
-            const float d = x[i] - x0;
-            s += d;
-            q = fmaf(d, d, q);
-        }
+        const float d = tid + NT * k < E ? xv[k] - x0 : 0.f;
+        s += d;
+        q = fmaf(d, d, q);
     }
     s = wsum(s);
     q = wsum(q);
@@ -335,7 +338,7 @@ __device__ __forceinline__ void layernorm(int tid, const float *x, float *xin, c
 #pragma unroll
     for (int k = 0; k < NE; ++k) {
         const int i = tid + NT * k;
-        if (i < E) xin[i] = fmaf((x[i] - mean) * inv, lp.g[k], lp.b[k]);
+        if (i < E) xin[i] = fmaf((xv[k] - mean) * inv, lp.g[k], lp.b[k]);
     }
     bar();
 }
