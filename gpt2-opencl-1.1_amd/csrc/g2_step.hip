@@ -354,11 +354,30 @@ struct plan : g2p_rows {
     const u32x4 *W;
 };
 
+/* The work-group's row shares of every matrix kind, computed once per
+ * launch (they do not change from layer to layer). */
+struct shares {
+    g2p_rows qkv, proj, fc, fc2, lm;
+};
+
 template <typename WT>
-__device__ __forceinline__ plan make_plan(const void *W, int N, int K)
+__device__ __forceinline__ shares make_shares(int E, int NH, int F, int V)
+{
+    constexpr int VE = chunk_t<WT>::V;
+    const long wg = blockIdx.x, nwg = gridDim.x;
+    shares s;
+    s.qkv = g2p_rows_plan(3 * E, E, VE, wg, nwg);
+    s.proj = g2p_proj_plan(E, VE, NH, wg, nwg); /* none for a head-merging work-group */
+    s.fc = g2p_rows_plan(F, E, VE, wg, nwg);
+    s.fc2 = g2p_rows_plan(E, F, VE, wg, nwg);
+    s.lm = g2p_rows_plan(V, E, VE, wg, nwg);
+    return s;
+}
+
+__device__ __forceinline__ plan make_plan(const void *W, const g2p_rows &r)
 {
     plan p;
-    static_cast<g2p_rows &>(p) = g2p_rows_plan(N, K, chunk_t<WT>::V, blockIdx.x, gridDim.x);
+    static_cast<g2p_rows &>(p) = r;
     p.W = (const u32x4 *)W;
     return p;
 }
@@ -373,7 +392,7 @@ __device__ __forceinline__ plan make_plan(const void *W, int N, int K)
 template <int UM>
 __device__ __forceinline__ void load_set(int tid, u32x4 (&w)[UM][4], const plan &p, int batch)
 {
-    const int wave = tid >> 6, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
 #pragma unroll
     for (int j = 0; j < UM; ++j) {
         const g2p_unit un = g2p_unit_at(&p, UM, batch, wave, j);
@@ -385,37 +404,57 @@ __device__ __forceinline__ void load_set(int tid, u32x4 (&w)[UM][4], const plan 
     }
 }
 
+/* acc + (16-byte chunk of weights) . x, as one fma chain element by element */
+template <typename WT>
+__device__ __forceinline__ float chunk_fma(const u32x4 &w, const float *x, float acc)
+{
+    if constexpr (sizeof(WT) == 4) {
+        acc = fmaf(__uint_as_float(w.x), x[0], acc);
+        acc = fmaf(__uint_as_float(w.y), x[1], acc);
+        acc = fmaf(__uint_as_float(w.z), x[2], acc);
+        return fmaf(__uint_as_float(w.w), x[3], acc);
+    } else {
+        const f16x8 h = __builtin_bit_cast(f16x8, w);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc = fmaf((float)h[e], x[e], acc);
+        return acc;
+    }
+}
+
 /* Dot products of a loaded batch with xin (LDS); unit sums to part[u].
  * Every unit of the wave covers the same chunks of x, so they are read from
- * LDS once. */
+ * LDS once (unconditionally, at a clamped index: a read under a lane
+ * condition would be waited for on its own).  The units' sums are
+ * independent fma chains, interleaved chunk by chunk. */
 template <typename WT, int UM>
 __device__ __forceinline__ void dot_set(int tid, const u32x4 (&w)[UM][4], const plan &p, int batch,
                                         const float *xin, float *part)
 {
     constexpr int VE = chunk_t<WT>::V;
-    const int wave = tid >> 6, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     if (batch * NW * UM + wave >= p.nunits) return; /* wave-uniform */
     float xv[4][VE];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int cc = g2p_dot_chunk(&p, wave, lane, i);
+        const int ci = cc < 0 ? 0 : cc;
 #pragma unroll
         for (int e = 0; e < VE; e += 4) {
-            f32x4 v = (f32x4){0.f, 0.f, 0.f, 0.f};
-            if (cc >= 0) v = *(const f32x4 *)(xin + cc * VE + e);
-            xv[i][e] = v.x; xv[i][e + 1] = v.y; xv[i][e + 2] = v.z; xv[i][e + 3] = v.w;
+            const f32x4 v = *(const f32x4 *)(xin + ci * VE + e);
+            xv[i][e] = cc < 0 ? 0.f : v.x;
+            xv[i][e + 1] = cc < 0 ? 0.f : v.y;
+            xv[i][e + 2] = cc < 0 ? 0.f : v.z;
+            xv[i][e + 3] = cc < 0 ? 0.f : v.w;
         }
     }
     if constexpr (UM == 4) {
         /* the four units' sums in one transposed reduction: unit j's total
          * lands in row (0, 2, 1, 3)[j] of the wave */
-        float acc[4];
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            acc[j] = 0.f;
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[j] += chunk_dot<WT>(w[j][i], xv[i]);
-        }
+            for (int j = 0; j < 4; ++j) acc[j] = chunk_fma<WT>(w[j][i], xv[i], acc[j]);
         const float v = wsum4(acc[0], acc[1], acc[2], acc[3]);
         if ((lane & 15) == 0) {
             const int j = (lane >> 4) == 0 ? 0 : ((lane >> 4) == 1 ? 2 : ((lane >> 4) == 2 ? 1 : 3));
@@ -427,9 +466,11 @@ __device__ __forceinline__ void dot_set(int tid, const u32x4 (&w)[UM][4], const 
         for (int j = 0; j < UM; ++j) {
             const int u = batch * NW * UM + wave + NW * j;
             if (u >= p.nunits) break; /* wave-uniform */
-            float acc = 0.f;
+            /* one chain per chunk, summed in chunk order */
+            float a4[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc += chunk_dot<WT>(w[j][i], xv[i]);
+            for (int i = 0; i < 4; ++i) a4[i] = chunk_fma<WT>(w[j][i], xv[i], 0.f);
+            float acc = ((a4[0] + a4[1]) + a4[2]) + a4[3];
             acc = wsum(acc);
             if (lane == 0) part[u] = acc;
         }
@@ -703,7 +744,7 @@ __device__ __forceinline__ bool grid_resident(int tid, const ctx &c, const u64 *
  * work-group 0 merges them (g2k_argmax_merge with advance) and advances the
  * device state.  All threads of the work-group take part. */
 template <typename WT>
-__device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, const u64 *xlast, u64 *AM,
+__device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, const shares &sh, const u64 *xlast, u64 *AM,
                                         u32x4 (&wa)[UMAX][4], bool preloaded, float *xres, float *xin,
                                         float *part, float *red, float *amv, int *ami, lds_flag *flag)
 {
@@ -716,7 +757,7 @@ __device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, con
     const unsigned seq = (unsigned)a.state[G2S_SEQ];
     constexpr int NPE = (G2_STEP_MAXE + NT - 1) / NT;
     const ln_params<NPE> lpf = ln_load<NPE>(tid, gl(a.lnf_w), gl(a.lnf_b), E);
-    const plan p = make_plan<WT>(a.lm_w, V, E);
+    const plan p = make_plan(a.lm_w, sh.lm);
     if (!preloaded) load_set<UMAX>(tid, wa, p, 0);
     fetch<NPE>(tid, c, xlast, E, nwg, xres, flag);
     TRACE(0);
@@ -804,6 +845,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     /* register sets: wa carries qkv -> fc -> fc2 -> next qkv (each loaded as
      * soon as the previous matrix is consumed), wp the proj rows */
     u32x4 wa[UMAX][4], wp[UPROJ][4];
+    const shares sh = make_shares<WT>(E, NH, F, V);
     {
         const G2_CONST g2_step_layer *LT0 = (const G2_CONST g2_step_layer *)a.layers;
         const int tid = fresh_tid();
@@ -819,8 +861,8 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             if (a.plain && !(a.plain == 2 && wg == 1))
                 ll_put(a.xbuf + G2X_ARRIVE(a.L, a.xlayer, nwg) + wg, 0.f, c.tag);
         }
-        load_set<UMAX>(tid, wa, make_plan<WT>(LT0->qkv_w, 3 * E, E), 0);
-        load_set<UPROJ>(tid, wp, make_plan<WT>(LT0->proj_w, E, E), 0);
+        load_set<UMAX>(tid, wa, make_plan(LT0->qkv_w, sh.qkv), 0);
+        if (wg >= NH) load_set<UPROJ>(tid, wp, make_plan(LT0->proj_w, sh.proj), 0);
         /* embedding of the token at its position (embed, math.cl:333-350) */
         for (int d = tid; d < E; d += NT)
             xres[d] = ldw((const WT *)a.wte, (size_t)tok * E + d) + ldw((const WT *)a.wpe, (size_t)pos * E + d);
@@ -836,7 +878,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         {
             const int tid = fresh_tid();
             TRACE(0);
-            const plan p = make_plan<WT>(y.qkv_w, 3 * E, E);
+            const plan p = make_plan(y.qkv_w, sh.qkv);
             const ln_params<NPE> lp = ln_load<NPE>(tid, gl(y.ln1_w), gl(y.ln1_b), E);
             const float bias = gl(y.qkv_b)[min(p.r0 + tid, 3 * E - 1)]; /* used by tid < nrows */
             if (l > 0) {
@@ -881,7 +923,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             TRACE(3);
             /* the fc rows stream from here on; a work-group that merges a head
              * issues them after its merge, so its merge waits behind nothing */
-            if (wg >= NH) load_set<UMAX>(tid, wa, make_plan<WT>(y.fc_w, F, E), 0);
+            if (wg >= NH) load_set<UMAX>(tid, wa, make_plan(y.fc_w, sh.fc), 0);
         }
 
         /* ---- MERGE: head h by work-group h (g2k_attn_merge) */
@@ -908,14 +950,18 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         }
         {
             const int tid = fresh_tid();
-            if (wg < NH) load_set<UMAX>(tid, wa, make_plan<WT>(y.fc_w, F, E), 0);
+            if (wg < NH) load_set<UMAX>(tid, wa, make_plan(y.fc_w, sh.fc), 0);
             TRACE(4);
         }
 
-        /* ---- PROJ: X1 = x + (O . Wp + b) */
-        {
+        /* ---- PROJ: X1 = x + (O . Wp + b), by the work-groups merging no head */
+        if (wg < NH) {
             const int tid = fresh_tid();
-            const plan p = make_plan<WT>(y.proj_w, E, E);
+            TRACE(5);
+            TRACE(6);
+        } else {
+            const int tid = fresh_tid();
+            const plan p = make_plan(y.proj_w, sh.proj);
             const float bias = gl(y.proj_b)[min(p.r0 + tid, E - 1)];
             fetch<NPE>(tid, c, R + G2X_O(E, NH), E, NH, xin, (lds_flag *)&flag);
             TRACE(5);
@@ -927,17 +973,17 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 ll_put(R + G2X_X1(E, NH) + r, v + xres[r], c.tag);
             }
             TRACE(6);
-            if (l + 1 < a.L) load_set<UPROJ>(tid, wp, make_plan<WT>(LT[l + 1].proj_w, E, E), 0);
+            if (l + 1 < a.L) load_set<UPROJ>(tid, wp, make_plan(LT[l + 1].proj_w, sh.proj), 0);
             __syncthreads();
         }
 
         /* ---- FC: H = gelu(LayerNorm(X1) . Wfc + b) */
         {
             const int tid = fresh_tid();
-            const plan p = make_plan<WT>(y.fc_w, F, E);
+            const plan p = make_plan(y.fc_w, sh.fc);
             const ln_params<NPE> lp = ln_load<NPE>(tid, gl(y.ln2_w), gl(y.ln2_b), E);
             const float bias = gl(y.fc_b)[min(p.r0 + tid, F - 1)];
-            fetch<NPE>(tid, c, R + G2X_X1(E, NH), E, nwg, xres, (lds_flag *)&flag);
+            fetch<NPE>(tid, c, R + G2X_X1(E, NH), E, nwg - NH, xres, (lds_flag *)&flag);
             TRACE(7);
             layernorm(tid, xres, xin, lp, E, red);
             TRACE(13);
@@ -950,14 +996,14 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 ll_put(R + G2X_H(E, NH) + r, gelu_f(v), c.tag);
             }
             TRACE(8);
-            load_set<UMAX>(tid, wa, make_plan<WT>(y.fc2_w, E, F), 0);
+            load_set<UMAX>(tid, wa, make_plan(y.fc2_w, sh.fc2), 0);
             __syncthreads();
         }
 
         /* ---- FC2: X2 = X1 + (H . Wfc2 + b) */
         {
             const int tid = fresh_tid();
-            const plan p = make_plan<WT>(y.fc2_w, E, F);
+            const plan p = make_plan(y.fc2_w, sh.fc2);
             const float bias = gl(y.fc2_b)[min(p.r0 + tid, E - 1)];
             fetch<PMAX>(tid, c, R + G2X_H(E, NH), F, nwg, xin, (lds_flag *)&flag);
             TRACE(9);
@@ -970,14 +1016,14 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 ll_put(R + G2X_X2(E, NH, F) + r, v + xres[r], c.tag);
             }
             TRACE(10);
-            if (l + 1 < a.L) load_set<UMAX>(tid, wa, make_plan<WT>(LT[l + 1].qkv_w, 3 * E, E), 0);
-            else load_set<UMAX>(tid, wa, make_plan<WT>(a.lm_w, V, E), 0);
+            if (l + 1 < a.L) load_set<UMAX>(tid, wa, make_plan(LT[l + 1].qkv_w, sh.qkv), 0);
+            else load_set<UMAX>(tid, wa, make_plan(a.lm_w, sh.lm), 0);
             __syncthreads();
         }
     }
 
     /* the first batch of lm_head rows was loaded by the last fc2 phase */
-    lm_pick<WT>(a, c, X + (size_t)(a.L - 1) * a.xlayer + G2X_X2(E, NH, F), X + (size_t)a.L * a.xlayer, wa, true,
+    lm_pick<WT>(a, c, sh, X + (size_t)(a.L - 1) * a.xlayer + G2X_X2(E, NH, F), X + (size_t)a.L * a.xlayer, wa, true,
                 xres, xin, part, red, amv, ami, (lds_flag *)&flag);
 }
 

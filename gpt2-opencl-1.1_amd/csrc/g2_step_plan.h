@@ -28,7 +28,7 @@ G2P_FN int g2p_min(int a, int b) { return a < b ? a : b; }
  * of the wave count) segments of SL <= 256 chunks; a (row, segment) unit is
  * one wave's job, 64 lanes x up to 4 chunks. */
 typedef struct {
-    int C, nseg, SL, r0, nrows, nunits;
+    int C, nseg, lseg, SL, r0, nrows, nunits; /* nseg = 1 << lseg */
 } g2p_rows;
 
 G2P_FN g2p_rows g2p_rows_plan(int N, int K, int VE, long wg, long nwg)
@@ -36,12 +36,29 @@ G2P_FN g2p_rows g2p_rows_plan(int N, int K, int VE, long wg, long nwg)
     g2p_rows p;
     p.C = K / VE;
     const int need = (p.C + G2P_SEGC - 1) / G2P_SEGC;
-    p.nseg = need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : 8));
+    p.lseg = need <= 1 ? 0 : (need <= 2 ? 1 : (need <= 4 ? 2 : 3));
+    p.nseg = 1 << p.lseg;
     p.SL = (p.C + p.nseg - 1) / p.nseg;
     p.r0 = (int)(((long)N * wg) / nwg);
     p.nrows = (int)(((long)N * (wg + 1)) / nwg) - p.r0;
     p.nunits = p.nrows * p.nseg;
     return p;
+}
+
+/* The proj rows go to the work-groups that merge no attention head (wg >=
+ * NH, of which the host admits at least one): a merging work-group issues
+ * its fc rows after its merge, and its O fetch then completes only behind
+ * them, so proj rows of its own would be the last X1 rows to arrive.  A
+ * merging work-group gets no rows (nrows = nunits = 0). */
+G2P_FN g2p_rows g2p_proj_plan(int E, int VE, int NH, long wg, long nwg)
+{
+    if (wg < NH) {
+        g2p_rows p = g2p_rows_plan(E, E, VE, 0, nwg - NH);
+        p.nrows = 0;
+        p.nunits = 0;
+        return p;
+    }
+    return g2p_rows_plan(E, E, VE, wg - NH, nwg - NH);
 }
 
 /* Unit j of a register set of UM units per wave, for the batch `batch` of
@@ -59,8 +76,8 @@ G2P_FN g2p_unit g2p_unit_at(const g2p_rows *p, int UM, int batch, int wave, int 
     g2p_unit a;
     const int u = batch * G2P_NW * UM + wave + G2P_NW * j;
     a.uv = u < p->nunits;
-    const int row = p->r0 + (a.uv ? u / p->nseg : 0);
-    a.c0 = (a.uv ? u % p->nseg : 0) * p->SL;
+    const int row = p->r0 + (a.uv ? u >> p->lseg : 0);
+    a.c0 = (a.uv ? u & (p->nseg - 1) : 0) * p->SL;
     a.clast = g2p_min(p->C, a.c0 + p->SL) - 1;
     a.base = (long)row * p->C;
     return a;
@@ -79,7 +96,7 @@ G2P_FN long g2p_unit_chunk(const g2p_unit *a, int lane, int i)
  * lies past the segment (its product is skipped). */
 G2P_FN int g2p_dot_chunk(const g2p_rows *p, int wave, int lane, int i)
 {
-    const int c0 = (wave % p->nseg) * p->SL;
+    const int c0 = (wave & (p->nseg - 1)) * p->SL;
     const int c1 = g2p_min(p->C, c0 + p->SL);
     const int cc = c0 + lane + 64 * i;
     return cc < c1 ? cc : -1;
@@ -114,12 +131,14 @@ G2P_FN const char *g2p_step_refusal(int E, int NH, int F, int V, int VE, int nwg
     if (nwg <= 0 || nwg > G2_STEP_THREADS) return "no step grid";
     if (E > G2_STEP_MAXE || F > G2_STEP_MAXF) return "n_embd or ffn above the step kernel's ceilings";
     if (E % VE || F % VE || E != 64 * NH) return "sizes not multiples of the weight chunk or head dim not 64";
-    const int dims[5][2] = { { 3 * E, E }, { E, E }, { F, E }, { E, F }, { V, E } };
+    if (nwg <= NH) return "no work-group left for the proj rows beside the head merges";
+    /* rows, K and the work-groups sharing the rows (proj: those merging no head) */
+    const int dims[5][3] = { { 3 * E, E, nwg }, { E, E, nwg - NH }, { F, E, nwg }, { E, F, nwg }, { V, E, nwg } };
     for (int i = 0; i < 5; ++i) {
         const int C = dims[i][1] / VE, need = (C + G2P_SEGC - 1) / G2P_SEGC;
         if (need > 8) return "a matrix row exceeds 8 segments";
         const int nseg = need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : 8));
-        if ((long)((dims[i][0] + nwg - 1) / nwg) * nseg > G2_STEP_MAXUNITS)
+        if ((long)((dims[i][0] + dims[i][2] - 1) / dims[i][2]) * nseg > G2_STEP_MAXUNITS)
             return "a matrix exceeds the units per work-group";
     }
     return 0;

@@ -124,6 +124,7 @@ int main(int argc, char **argv)
         printf("refused: %s\n", why);
         return 3;
     }
+    long proj_rows = 0; /* rows of proj over all work-groups and layers */
     for (long wg = 0; wg < nwg; ++wg) {
         /* embedding of the token at pos, LayerNorm parameters */
         for (int tid = 0; tid < NT; ++tid) {
@@ -179,9 +180,13 @@ int main(int argc, char **argv)
                 chk("O words", R + G2X_O(E, NH) + h * 64, R + G2X_O(E, NH) + h * 64 + 64, R + G2X_X1(E, NH));
             }
             /* PROJ, FC, FC2 */
-            matrix("proj weights", "b", E, E, VE, 1, wg, nwg);
-            const g2p_rows pp = g2p_rows_plan(E, E, VE, wg, nwg);
-            chk("X1 words", R + G2X_X1(E, NH) + pp.r0, R + G2X_X1(E, NH) + pp.r0 + pp.nrows, R + G2X_H(E, NH));
+            /* proj: the work-groups merging no head */
+            if (wg >= NH) {
+                matrix("proj weights", "b", E, E, VE, 1, wg - NH, nwg - NH);
+                const g2p_rows pp = g2p_proj_plan(E, VE, NH, wg, nwg);
+                chk("X1 words", R + G2X_X1(E, NH) + pp.r0, R + G2X_X1(E, NH) + pp.r0 + pp.nrows, R + G2X_H(E, NH));
+                proj_rows += pp.nrows;
+            }
             matrix("fc weights", "b", F, E, VE, 4, wg, nwg);
             const g2p_rows pf = g2p_rows_plan(F, E, VE, wg, nwg);
             chk("H words", R + G2X_H(E, NH) + pf.r0, R + G2X_H(E, NH) + pf.r0 + pf.nrows, R + G2X_X2(E, NH, F));
@@ -197,6 +202,8 @@ int main(int argc, char **argv)
         const long AM = G2X_HEAD + (long)L * xlayer;
         chk("argmax words", AM + 2 * wg, AM + 2 * wg + 2, G2X_ARRIVE(L, xlayer, nwg));
     }
+    /* the proj rows of the non-merging work-groups cover every row once */
+    if (proj_rows != (long)L * E) chk("proj rows covered once", 0, 1, 0);
     printf("checked %ld accesses, %ld out of bounds%s%s\n", n_checked, n_bad, n_bad ? "; first: " : "",
            n_bad ? first_bad : "");
     return n_bad ? 1 : 0;
