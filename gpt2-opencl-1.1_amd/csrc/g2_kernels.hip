@@ -1274,15 +1274,20 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_mfma(const g2
  *      one dim);
  *   P  written in fp32 as [row][key] and read back as the A operand (8
  *      consecutive keys of one row), split after the read.
- * Row pitch 72 halves (144 bytes): the 16 lanes of a 16-byte read or write
- * pass start 36 dwords apart, which covers the 64 banks once. */
+ * Bank-conflict-free layouts by XOR swizzle, no padding: a staged K/V row
+ * is 128 bytes (8 chunks of 8 halves), chunk c of row r at slot
+ * c ^ (r / 2 % 8), the GEMM tiles' scheme (the 16 rows of an operand read
+ * fall on distinct banks); a P row is 256 bytes (16 chunks of 4 floats),
+ * chunk c of row r at slot c ^ (r % 16). */
+__device__ __forceinline__ int kv_at(int row, int chunk) { return row * 64 + 8 * (chunk ^ ((row >> 1) & 7)); }
+__device__ __forceinline__ int p_at(int row, int chunk) { return row * 64 + 4 * (chunk ^ (row & 15)); }
+
 extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_attnp_args a)
 {
-    constexpr int KP = 72, LDP = 68;
-    constexpr int TILE = 64 * KP; /* halves per staged array */
+    constexpr int TILE = 64 * 64; /* halves per staged array */
     /* per half hs: Kh, Kl, Vh, Vl at (4 hs + 0..3) * TILE */
     __shared__ __attribute__((aligned(16))) _Float16 kvs[8 * TILE];
-    __shared__ __attribute__((aligned(16))) float Ps[8][16 * LDP];
+    __shared__ __attribute__((aligned(16))) float Ps[8][16 * 64];
     const int h = blockIdx.x, qb = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
     const int rg = wave & 3, hs = wave >> 2;
@@ -1340,10 +1345,11 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
                 kh[e] = hi16(kx[8 * c + e]); kl[e] = lo16(kx[8 * c + e]);
                 vh[e] = hi16(vx[8 * c + e]); vl[e] = lo16(vx[8 * c + e]);
             }
-            *(f16x8 *)(Kh + sj * KP + 16 * sc + 8 * c) = kh;
-            *(f16x8 *)(Kl + sj * KP + 16 * sc + 8 * c) = kl;
-            *(f16x8 *)(Vh + sj * KP + 16 * sc + 8 * c) = vh;
-            *(f16x8 *)(Vl + sj * KP + 16 * sc + 8 * c) = vl;
+            const int at = kv_at(sj, 2 * sc + c);
+            *(f16x8 *)(Kh + at) = kh;
+            *(f16x8 *)(Kl + at) = kl;
+            *(f16x8 *)(Vh + at) = vh;
+            *(f16x8 *)(Vl + at) = vl;
         }
         __syncthreads();
         kvload(kb + 2);
@@ -1357,8 +1363,9 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
             for (int t = 0; t < 4; ++t)
 #pragma unroll
                 for (int s2 = 0; s2 < 2; ++s2) {
-                    bh[t][s2] = *(const f16x8 *)(Kh + (16 * t + lr) * KP + 32 * s2 + 8 * lg);
-                    bl[t][s2] = *(const f16x8 *)(Kl + (16 * t + lr) * KP + 32 * s2 + 8 * lg);
+                    const int at = kv_at(16 * t + lr, 4 * s2 + lg);
+                    bh[t][s2] = *(const f16x8 *)(Kh + at);
+                    bl[t][s2] = *(const f16x8 *)(Kl + at);
                 }
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2)
@@ -1403,7 +1410,7 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) pw[(4 * lg + r) * LDP + 16 * t + lr] = sacc[t][r];
+            for (int r = 0; r < 4; ++r) pw[p_at(4 * lg + r, 4 * t + (lr >> 2)) + (lr & 3)] = sacc[t][r];
         __builtin_amdgcn_wave_barrier();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
@@ -1413,8 +1420,8 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
         f16x8 ph[2], pl[2];
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-            const f32x4 x0 = *(const f32x4 *)(pw + lr * LDP + 32 * s2 + 8 * lg);
-            const f32x4 x1 = *(const f32x4 *)(pw + lr * LDP + 32 * s2 + 8 * lg + 4);
+            const f32x4 x0 = *(const f32x4 *)(pw + p_at(lr, 8 * s2 + 2 * lg));
+            const f32x4 x1 = *(const f32x4 *)(pw + p_at(lr, 8 * s2 + 2 * lg + 1));
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 ph[s2][e] = hi16(x0[e]); pl[s2][e] = lo16(x0[e]);
@@ -1427,8 +1434,9 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
             for (int t = 0; t < 4; ++t)
 #pragma unroll
                 for (int s2 = 0; s2 < 2; ++s2) {
-                    bh[t][s2] = *(const f16x8 *)(Vh + (16 * t + lr) * KP + 32 * s2 + 8 * lg);
-                    bl[t][s2] = *(const f16x8 *)(Vl + (16 * t + lr) * KP + 32 * s2 + 8 * lg);
+                    const int at = kv_at(16 * t + lr, 4 * s2 + lg);
+                    bh[t][s2] = *(const f16x8 *)(Vh + at);
+                    bl[t][s2] = *(const f16x8 *)(Vl + at);
                 }
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2)
@@ -1445,7 +1453,8 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
         }
     }
     __syncthreads();
-    float *xw = (float *)kvs + (size_t)(rg * 64 + lane) * 24;
+    /* odd stride: the 64 lanes of a word access fall on distinct banks */
+    float *xw = (float *)kvs + (size_t)(rg * 64 + lane) * 25;
     if (hs == 1) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
