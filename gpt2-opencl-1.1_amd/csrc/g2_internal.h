@@ -64,7 +64,10 @@ extern "C" {
     X(HGEMM_PARTIAL, "g2k_hgemm_partial") X(SPLITK_RESID, "g2k_splitk_resid") \
     X(HGEMM2_GELU, "g2k_hgemm2_gelu") X(HGEMM2_RESID, "g2k_hgemm2_resid")     \
     X(HGEMM2_QKV, "g2k_hgemm2_qkv") X(HGEMM2_PARTIAL, "g2k_hgemm2_partial")   \
-    X(LAYERNORM_SPLIT, "g2k_layernorm_split") X(SPLITK_RESID_LN, "g2k_splitk_resid_ln")
+    X(LAYERNORM_SPLIT, "g2k_layernorm_split") X(SPLITK_RESID_LN, "g2k_splitk_resid_ln") \
+    X(SGEMM_GELU, "g2k_sgemm_gelu") X(SGEMM_RESID, "g2k_sgemm_resid")         \
+    X(SGEMM_QKV, "g2k_sgemm_qkv") X(SGEMM_PARTIAL, "g2k_sgemm_partial")       \
+    X(SPLITK_EPI, "g2k_splitk_epi")
 
 #define G2_ENUM_ENTRY(id, name) G2F_##id,
 enum { G2_KERNEL_LIST(G2_ENUM_ENTRY) G2F_COUNT };
@@ -89,6 +92,12 @@ int g2i_launch(int fid, unsigned gx, unsigned gy, unsigned bx, void *args);
 int g2i_launch3(int fid, unsigned gx, unsigned gy, unsigned gz, unsigned bx, void *args);
 /* largest K split of the fp16 prefill GEMM (its slice buffer holds this many) */
 #define G2_PF_MAXSPLIT 5
+/* the fp32-weight prefill GEMM's split-K slices (floats; 8 MiB) and its
+ * epilogue codes (g2k_sgemm_*, g2k_splitk_epi) */
+#define G2_SG_PART_FLOATS ((size_t)512 * 4096)
+#define G2_SG_GELU 1
+#define G2_SG_RESID 2
+#define G2_SG_QKV 3
 /* Cooperative launch (all gx work-groups co-resident) of a 1-D grid. */
 int g2i_coop_launch(int fid, unsigned gx, unsigned bx, void *args);
 /* Work-groups of the persistent step kernel's grid (0: not supported). */

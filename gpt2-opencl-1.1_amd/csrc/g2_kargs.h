@@ -76,6 +76,19 @@ typedef struct {
 } g2_skred_args;
 #define G2_SKLN_MAXN 2048
 
+/* The split-K epilogue of the fp32-weight prefill GEMM (g2k_splitk_epi):
+ * v[m,n] = (sum over z < ks in order of part[z][m][n]) + bias[n], then epi
+ * 1 gelu (C = gelu(v)), 2 resid (C = C + v), 3 qkv (q_out / k_cache /
+ * v_cache as g2_gemm_args' qkv epilogue).  N % 4 == 0. */
+typedef struct {
+    const float *part;
+    const float *bias;
+    float *C;
+    float *q_out, *k_cache, *v_cache;
+    int M, N, ks, epi;
+    int E, S, pos0;
+} g2_skepi_args;
+
 /* Reference-layout matvec, first pass: partial[split*N + n] = sum over the
  * split's contiguous k-range of A[k] B[k*N + n]; grid (column tiles, splits). */
 typedef struct {

@@ -537,6 +537,188 @@ G2_GEMM(g2k_gemm_nk_f32_qkv, float, true, GEPI_QKV)
 G2_GEMM(g2k_gemm_nk_f16_qkv, _Float16, true, GEPI_QKV)
 
 /* ======================================================================
+ * fp32-weight GEMM of the fused prefill, C = A . W^T with W [N,K] packed
+ * output-major (fp32): 64x64 tiles, 4 waves of 32x32 (2x2 fragments of
+ * v_mfma_f32_16x16x4f32), K in steps of 32 streamed global -> LDS with
+ * global_load_lds_dwordx4 into a three-step ring (two steps in flight, one
+ * barrier per step).  Rows of a staged tile are 128 bytes, chunk c of row r
+ * at slot c ^ (r / 2 % 8), so the 16 rows of a fragment read fall on
+ * distinct banks.  A lane reads the 4 consecutive k of one chunk with one
+ * 16-byte read and feeds them to 4 successive products: in product s, the
+ * instruction's k index j (lane / 16) stands for k = 16 kk + 4 j + s, for A
+ * and W alike, so the 4 products of a chunk pass cover its 16 k once.
+ * Split-K: gridDim.z slices of whole steps (slices differ by at most one),
+ * each writing its partial tile to part[z][M][N]; g2k_splitk_epi then sums
+ * the slices in order and applies the epilogue.  With one slice the
+ * epilogue runs here.  Requires K % 32 == 0.
+ * ==================================================================== */
+namespace sg {
+constexpr int BM = 64, BN = 64, BK = 32, NS = 3;
+constexpr int TB = BM * BK * 4; /* bytes of one 64 x 32 fp32 tile */
+constexpr int STAGE = 2 * TB;   /* A, W: 16 KB */
+typedef __attribute__((address_space(3))) void lds_t;
+
+/* The wave's products of one step from the stage at st. */
+__device__ __forceinline__ void mma(f32x4 (&acc)[2][2], const unsigned char *st, int wm, int wn, int lane)
+{
+    const int fr = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+        const int c = 4 * kk + g;
+        f32x4 af[2], bf[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int row = wm * 32 + i * 16 + fr;
+            af[i] = *(const f32x4 *)(st + row * 128 + ((c ^ ((row >> 1) & 7)) << 4));
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int row = wn * 32 + j * 16 + fr;
+            bf[j] = *(const f32x4 *)(st + TB + row * 128 + ((c ^ ((row >> 1) & 7)) << 4));
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][q], bf[j][q], acc[i][j], 0, 0, 0);
+    }
+}
+} /* namespace sg */
+
+template <int EPI>
+__device__ void sgemm_impl(const g2_gemm_args &a)
+{
+    using namespace sg;
+    __shared__ __attribute__((aligned(1024))) unsigned char lds[NS * STAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int M = a.M, N = a.N, K = a.K;
+    const int nkt = K / BK, ks = gridDim.z;
+    const int s0 = (int)(((long)nkt * blockIdx.z) / ks), s1 = (int)(((long)nkt * (blockIdx.z + 1)) / ks);
+    const int nk = s1 - s0;
+    /* this lane's load sources: wave w fills rows 16w..16w+15 of each tile
+     * with two instructions of 8 rows (lane -> row l/8, slot l%8, holding
+     * the chunk that the swizzle puts there); rows past M or N read the
+     * last row (their results are not stored) */
+    const float *as[2], *bs[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int row = 16 * wave + 8 * h + (lane >> 3);
+        const int ch = (lane & 7) ^ ((row >> 1) & 7);
+        as[h] = a.A + (size_t)min(m0 + row, M - 1) * K + s0 * BK + 4 * ch;
+        bs[h] = (const float *)a.B + (size_t)min(n0 + row, N - 1) * K + s0 * BK + 4 * ch;
+    }
+    /* step t's loads into stage buffer b (steps past the last reload it) */
+    auto issue = [&](int t, int b) {
+        const int k = min(t, nk - 1) * BK;
+        unsigned char *st = lds + b * STAGE + (16 * wave) * 128;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            __builtin_amdgcn_global_load_lds(as[h] + k, (lds_t *)(st + h * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(bs[h] + k, (lds_t *)(st + TB + h * 1024), 16, 0, 0);
+        }
+    };
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    issue(0, 0);
+    issue(1, 1);
+    int cur = 0;
+    for (int t = 0; t < nk; ++t) {
+        /* step t has landed (the 4 loads per wave of step t+1 may remain in
+         * flight); every wave is done with the buffer of step t-1 */
+        asm volatile("s_waitcnt vmcnt(4)\n\ts_barrier" ::: "memory");
+        issue(t + 2, cur == 0 ? 2 : cur - 1);
+        mma(acc, lds + cur * STAGE, wm, wn, lane);
+        cur = cur == 2 ? 0 : cur + 1;
+    }
+    /* no load may land in LDS after the work-group has ended */
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    if constexpr (EPI == GEPI_PARTIAL) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
+                    const int n = n0 + wn * 32 + j * 16 + (lane & 15);
+                    if (m < M && n < N) a.part[((size_t)blockIdx.z * M + m) * N + n] = acc[i][j][r];
+                }
+        return;
+    }
+    epi_add<EPI>(acc, a, m0 + wm * 32, n0 + wn * 32, lane, M, N);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
+                const int n = n0 + wn * 32 + j * 16 + (lane & 15);
+                if (m >= M || n >= N) continue;
+                const float v = acc[i][j][r];
+                if (EPI == GEPI_GELU) {
+                    a.C[(size_t)m * N + n] = gelu_f(v);
+                } else if (EPI == GEPI_RESID) {
+                    a.C[(size_t)m * N + n] = v;
+                } else {
+                    const int E = a.E, pos = a.pos0 + m;
+                    if (n < E) a.q_out[(size_t)m * E + n] = v;
+                    else if (n < 2 * E) a.k_cache[(size_t)(n - E) * a.S + pos] = v;
+                    else a.v_cache[(size_t)pos * E + (n - 2 * E)] = v;
+                }
+            }
+}
+
+#define G2_SGEMM(name, EPI) \
+    G2K void name(const g2_gemm_args a) { sgemm_impl<EPI>(a); }
+G2_SGEMM(g2k_sgemm_gelu, GEPI_GELU)
+G2_SGEMM(g2k_sgemm_resid, GEPI_RESID)
+G2_SGEMM(g2k_sgemm_qkv, GEPI_QKV)
+G2_SGEMM(g2k_sgemm_partial, GEPI_PARTIAL)
+
+/* The split-K epilogue of g2k_sgemm_partial: v = (part[0][m][n] + ... +
+ * part[ks-1][m][n]) + bias[n], then by epi: gelu (C = gelu(v)), resid
+ * (C = C + v, in place), qkv (the K/V cache scatter of GEPI_QKV).  Four
+ * consecutive columns per thread (16-byte loads; N % 4 == 0). */
+G2K void g2k_splitk_epi(const g2_skepi_args a)
+{
+    const int N4 = a.N >> 2;
+    const size_t MN = (size_t)a.M * a.N, n4s = (size_t)a.M * N4;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4s; i += (size_t)gridDim.x * 256) {
+        const int m = (int)(i / N4), n = (int)(i % N4) * 4;
+        const size_t o = (size_t)m * a.N + n;
+        f32x4 v = *(const f32x4 *)(a.part + o);
+        for (int z = 1; z < a.ks; ++z) v += *(const f32x4 *)(a.part + (size_t)z * MN + o);
+        if (a.bias) v += *(const f32x4 *)(a.bias + n);
+        if (a.epi == GEPI_GELU) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a.C[o + e] = gelu_f(v[e]);
+        } else if (a.epi == GEPI_RESID) {
+            const f32x4 c = *(const f32x4 *)(a.C + o);
+            *(f32x4 *)(a.C + o) = c + v;
+        } else {
+            const int E = a.E, pos = a.pos0 + m;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int c = n + e;
+                if (c < E) a.q_out[(size_t)m * E + c] = v[e];
+                else if (c < 2 * E) a.k_cache[(size_t)(c - E) * a.S + pos] = v[e];
+                else a.v_cache[(size_t)pos * E + (c - 2 * E)] = v[e];
+            }
+        }
+    }
+}
+
+/* ======================================================================
  * fp16 MFMA GEMM for the fused prefill with fp16 weights:
  * C[M,N] = A[M,K] . W[N,K]^T + bias with the epilogues of g2_gemm_args.
  *

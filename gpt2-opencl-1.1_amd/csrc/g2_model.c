@@ -229,6 +229,7 @@ static int alloc_workspaces(g2_model *m)
     A(m->qkv_new, T * 4); A(m->qkv_full, S * T * 4); A(m->last_hidden, E * 4);
     A(m->logits, V * 4); A(m->ids_dev, S * 4); A(m->partial, 8 * V * 4);
     if (m->path == G2_PATH_FUSED && m->dtype == G2_F16) A(m->pf_part, (size_t)G2_PF_MAXSPLIT * S * E * 4);
+    if (m->path == G2_PATH_FUSED && m->dtype == G2_F32) A(m->pf_part, (size_t)G2_SG_PART_FLOATS * 4);
     A(m->scores, NH * S * 4); A(m->q, S * E * 4);
     A(m->state, G2S_WORDS * 4);
     A(m->att_part, NH * G2_ATTN_MAX_CHUNKS * 66 * 4);
@@ -876,6 +877,37 @@ static int prefill_resid(g2_model *m, const float *A, const uint16_t *Ah, const 
     return rc;
 }
 
+/* The fp32-weight prefill GEMM (g2k_sgemm_*, K % 32 == 0) with epilogue
+ * epi (G2_SG_GELU, _RESID or _QKV as g2_gemm_args describes them).  A
+ * prompt too short to fill the machine with 64x64 tiles gets split-K
+ * slices (at most 8, each at least two K steps of 32), summed in order with
+ * the bias and the epilogue by g2k_splitk_epi: as many as keep the
+ * work-groups within 256, or within 512 for a K of 64 steps or more (fc2).
+ * Measured at 64..512 rows and n_embd 768..1280, this picks the best or
+ * within 10% of the best of 1..8 slices for every GEMM.  ks slices of at
+ * most 64 ceil(M/64) x 64 ceil(N/64) floats each fit G2_SG_PART_FLOATS:
+ * ks * tiles <= 512. */
+static int prefill_sgemm(g2_model *m, int epi, g2_gemm_args *g)
+{
+    const unsigned gx = cdivu(g->N, 64), gy = cdivu(g->M, 64), tiles = gx * gy;
+    const int nk = g->K / 32;
+    const unsigned target = nk >= 64 ? 512 : 256;
+    int ks = tiles >= target ? 1 : (int)(target / tiles);
+    if (ks > 8) ks = 8;
+    if (ks > nk / 2) ks = nk / 2 > 1 ? nk / 2 : 1;
+    if ((size_t)ks * g->M * g->N > G2_SG_PART_FLOATS) return g2i_err(G2_E_LIMIT, "split-K slices exceed the buffer");
+    if (ks == 1)
+        return g2i_launch(epi == G2_SG_GELU ? G2F_SGEMM_GELU : epi == G2_SG_RESID ? G2F_SGEMM_RESID : G2F_SGEMM_QKV,
+                          gx, gy, 256, g);
+    g->part = m->pf_part;
+    int rc = g2i_launch3(G2F_SGEMM_PARTIAL, gx, gy, (unsigned)ks, 256, g);
+    g2_skepi_args e = { m->pf_part, g->bias, g->C, g->q_out, g->k_cache, g->v_cache, g->M, g->N, ks, epi,
+                        g->E, g->S, g->pos0 };
+    const unsigned n4 = cdivu((unsigned)(g->M * g->N / 4), 256);
+    if (!rc) rc = g2i_launch(G2F_SPLITK_EPI, n4 < 2048 ? n4 : 2048, 1, 256, &e);
+    return rc;
+}
+
 static int fused_prefill(g2_model *m, int P)
 {
     const int E = m->cfg.n_embd, F = m->cfg.ffn_dim, NH = m->cfg.n_head;
@@ -889,6 +921,9 @@ static int fused_prefill(g2_model *m, int P)
      * keeps the 64x64 ones, whose results are identical) */
     const char *p64 = getenv("G2_PREFILL_GEMM64");
     const int big = h && P > 64 && !(p64 && p64[0] == '1');
+    /* fp32 weights: the 64x64 fp32-MFMA GEMM with K steps of 32 streamed
+     * through LDS, split-K for short prompts */
+    const int sg = !f16 && E % 32 == 0 && F % 32 == 0;
     const int f_qkv = big ? G2F_HGEMM2_QKV : h ? G2F_HGEMM_QKV : (f16 ? G2F_GEMM_NK_F16_QKV : G2F_GEMM_NK_F32_QKV);
     const int f_resid = h ? G2F_HGEMM_RESID : (f16 ? G2F_GEMM_NK_F16_RESID : G2F_GEMM_NK_F32_RESID);
     const int f_gelu = big ? G2F_HGEMM2_GELU : h ? G2F_HGEMM_GELU : (f16 ? G2F_GEMM_NK_F16_GELU : G2F_GEMM_NK_F32_GELU);
@@ -916,7 +951,8 @@ static int fused_prefill(g2_model *m, int P)
         g.k_cache = y->k_cache; g.v_cache = y->v_cache; g.M = P; g.N = 3 * E; g.K = E;
         g.E = E; g.S = G2_KV_MAX_SEQ; g.pos0 = 0;
         if (!rc) rc = big ? g2i_launch(f_qkv, 8 * cdivu(cdivu(3 * E, 128), 8) * cdivu(P, 128), 1, 1024, &g)
-                          : g2i_launch(f_qkv, cdivu(3 * E, 64), cdivu(P, 64), 256, &g);
+                      : sg  ? prefill_sgemm(m, G2_SG_QKV, &g)
+                            : g2i_launch(f_qkv, cdivu(3 * E, 64), cdivu(P, 64), 256, &g);
         g2_attnp_args t = { m->q, y->k_cache, y->v_cache, m->attn, P, E, NH, G2_KV_MAX_SEQ, 1.0f / sqrtf(64.0f),
                             big ? at_h : NULL, big ? at_l : NULL };
         if (!rc) rc = g2i_launch(attn32 ? G2F_ATTN_PREFILL_MFMA : G2F_ATTN_PREFILL_H16, (unsigned)NH, cdivu(P, 64), 512, &t);
@@ -925,7 +961,8 @@ static int fused_prefill(g2_model *m, int P)
         int ln2_done = 0;
         if (!rc) rc = h ? prefill_resid(m, m->attn, at_h, at_l, y->proj_w, y->proj_b, m->hidden, P, E, E, big,
                                         y->ln2_w, y->ln2_b, ln_h, ln_l, &ln2_done)
-                        : g2i_launch(f_resid, cdivu(E, 64), cdivu(P, 64), 256, &g);
+                      : sg ? prefill_sgemm(m, G2_SG_RESID, &g)
+                           : g2i_launch(f_resid, cdivu(E, 64), cdivu(P, 64), 256, &g);
         g2_lnsplit_args ls2 = { m->hidden, ln_h, ln_l, y->ln2_w, y->ln2_b, E, P };
         if (!rc && !ln2_done)
             rc = big ? g2i_launch(G2F_LAYERNORM_SPLIT, (unsigned)P, 1, 256, &ls2)
@@ -934,14 +971,16 @@ static int fused_prefill(g2_model *m, int P)
         g.A = m->ln_out; g.B = y->fc_w; g.bias = y->fc_b; g.C = m->ffn1; g.M = P; g.N = F; g.K = E;
         g.Ah = ln_h; g.Al = ln_l; g.Ch = ff_h; g.Cl = ff_l;
         if (!rc) rc = big ? g2i_launch(f_gelu, 8 * cdivu(cdivu(F, 128), 8) * cdivu(P, 128), 1, 1024, &g)
-                          : g2i_launch(f_gelu, cdivu(F, 64), cdivu(P, 64), 256, &g);
+                      : sg  ? prefill_sgemm(m, G2_SG_GELU, &g)
+                            : g2i_launch(f_gelu, cdivu(F, 64), cdivu(P, 64), 256, &g);
         memset(&g, 0, sizeof g);
         g.A = m->ffn1; g.B = y->fc2_w; g.bias = y->fc2_b; g.C = m->hidden; g.M = P; g.N = E; g.K = F;
         const g2_layer *yn = l + 1 < m->cfg.n_layer ? &m->L[l + 1] : NULL;
         ln1_done = 0;
         if (!rc) rc = h ? prefill_resid(m, m->ffn1, ff_h, ff_l, y->fc2_w, y->fc2_b, m->hidden, P, E, F, big,
                                         yn ? yn->ln1_w : NULL, yn ? yn->ln1_b : NULL, ln_h, ln_l, &ln1_done)
-                        : g2i_launch(f_resid, cdivu(E, 64), cdivu(P, 64), 256, &g);
+                      : sg ? prefill_sgemm(m, G2_SG_RESID, &g)
+                           : g2i_launch(f_resid, cdivu(E, 64), cdivu(P, 64), 256, &g);
     }
     if (!rc) rc = fused_lm_head(m, m->hidden + (size_t)(P - 1) * E, 1);
     return rc;
