@@ -161,8 +161,6 @@ extern "C" __global__ __launch_bounds__(64) void g2k_attn_merge(const g2_attn1q_
  * ==================================================================== */
 enum { EPI_STORE = 0, EPI_GELU = 1, EPI_RESID = 2, EPI_QKV = 3, EPI_ARGMAX = 4 };
 
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
 template <typename WT> struct chunk_t;
 template <> struct chunk_t<float> { static constexpr int V = 4; };
 template <> struct chunk_t<_Float16> { static constexpr int V = 8; };

@@ -55,7 +55,6 @@ extern "C" {
     X(GEMM_NK_F16_RESID, "g2k_gemm_nk_f16_resid")                             \
     X(GEMM_NK_F32_QKV, "g2k_gemm_nk_f32_qkv")                                 \
     X(GEMM_NK_F16_QKV, "g2k_gemm_nk_f16_qkv")                                 \
-    X(ATTN_PREFILL, "g2k_attn_prefill")                                       \
     X(STEP_F32, "g2k_step_f32") X(STEP_F16, "g2k_step_f16")                   \
     X(HGEMM_STORE, "g2k_hgemm_store") X(HGEMM_GELU, "g2k_hgemm_gelu")         \
     X(HGEMM_RESID, "g2k_hgemm_resid") X(HGEMM_QKV, "g2k_hgemm_qkv")           \

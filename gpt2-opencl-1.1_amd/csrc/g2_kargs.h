@@ -55,6 +55,11 @@ typedef struct {
     int E, S, pos0;
     float *part;
     int ksplit;
+    /* qkv epilogue, when non-NULL: the key columns also as fp16 halves to
+     * kh, kl [S rows (positions)][E], the value columns as fp16 halves to
+     * vth, vtl [E][S] (transposed): the staged operands of the prompt
+     * attention (g2_attnp_args) */
+    uint16_t *kh, *kl, *vth, *vtl;
     /* the 128x128 fp16 GEMM (g2k_hgemm2_*): A given as its fp16 halves
      * Ah = fp16(a), Al = fp16(a - Ah), [M,K] each (A unused); epilogue
      * gelu_split writes gelu(acc + bias) as halves to Ch, Cl [M,N] */
@@ -87,6 +92,7 @@ typedef struct {
     float *q_out, *k_cache, *v_cache;
     int M, N, ks, epi;
     int E, S, pos0;
+    uint16_t *kh, *kl, *vth, *vtl; /* as in g2_gemm_args */
 } g2_skepi_args;
 
 /* Reference-layout matvec, first pass: partial[split*N + n] = sum over the
@@ -285,7 +291,9 @@ typedef struct {
 #define G2X_ARRIVE(L, xlayer, nwg) ((long)G2X_HEAD + (long)(L) * (xlayer) + 2L * (nwg) + 32)
 
 /* Causal attention over a prompt block: rows i < P of q[P,E]; keys/values
- * j <= i from the transposed K cache and the V cache; head dim 64. */
+ * j <= i, head dim 64: g2k_attn_prefill_mfma reads them from the transposed
+ * K cache and the V cache, g2k_attn_prefill_h16 from the fp16 halves the
+ * qkv epilogue wrote (kh, kl [S][E]; vth, vtl [E][S]). */
 typedef struct {
     const float *q;
     const float *k_cache;
@@ -296,6 +304,7 @@ typedef struct {
     /* non-NULL: the output is written as fp16 halves (see g2_lnsplit_args)
      * to out_hi, out_lo [P,E] instead of to out */
     uint16_t *out_hi, *out_lo;
+    const uint16_t *kh, *kl, *vth, *vtl;
 } g2_attnp_args;
 
 #endif /* G2_KARGS_H */

@@ -26,6 +26,7 @@
 #define G2K extern "C" __global__ __launch_bounds__(256)
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 
@@ -226,6 +227,91 @@ __device__ __forceinline__ _Float16 lo16(float v)
 {
 #pragma clang fp contract(off)
     return (_Float16)(v - (float)(_Float16)v);
+}
+
+/* Two fp16 values packed low-first into one word. */
+__device__ __forceinline__ unsigned pk16(_Float16 a, _Float16 b)
+{
+    return (unsigned)__builtin_bit_cast(uint16_t, a) | ((unsigned)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+/* The qkv epilogue of output (m, n), v final: columns < E to q_out[m][n];
+ * key columns E..2E-1 to the transposed K cache at position pos0 + m and,
+ * when kh is set, as fp16 halves to kh/kl [position][E]; value columns
+ * 2E..3E-1 to the V cache and as halves to vth/vtl [E][S] (transposed).
+ * The halves are the staged operands of g2k_attn_prefill_h16. */
+struct qkv_dst {
+    float *q_out, *k_cache, *v_cache;
+    uint16_t *kh, *kl, *vth, *vtl;
+    int E, S, pos0;
+};
+__device__ __forceinline__ void qkv_store(const qkv_dst &d, int m, int n, float v)
+{
+    const int E = d.E, pos = d.pos0 + m;
+    if (n < E) {
+        d.q_out[(size_t)m * E + n] = v;
+    } else if (n < 2 * E) {
+        d.k_cache[(size_t)(n - E) * d.S + pos] = v;
+        if (d.kh) split_store(d.kh, d.kl, (size_t)pos * E + (n - E), v);
+    } else {
+        d.v_cache[(size_t)pos * E + (n - 2 * E)] = v;
+        if (d.kh) split_store(d.vth, d.vtl, (size_t)(n - 2 * E) * d.S + pos, v);
+    }
+}
+template <typename ARGS>
+__device__ __forceinline__ qkv_dst qkv_of(const ARGS &a)
+{
+    return qkv_dst{a.q_out, a.k_cache, a.v_cache, a.kh, a.kl, a.vth, a.vtl, a.E, a.S, a.pos0};
+}
+
+/* The qkv epilogue of rows mb..mb+3 (those < M) of column n, the four
+ * values a lane holds in a 16x16 MFMA result tile: the transposed K cache
+ * and the transposed V halves take the four consecutive positions with one
+ * 16-byte (fp32) or two 8-byte (halves) stores when all four rows exist
+ * and the first position is a multiple of 4. */
+__device__ __forceinline__ void qkv_store4(const qkv_dst &d, int mb, int M, int n, const f32x4 &v)
+{
+    const int E = d.E, pos = d.pos0 + mb;
+    const bool full = mb + 3 < M && (pos & 3) == 0;
+    if (n < E) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (mb + q < M) d.q_out[(size_t)(mb + q) * E + n] = v[q];
+    } else if (n < 2 * E) {
+        float *kc = d.k_cache + (size_t)(n - E) * d.S + pos;
+        if (full) {
+            *(f32x4 *)kc = v;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (mb + q < M) kc[q] = v[q];
+        }
+        if (d.kh) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (mb + q < M) split_store(d.kh, d.kl, (size_t)(pos + q) * E + (n - E), v[q]);
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if (mb + q < M) d.v_cache[(size_t)(pos + q) * E + (n - 2 * E)] = v[q];
+        if (d.kh) {
+            const size_t o = (size_t)(n - 2 * E) * d.S + pos;
+            if (full) {
+                uint2 hv, lv;
+                hv.x = pk16(hi16(v[0]), hi16(v[1]));
+                hv.y = pk16(hi16(v[2]), hi16(v[3]));
+                lv.x = pk16(lo16(v[0]), lo16(v[1]));
+                lv.y = pk16(lo16(v[2]), lo16(v[3]));
+                *(uint2 *)(d.vth + o) = hv;
+                *(uint2 *)(d.vtl + o) = lv;
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    if (mb + q < M) split_store(d.vth, d.vtl, o + q, v[q]);
+            }
+        }
+    }
 }
 
 /* ---- layernorm (math.cl:283-311): one work-group per row, two-pass mean and
@@ -497,6 +583,17 @@ __device__ void gemm_impl(const g2_gemm_args &a)
     }
 
     epi_add<EPI>(acc, a, m0 + wm * 32, n0 + wn * 32, lane, M, N);
+    if constexpr (EPI == GEPI_QKV) {
+        const qkv_dst d = qkv_of(a);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int n = n0 + wn * 32 + j * 16 + (lane & 15);
+                if (n < N) qkv_store4(d, m0 + wm * 32 + i * 16 + 4 * (lane >> 4), M, n, acc[i][j]);
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -513,11 +610,6 @@ __device__ void gemm_impl(const g2_gemm_args &a)
                     a.C[(size_t)m * N + n] = gelu_f(v);
                 } else if (EPI == GEPI_RESID) {
                     a.C[(size_t)m * N + n] = v;
-                } else {
-                    const int E = a.E, pos = a.pos0 + m;
-                    if (n < E) a.q_out[(size_t)m * E + n] = v;
-                    else if (n < 2 * E) a.k_cache[(size_t)(n - E) * a.S + pos] = v;
-                    else a.v_cache[(size_t)pos * E + (n - 2 * E)] = v;
                 }
             }
 }
@@ -655,6 +747,17 @@ __device__ void sgemm_impl(const g2_gemm_args &a)
         return;
     }
     epi_add<EPI>(acc, a, m0 + wm * 32, n0 + wn * 32, lane, M, N);
+    if constexpr (EPI == GEPI_QKV) {
+        const qkv_dst d = qkv_of(a);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int n = n0 + wn * 32 + j * 16 + (lane & 15);
+                if (n < N) qkv_store4(d, m0 + wm * 32 + i * 16 + 4 * (lane >> 4), M, n, acc[i][j]);
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -669,11 +772,6 @@ __device__ void sgemm_impl(const g2_gemm_args &a)
                     a.C[(size_t)m * N + n] = gelu_f(v);
                 } else if (EPI == GEPI_RESID) {
                     a.C[(size_t)m * N + n] = v;
-                } else {
-                    const int E = a.E, pos = a.pos0 + m;
-                    if (n < E) a.q_out[(size_t)m * E + n] = v;
-                    else if (n < 2 * E) a.k_cache[(size_t)(n - E) * a.S + pos] = v;
-                    else a.v_cache[(size_t)pos * E + (n - 2 * E)] = v;
                 }
             }
 }
@@ -706,14 +804,9 @@ G2K void g2k_splitk_epi(const g2_skepi_args a)
             const f32x4 c = *(const f32x4 *)(a.C + o);
             *(f32x4 *)(a.C + o) = c + v;
         } else {
-            const int E = a.E, pos = a.pos0 + m;
+            const qkv_dst d = qkv_of(a);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int c = n + e;
-                if (c < E) a.q_out[(size_t)m * E + c] = v[e];
-                else if (c < 2 * E) a.k_cache[(size_t)(c - E) * a.S + pos] = v[e];
-                else a.v_cache[(size_t)pos * E + (c - 2 * E)] = v[e];
-            }
+            for (int e = 0; e < 4; ++e) qkv_store(d, m, n + e, v[e]);
         }
     }
 }
@@ -818,6 +911,17 @@ __device__ void hgemm_impl(const g2_gemm_args &a)
     }
 
     epi_add<EPI>(acc, a, m0 + wm * 32, n0 + wn * 32, lane, M, N);
+    if constexpr (EPI == GEPI_QKV) {
+        const qkv_dst d = qkv_of(a);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int n = n0 + wn * 32 + j * 16 + (lane & 15);
+                if (n < N) qkv_store4(d, m0 + wm * 32 + i * 16 + 4 * (lane >> 4), M, n, acc[i][j]);
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -838,11 +942,6 @@ __device__ void hgemm_impl(const g2_gemm_args &a)
                     a.C[(size_t)m * N + n] = gelu_f(v);
                 } else if (EPI == GEPI_RESID) {
                     a.C[(size_t)m * N + n] = v;
-                } else {
-                    const int E = a.E, pos = a.pos0 + m;
-                    if (n < E) a.q_out[(size_t)m * E + n] = v;
-                    else if (n < 2 * E) a.k_cache[(size_t)(n - E) * a.S + pos] = v;
-                    else a.v_cache[(size_t)pos * E + (n - 2 * E)] = v;
                 }
             }
 }
@@ -1029,6 +1128,17 @@ __device__ void hgemm2_impl(const g2_gemm_args &a)
                     asm volatile("" : "+v"(acc[i][j][q]));
                 }
     }
+    if constexpr (EPI == GEPI_QKV) {
+        const qkv_dst d = qkv_of(a);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int n = n0 + wn * 32 + j * 16 + (lane & 15);
+                if (n < N) qkv_store4(d, m0 + wm * 32 + i * 16 + 4 * (lane >> 4), M, n, acc[i][j]);
+            }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -1047,11 +1157,6 @@ __device__ void hgemm2_impl(const g2_gemm_args &a)
                     split_store(a.Ch, a.Cl, (size_t)m * N + n, gelu_f(v));
                 } else if (EPI == GEPI_RESID) {
                     a.C[(size_t)m * N + n] = v;
-                } else {
-                    const int E = a.E, pos = a.pos0 + m;
-                    if (n < E) a.q_out[(size_t)m * E + n] = v;
-                    else if (n < 2 * E) a.k_cache[(size_t)(n - E) * a.S + pos] = v;
-                    else a.v_cache[(size_t)pos * E + (n - 2 * E)] = v;
                 }
             }
 }
@@ -1142,100 +1247,15 @@ G2K void g2k_hgemm_gelu(const g2_gemm_args a) { hgemm_impl<GEPI_GELU>(a); }
 G2K void g2k_hgemm_resid(const g2_gemm_args a) { hgemm_impl<GEPI_RESID>(a); }
 G2K void g2k_hgemm_qkv(const g2_gemm_args a) { hgemm_impl<GEPI_QKV>(a); }
 
-/* ======================================================================
- * Causal attention over a prompt (prefill), head dim 64
- *
- * grid (NH, ceil(P/64)), 256 threads: thread (r = tid/4, g = tid%4) owns
- * query row r of the block, keys g*16..g*16+15 of each key block for the
- * scores and dims g*16..g*16+15 of the output.  Key blocks 0..qb are staged
- * in LDS (K transposed as in the cache, V row-major); online softmax.
- * ==================================================================== */
-G2K void g2k_attn_prefill(const g2_attnp_args a)
-{
-    constexpr int LD = 65;
-    __shared__ float Qs[64 * LD];
-    __shared__ float Kt[64 * LD];
-    __shared__ float Vs[64 * LD];
-    __shared__ float Ps[64 * LD];
-    const int h = blockIdx.x, qb = blockIdx.y, tid = threadIdx.x;
-    const int r = tid >> 2, g = tid & 3;
-    const int i = qb * 64 + r;
-    const bool row_ok = i < a.P;
-    if (h >= a.NH || qb * 64 >= a.P) return;
-    for (int idx = tid; idx < 64 * 64; idx += 256) {
-        const int rr = idx >> 6, d = idx & 63, ii = qb * 64 + rr;
-        Qs[rr * LD + d] = ii < a.P ? a.q[(size_t)ii * a.E + h * 64 + d] : 0.f;
-    }
-    float o[16];
-#pragma unroll
-    for (int d = 0; d < 16; ++d) o[d] = 0.f;
-    float m = -INFINITY, l = 0.f;
-    for (int kb = 0; kb <= qb; ++kb) {
-        __syncthreads();
-        for (int idx = tid; idx < 64 * 64; idx += 256) {
-            const int d = idx >> 6, key = idx & 63, j = kb * 64 + key;
-            Kt[d * LD + key] = j < a.P ? a.k_cache[(size_t)(h * 64 + d) * a.S + j] : 0.f;
-        }
-        for (int idx = tid; idx < 64 * 64; idx += 256) {
-            const int key = idx >> 6, d = idx & 63, j = kb * 64 + key;
-            Vs[key * LD + d] = j < a.P ? a.v_cache[(size_t)j * a.E + h * 64 + d] : 0.f;
-        }
-        __syncthreads();
-        float s[16];
-#pragma unroll
-        for (int kk = 0; kk < 16; ++kk) s[kk] = 0.f;
-        for (int d = 0; d < 64; ++d) {
-            const float qv = Qs[r * LD + d];
-#pragma unroll
-            for (int kk = 0; kk < 16; ++kk) s[kk] = fmaf(qv, Kt[d * LD + g * 16 + kk], s[kk]);
-        }
-        float bm = -INFINITY;
-#pragma unroll
-        for (int kk = 0; kk < 16; ++kk) {
-            const int j = kb * 64 + g * 16 + kk;
-            s[kk] = (row_ok && j <= i) ? s[kk] * a.scale : -INFINITY;
-            bm = fmaxf(bm, s[kk]);
-        }
-        bm = fmaxf(bm, __shfl_xor(bm, 1));
-        bm = fmaxf(bm, __shfl_xor(bm, 2));
-        const float mn = fmaxf(m, bm);
-        const float ms = mn == -INFINITY ? 0.f : mn;
-        const float alpha = expf(m - ms);
-        float ps = 0.f;
-#pragma unroll
-        for (int kk = 0; kk < 16; ++kk) {
-            const float p = expf(s[kk] - ms);
-            Ps[r * LD + g * 16 + kk] = p;
-            ps += p;
-        }
-        ps += __shfl_xor(ps, 1);
-        ps += __shfl_xor(ps, 2);
-        l = fmaf(l, alpha, ps);
-        m = mn;
-        __syncthreads();
-#pragma unroll
-        for (int d = 0; d < 16; ++d) o[d] *= alpha;
-        for (int key = 0; key < 64; ++key) {
-            const float p = Ps[r * LD + key];
-#pragma unroll
-            for (int d = 0; d < 16; ++d) o[d] = fmaf(p, Vs[key * LD + g * 16 + d], o[d]);
-        }
-    }
-    if (row_ok) {
-        const float inv = 1.0f / l;
-#pragma unroll
-        for (int d = 0; d < 16; ++d) a.out[(size_t)i * a.E + h * 64 + g * 16 + d] = o[d] * inv;
-    }
-}
-
-/* The same attention on the fp32 matrix cores (v_mfma_f32_16x16x4f32):
- * grid (NH, ceil(P/64)), 512 threads; waves w and w + 4 own query rows
+/* Causal attention over a prompt (prefill), head dim 64, on the fp32
+ * matrix cores (v_mfma_f32_16x16x4f32), keys and values from the transposed
+ * K cache and the V cache: grid (NH, ceil(P/64)), 512 threads; waves w and
+ * w + 4 own query rows
  * 16w..16w+15 of the block, the first over the even key blocks, the
  * second over the odd ones, each with its own online softmax, combined at
  * the end (the kernel lasts as long as its longest rows, whose key blocks
  * are thus shared by two waves).  Per 64-key block: S = Q K^T (4 tiles of
- * 16 keys, 16 k
- * steps of 4 dims), scaled and causally masked, online softmax over the
+ * 16 keys, 16 k steps of 4 dims), scaled and causally masked, online softmax over the
  * block (row statistics reduced across the 16 lanes of a row group), P
  * re-laid through LDS into the operand layout, O += P V (4 tiles of 16
  * dims, 16 k steps of 4 keys).  fp32 throughout, as the reference.
@@ -1435,41 +1455,96 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_mfma(const g2
 }
 
 /* Causal prompt attention on the fp16 matrix cores (same arguments, grid
- * and results as g2k_attn_prefill_mfma, whose wave layout, online softmax
- * and half combine it keeps).  Every fp32 operand x is split into fp16
- * halves hi = fp16(x), lo = fp16(x - hi) (split_store), and each product
- * of two split operands is hi.hi + hi.lo + lo.hi on v_mfma_f32_16x16x32_f16
- * (fp32 accumulate; the dropped lo.lo term is below fp32 rounding of the
- * sum): 48 matrix instructions of 16 cycles per wave and 64-key block
- * instead of 128 of 32.
+ * and results as g2k_attn_prefill_mfma: per head and 64-query block, 8
+ * waves, two per 16-row group, each taking every other 64-key block, their
+ * online-softmax states combined at the end).  Every fp32 operand x is
+ * split into fp16 halves hi = fp16(x), lo = fp16(x - hi) (split_store), and
+ * each product of two split operands is hi.hi + hi.lo + lo.hi on
+ * v_mfma_f32_16x16x32_f16 (fp32 accumulate; the dropped lo.lo term is below
+ * fp32 rounding of the sum).
  *
- * The online softmax works in base 2 (scores times log2 e, v_exp_f32),
- * the usual flash-attention form; the probabilities equal exp() of the
+ * The products are computed transposed, S^T = K Q^T and O^T = V^T P^T, so
+ * that a lane holds one query row (lane % 16) throughout: the softmax's row
+ * maximum and sum are in-lane over its 16 scores plus two cross-row lane
+ * swaps, the rescale of O is one factor per lane, and P^T reaches the
+ * second product by two permlane swaps instead of a round trip through LDS.
+ * The online softmax works in base 2 (scores times log2 e, v_exp_f32), the
+ * usual flash-attention form; the probabilities equal exp() of the
  * natural-base scores to fp32 rounding.
  *
  * Operand layouts (v_mfma_f32_16x16x32_f16: lane l supplies
  * A[l%16][8(l/16)..+7] and B[8(l/16)..+7][l%16]; D[4(l/16)+r][l%16]):
- *   Q  A operand, from global (rows of the block, dims 32s + 8(l/16)..+7);
- *   K  staged as [key][dim] halves (the B operand of S = Q K^T is 8
- *      consecutive dims of one key, one 16-byte LDS read);
- *   V  staged as [dim][key] halves (B of O = P V: 8 consecutive keys of
- *      one dim);
- *   P  written in fp32 as [row][key] and read back as the A operand (8
- *      consecutive keys of one row), split after the read.
- * Bank-conflict-free layouts by XOR swizzle, no padding: a staged K/V row
- * is 128 bytes (8 chunks of 8 halves), chunk c of row r at slot
- * c ^ (r / 2 % 8), the GEMM tiles' scheme (the 16 rows of an operand read
- * fall on distinct banks); a P row is 256 bytes (16 chunks of 4 floats),
- * chunk c of row r at slot c ^ (r % 16). */
+ *   K  A operand of S^T, staged as [key][dim] halves (8 consecutive dims of
+ *      one key, one 16-byte LDS read), streamed by LDS DMA from the halves
+ *      kh/kl the qkv epilogue wrote;
+ *   Q  B operand of S^T, from global (8 consecutive dims of the lane's row);
+ *   S^T, P^T  D tiles of 16 keys: lane 16g + row holds keys 4g..4g+3;
+ *   V  A operand of O^T, staged as [dim][key] halves (8 consecutive keys of
+ *      one dim), from the transposed halves vth/vtl;
+ *   P^T  B operand of O^T (8 consecutive keys of the lane's row), made from
+ *      two D tiles by a 32-lane and a 16-lane swap (pt_operand).
+ * Staged K/V rows are 128 bytes (8 chunks of 8 halves), chunk c of row r at
+ * slot c ^ (r / 2 % 8), so the 16 rows of an operand read fall on distinct
+ * banks.  Each half stages its key blocks in a two-stage ring (the next
+ * block's loads in flight during the products of the current one). */
 __device__ __forceinline__ int kv_at(int row, int chunk) { return row * 64 + 8 * (chunk ^ ((row >> 1) & 7)); }
-__device__ __forceinline__ int p_at(int row, int chunk) { return row * 64 + 4 * (chunk ^ (row & 15)); }
+
+/* max / sum over the four 16-lane rows of a wave (lanes l, l^16, l^32,
+ * l^48), the same value in every lane */
+__device__ __forceinline__ float xrow_max(float v)
+{
+    const auto s1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(s1[0]), __uint_as_float(s1[1]));
+    const auto s2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(s2[0]), __uint_as_float(s2[1]));
+}
+__device__ __forceinline__ float xrow_sum(float v)
+{
+    const auto s1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(s1[0]) + __uint_as_float(s1[1]);
+    const auto s2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(s2[0]) + __uint_as_float(s2[1]);
+}
+
+
+/* The B operand P^T of a 32-key chunk (lane 16G + row: keys 8G..8G+7 of the
+ * chunk, as hi and lo halves) from its two D tiles d0 (keys 0..15) and d1
+ * (16..31), where lane 16g + row holds keys 4g..4g+3 of its tile.  Row
+ * groups [a0 a1 a2 a3] of d0 and [b0 b1 b2 b3] of d1 become [a0 a1 b0 b1]
+ * and [a2 a3 b2 b3] (32-lane swap), then [a0 a2 b0 b2] and [a1 a3 b1 b3]
+ * (16-lane swap): keys 8G..8G+3 and 8G+4..8G+7. */
+__device__ __forceinline__ void pt_operand(const f32x4 &d0, const f32x4 &d1, f16x8 &ph, f16x8 &pl)
+{
+    unsigned h[2][2], l[2][2]; /* [tile][key pair] */
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        h[0][q] = pk16(hi16(d0[2 * q]), hi16(d0[2 * q + 1]));
+        l[0][q] = pk16(lo16(d0[2 * q]), lo16(d0[2 * q + 1]));
+        h[1][q] = pk16(hi16(d1[2 * q]), hi16(d1[2 * q + 1]));
+        l[1][q] = pk16(lo16(d1[2 * q]), lo16(d1[2 * q + 1]));
+    }
+    u32x4 oh, ol;
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const auto a = __builtin_amdgcn_permlane32_swap(h[0][q], h[1][q], false, false);
+        const auto b = __builtin_amdgcn_permlane16_swap(a[0], a[1], false, false);
+        oh[q] = b[0];
+        oh[2 + q] = b[1];
+        const auto c = __builtin_amdgcn_permlane32_swap(l[0][q], l[1][q], false, false);
+        const auto d = __builtin_amdgcn_permlane16_swap(c[0], c[1], false, false);
+        ol[q] = d[0];
+        ol[2 + q] = d[1];
+    }
+    ph = __builtin_bit_cast(f16x8, oh);
+    pl = __builtin_bit_cast(f16x8, ol);
+}
 
 extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_attnp_args a)
 {
     constexpr int TILE = 64 * 64; /* halves per staged array */
-    /* per half hs: Kh, Kl, Vh, Vl at (4 hs + 0..3) * TILE */
-    __shared__ __attribute__((aligned(16))) _Float16 kvs[8 * TILE];
-    __shared__ __attribute__((aligned(16))) float Ps[8][16 * 64];
+    constexpr int TB = 2 * TILE;  /* its bytes */
+    /* stage b of half hs: Kh, Kl, Vh, Vl at (4 (2 hs + b) + 0..3) * TILE */
+    __shared__ __attribute__((aligned(1024))) _Float16 kvs[16 * TILE];
     const int h = blockIdx.x, qb = blockIdx.y, tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
     const int rg = wave & 3, hs = wave >> 2;
@@ -1477,11 +1552,12 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
     /* scores in base-2 units (scaled by log2 e): the softmax's
      * exponentials are single v_exp_f32 instructions */
     const float scale2 = a.scale * 1.4426950408889634f;
-    const int E = a.E, P = a.P;
+    const int E = a.E, P = a.P, S = a.S;
+    /* this lane's query row */
+    const int i = qb * 64 + 16 * rg + lr;
     f16x8 qh[2], ql[2];
     {
-        const int i = min(qb * 64 + 16 * rg + lr, P - 1);
-        const float *qp = a.q + (size_t)i * E + h * 64 + 8 * lg;
+        const float *qp = a.q + (size_t)min(i, P - 1) * E + h * 64 + 8 * lg;
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
             const f32x4 x0 = *(const f32x4 *)(qp + 32 * s2), x1 = *(const f32x4 *)(qp + 32 * s2 + 4);
@@ -1492,182 +1568,166 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
             }
         }
     }
-    f32x4 o[4];
+    f32x4 o[4]; /* O^T: tile t = dims 16t..16t+15, lane 16g + row holds dims 16t + 4g..+3 */
 #pragma unroll
     for (int t = 0; t < 4; ++t) o[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    float m[4], l[4];
+    float m = -INFINITY, l = 0.f;
+    /* Staging of key block kb into stage b by LDS DMA (global_load_lds_
+     * dwordx4: lane l of an instruction writes 16 bytes at LDS base + 16 l),
+     * from the halves the qkv epilogue wrote, with no conversion: wave w4 of
+     * the half fills rows 16 w4..16 w4 + 15 of each array with two
+     * instructions of 8 rows (lane -> row l/8, slot l%8, holding the chunk
+     * that the swizzle puts there).  K rows are keys (8 dims per chunk, from
+     * kh/kl [position][E]), V rows are dims (8 keys per chunk, from vth/vtl
+     * [E][S]); every address is inside the arrays (positions j0 + 63 <= 1023
+     * < S, dims < E). */
+    const int w4 = wave & 3;
+    typedef __attribute__((address_space(3))) void lds_t;
+    auto stage = [&](int kb, int b) {
+        const int j0 = kb * 64;
+        unsigned char *st = (unsigned char *)(kvs + 4 * (2 * hs + b) * TILE);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) { m[r] = -INFINITY; l[r] = 0.f; }
-    const int i_base = qb * 64 + 16 * rg + 4 * lg;
-    /* staging (per half, 256 threads): K: key sj = t % 64, dims 16 sc..+15;
-     * V: dim sj, keys 16 sc..+15; 4-byte loads, consecutive lanes read
-     * consecutive words */
-    const int st_ = tid & 255, sj = st_ & 63, sc = st_ >> 6;
-    float kx[16], vx[16];
-    auto kvload = [&](int kb) {
-        const int jb = min(kb, qb) * 64;
-        const float *kp = a.k_cache + (size_t)(h * 64 + 16 * sc) * a.S + min(jb + sj, a.S - 1);
-#pragma unroll
-        for (int d = 0; d < 16; ++d) kx[d] = kp[(size_t)d * a.S];
-#pragma unroll
-        for (int k = 0; k < 16; ++k) vx[k] = a.v_cache[(size_t)min(jb + 16 * sc + k, a.S - 1) * E + h * 64 + sj];
-    };
-    kvload(hs);
-    const int nit = (qb + 2) >> 1;
-    _Float16 *Kh = kvs + (4 * hs + 0) * TILE, *Kl = kvs + (4 * hs + 1) * TILE;
-    _Float16 *Vh = kvs + (4 * hs + 2) * TILE, *Vl = kvs + (4 * hs + 3) * TILE;
-    for (int it = 0; it < nit; ++it) {
-        const int kb = 2 * it + hs, j0 = kb * 64;
-        __syncthreads(); /* the previous blocks have been consumed */
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            f16x8 kh, kl, vh, vl;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                kh[e] = hi16(kx[8 * c + e]); kl[e] = lo16(kx[8 * c + e]);
-                vh[e] = hi16(vx[8 * c + e]); vl[e] = lo16(vx[8 * c + e]);
-            }
-            const int at = kv_at(sj, 2 * sc + c);
-            *(f16x8 *)(Kh + at) = kh;
-            *(f16x8 *)(Kl + at) = kl;
-            *(f16x8 *)(Vh + at) = vh;
-            *(f16x8 *)(Vl + at) = vl;
+        for (int e = 0; e < 2; ++e) {
+            const int rw = 16 * w4 + 8 * e + (lane >> 3);
+            const int c = (lane & 7) ^ ((rw >> 1) & 7);
+            const size_t ko = (size_t)(j0 + rw) * E + h * 64 + 8 * c;
+            const size_t vo = (size_t)(h * 64 + rw) * S + j0 + 8 * c;
+            unsigned char *dst = st + (16 * w4 + 8 * e) * 128;
+            __builtin_amdgcn_global_load_lds(a.kh + ko, (lds_t *)dst, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(a.kl + ko, (lds_t *)(dst + TB), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(a.vth + vo, (lds_t *)(dst + 2 * TB), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(a.vtl + vo, (lds_t *)(dst + 3 * TB), 16, 0, 0);
         }
-        __syncthreads();
-        kvload(kb + 2);
-        if (kb > qb) continue; /* wave-uniform */
+    };
+    const int nit = (qb + 2) >> 1;
+    if (hs <= qb) stage(hs, 0); /* wave-uniform */
+    for (int it = 0; it < nit; ++it) {
+        const int kb = 2 * it + hs, j0 = kb * 64, b = it & 1;
+        /* this wave's part of block kb has landed; every wave is past the
+         * products of the block before, which read stage b ^ 1 */
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        if (kb + 2 <= qb) stage(kb + 2, b ^ 1); /* wave-uniform */
+        if (kb > qb) continue;                   /* wave-uniform */
+        const _Float16 *Kh = kvs + 4 * (2 * hs + b) * TILE, *Kl = Kh + TILE;
+        const _Float16 *Vh = Kh + 2 * TILE, *Vl = Kh + 3 * TILE;
+        /* S^T tiles: keys j0 + 16t + 4lg + r of row i */
         f32x4 sacc[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) sacc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
         {
-            f16x8 bh[4][2], bl[4][2];
+            f16x8 kh[4][2], kl[4][2];
 #pragma unroll
             for (int t = 0; t < 4; ++t)
 #pragma unroll
                 for (int s2 = 0; s2 < 2; ++s2) {
                     const int at = kv_at(16 * t + lr, 4 * s2 + lg);
-                    bh[t][s2] = *(const f16x8 *)(Kh + at);
-                    bl[t][s2] = *(const f16x8 *)(Kl + at);
+                    kh[t][s2] = *(const f16x8 *)(Kh + at);
+                    kl[t][s2] = *(const f16x8 *)(Kl + at);
                 }
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[s2], bh[t][s2], sacc[t], 0, 0, 0);
-                    sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[s2], bl[t][s2], sacc[t], 0, 0, 0);
+                    sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[t][s2], ql[s2], sacc[t], 0, 0, 0);
+                    sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl[t][s2], qh[s2], sacc[t], 0, 0, 0);
                 }
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
-                    sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[s2], bh[t][s2], sacc[t], 0, 0, 0);
+                    sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[t][s2], qh[s2], sacc[t], 0, 0, 0);
         }
-        float alpha[4];
+        float bm = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int i = i_base + r;
-            float bm = -INFINITY;
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const int j = j0 + 16 * t + lr;
+            for (int r = 0; r < 4; ++r) {
+                const int j = j0 + 16 * t + 4 * lg + r;
                 const float v = (i < P && j <= i) ? sacc[t][r] * scale2 : -INFINITY;
                 sacc[t][r] = v;
                 bm = fmaxf(bm, v);
             }
-            bm = row16_max(bm);
-            const float mn = fmaxf(m[r], bm);
-            const float ms = mn == -INFINITY ? 0.f : mn;
-            alpha[r] = __builtin_amdgcn_exp2f(m[r] - ms);
-            float ps = 0.f;
+        bm = xrow_max(bm);
+        const float mn = fmaxf(m, bm);
+        const float ms = mn == -INFINITY ? 0.f : mn;
+        const float alpha = __builtin_amdgcn_exp2f(m - ms);
+        float ps = 0.f;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
                 const float pv = __builtin_amdgcn_exp2f(sacc[t][r] - ms);
                 sacc[t][r] = pv;
                 ps += pv;
             }
-            l[r] = fmaf(l[r], alpha[r], row16_sum(ps));
-            m[r] = mn;
-        }
-        float *pw = Ps[wave];
+        l = fmaf(l, alpha, xrow_sum(ps));
+        m = mn;
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) pw[p_at(4 * lg + r, 4 * t + (lr >> 2)) + (lr & 3)] = sacc[t][r];
-        __builtin_amdgcn_wave_barrier();
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) o[t][r] *= alpha[r];
+            for (int r = 0; r < 4; ++r) o[t][r] *= alpha;
         f16x8 ph[2], pl[2];
 #pragma unroll
-        for (int s2 = 0; s2 < 2; ++s2) {
-            const f32x4 x0 = *(const f32x4 *)(pw + p_at(lr, 8 * s2 + 2 * lg));
-            const f32x4 x1 = *(const f32x4 *)(pw + p_at(lr, 8 * s2 + 2 * lg + 1));
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                ph[s2][e] = hi16(x0[e]); pl[s2][e] = lo16(x0[e]);
-                ph[s2][4 + e] = hi16(x1[e]); pl[s2][4 + e] = lo16(x1[e]);
-            }
-        }
+        for (int s2 = 0; s2 < 2; ++s2) pt_operand(sacc[2 * s2], sacc[2 * s2 + 1], ph[s2], pl[s2]);
         {
-            f16x8 bh[4][2], bl[4][2];
+            f16x8 vh[4][2], vl[4][2];
 #pragma unroll
             for (int t = 0; t < 4; ++t)
 #pragma unroll
                 for (int s2 = 0; s2 < 2; ++s2) {
                     const int at = kv_at(16 * t + lr, 4 * s2 + lg);
-                    bh[t][s2] = *(const f16x8 *)(Vh + at);
-                    bl[t][s2] = *(const f16x8 *)(Vl + at);
+                    vh[t][s2] = *(const f16x8 *)(Vh + at);
+                    vl[t][s2] = *(const f16x8 *)(Vl + at);
                 }
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl[s2], bh[t][s2], o[t], 0, 0, 0);
-                    o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s2], bl[t][s2], o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[t][s2], pl[s2], o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vl[t][s2], ph[s2], o[t], 0, 0, 0);
                 }
 #pragma unroll
             for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
-                    o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph[s2], bh[t][s2], o[t], 0, 0, 0);
+                    o[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vh[t][s2], ph[s2], o[t], 0, 0, 0);
         }
     }
     __syncthreads();
     /* odd stride: the 64 lanes of a word access fall on distinct banks */
-    float *xw = (float *)kvs + (size_t)(rg * 64 + lane) * 25;
+    float *xw = (float *)kvs + (size_t)(rg * 64 + lane) * 19;
     if (hs == 1) {
+        xw[0] = m;
+        xw[1] = l;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            xw[r] = m[r];
-            xw[4 + r] = l[r];
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int t = 0; t < 4; ++t) xw[8 + 4 * t + r] = o[t][r];
-        }
+            for (int r = 0; r < 4; ++r) xw[2 + 4 * t + r] = o[t][r];
     }
     __syncthreads();
-    if (hs == 1) return;
+    if (hs == 1 || i >= P) return;
+    const float m1 = xw[0], l1 = xw[1];
+    const float mx = fmaxf(m, m1);
+    const float f0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mx);
+    const float f1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mx);
+    const float inv = 1.0f / (l * f0 + l1 * f1);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const float m1 = xw[r], l1 = xw[4 + r];
-        const float mx = fmaxf(m[r], m1);
-        const float f0 = m[r] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[r] - mx);
-        const float f1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mx);
-        l[r] = l[r] * f0 + l1 * f1;
+    for (int t = 0; t < 4; ++t) {
+        f32x4 y;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) o[t][r] = o[t][r] * f0 + xw[8 + 4 * t + r] * f1;
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int i = i_base + r;
-        if (i >= P) continue;
-        const float inv = 1.0f / l[r];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const size_t idx = (size_t)i * E + h * 64 + 16 * t + lr;
-            if (a.out_hi) split_store(a.out_hi, a.out_lo, idx, o[t][r] * inv);
-            else a.out[idx] = o[t][r] * inv;
+        for (int r = 0; r < 4; ++r) y[r] = (o[t][r] * f0 + xw[2 + 4 * t + r] * f1) * inv;
+        const size_t idx = (size_t)i * E + h * 64 + 16 * t + 4 * lg;
+        if (a.out_hi) {
+            /* the four dims as one 8-byte store per half */
+            uint2 hv, lv;
+            hv.x = pk16(hi16(y[0]), hi16(y[1]));
+            hv.y = pk16(hi16(y[2]), hi16(y[3]));
+            lv.x = pk16(lo16(y[0]), lo16(y[1]));
+            lv.y = pk16(lo16(y[2]), lo16(y[3]));
+            *(uint2 *)(a.out_hi + idx) = hv;
+            *(uint2 *)(a.out_lo + idx) = lv;
+        } else {
+            *(f32x4 *)(a.out + idx) = y;
         }
     }
 }

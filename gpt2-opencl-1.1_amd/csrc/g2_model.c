@@ -47,6 +47,7 @@ struct g2_model {
     float *hidden, *ln_out, *attn, *attn_proj, *ffn1, *ffn2, *qkv_new, *qkv_full;
     float *last_hidden, *logits, *partial, *scores, *q;
     float *pf_part; /* split-K slices of the fp16 prefill GEMM */
+    uint16_t *pf_kv; /* the prompt's K and V as fp16 halves: kh, kl [S][E], vth, vtl [E][S] */
     int *ids_dev;
     /* fused path */
     int *state;
@@ -230,6 +231,12 @@ static int alloc_workspaces(g2_model *m)
     A(m->logits, V * 4); A(m->ids_dev, S * 4); A(m->partial, 8 * V * 4);
     if (m->path == G2_PATH_FUSED && m->dtype == G2_F16) A(m->pf_part, (size_t)G2_PF_MAXSPLIT * S * E * 4);
     if (m->path == G2_PATH_FUSED && m->dtype == G2_F32) A(m->pf_part, (size_t)G2_SG_PART_FLOATS * 4);
+    if (m->path == G2_PATH_FUSED) {
+        /* zeroed once: entries past a prompt are finite (zero or an earlier
+         * prompt's), so the masked keys of a block contribute 0 x finite */
+        A(m->pf_kv, 4 * S * E * 2);
+        if (!rc) rc = g2i_hip(hipMemsetAsync(m->pf_kv, 0, 4 * S * E * 2, g2i_stream()), "kv halves clear");
+    }
     A(m->scores, NH * S * 4); A(m->q, S * E * 4);
     A(m->state, G2S_WORDS * 4);
     A(m->att_part, NH * G2_ATTN_MAX_CHUNKS * 66 * 4);
@@ -282,7 +289,8 @@ int g2_model_free(g2_model *m)
     void *bufs[] = { m->wte, m->wpe, m->lnf_w, m->lnf_b, m->lm_head, m->hidden, m->ln_out,
                      m->attn, m->attn_proj, m->ffn1, m->ffn2, m->qkv_new, m->qkv_full,
                      m->last_hidden, m->logits, m->partial, m->scores, m->q, m->ids_dev,
-                     m->state, m->att_part, m->am_part, m->step_layers, m->xbuf, m->trace, m->pf_part };
+                     m->state, m->att_part, m->am_part, m->step_layers, m->xbuf, m->trace, m->pf_part,
+                     m->pf_kv };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; ++i)
         if (bufs[i]) hipFree(bufs[i]);
     for (int l = 0; l < m->cfg.n_layer; ++l) {
@@ -902,7 +910,7 @@ static int prefill_sgemm(g2_model *m, int epi, g2_gemm_args *g)
     g->part = m->pf_part;
     int rc = g2i_launch3(G2F_SGEMM_PARTIAL, gx, gy, (unsigned)ks, 256, g);
     g2_skepi_args e = { m->pf_part, g->bias, g->C, g->q_out, g->k_cache, g->v_cache, g->M, g->N, ks, epi,
-                        g->E, g->S, g->pos0 };
+                        g->E, g->S, g->pos0, g->kh, g->kl, g->vth, g->vtl };
     const unsigned n4 = cdivu((unsigned)(g->M * g->N / 4), 256);
     if (!rc) rc = g2i_launch(G2F_SPLITK_EPI, n4 < 2048 ? n4 : 2048, 1, 256, &e);
     return rc;
@@ -934,6 +942,9 @@ static int fused_prefill(g2_model *m, int P)
     uint16_t *ln_h = (uint16_t *)m->ln_out, *ln_l = ln_h + cap * E;
     uint16_t *at_h = (uint16_t *)m->attn, *at_l = at_h + cap * E;
     uint16_t *ff_h = (uint16_t *)m->ffn1, *ff_l = ff_h + cap * F;
+    /* the layer's K and V as fp16 halves, written by the qkv epilogue for
+     * the prompt attention: kh, kl [cap][E], vth, vtl [E][cap] */
+    uint16_t *kv_kh = m->pf_kv, *kv_kl = kv_kh + cap * E, *kv_vh = kv_kl + cap * E, *kv_vl = kv_vh + cap * E;
     g2_embed_args e = { m->wte, m->wpe, m->hidden, m->ids_dev, NULL, E, P, 0 };
     int rc = g2i_launch(f16 ? G2F_EMBED_F16 : G2F_EMBED_F32, cdivu(E, 256), (unsigned)P, 256, &e);
     int ln1_done = 0; /* the previous layer's fc2 sum already wrote this layer's ln_1 */
@@ -950,11 +961,12 @@ static int fused_prefill(g2_model *m, int P)
         g.A = m->ln_out; g.Ah = ln_h; g.Al = ln_l; g.B = y->qkv_w; g.bias = y->qkv_b; g.q_out = m->q;
         g.k_cache = y->k_cache; g.v_cache = y->v_cache; g.M = P; g.N = 3 * E; g.K = E;
         g.E = E; g.S = G2_KV_MAX_SEQ; g.pos0 = 0;
+        g.kh = kv_kh; g.kl = kv_kl; g.vth = kv_vh; g.vtl = kv_vl;
         if (!rc) rc = big ? g2i_launch(f_qkv, 8 * cdivu(cdivu(3 * E, 128), 8) * cdivu(P, 128), 1, 1024, &g)
                       : sg  ? prefill_sgemm(m, G2_SG_QKV, &g)
                             : g2i_launch(f_qkv, cdivu(3 * E, 64), cdivu(P, 64), 256, &g);
         g2_attnp_args t = { m->q, y->k_cache, y->v_cache, m->attn, P, E, NH, G2_KV_MAX_SEQ, 1.0f / sqrtf(64.0f),
-                            big ? at_h : NULL, big ? at_l : NULL };
+                            big ? at_h : NULL, big ? at_l : NULL, kv_kh, kv_kl, kv_vh, kv_vl };
         if (!rc) rc = g2i_launch(attn32 ? G2F_ATTN_PREFILL_MFMA : G2F_ATTN_PREFILL_H16, (unsigned)NH, cdivu(P, 64), 512, &t);
         memset(&g, 0, sizeof g);
         g.A = m->attn; g.B = y->proj_w; g.bias = y->proj_b; g.C = m->hidden; g.M = P; g.N = E; g.K = E;
