@@ -80,6 +80,7 @@ typedef struct {
     uint16_t *hi, *lo;
 } g2_skred_args;
 #define G2_SKLN_MAXN 2048
+#define G2_SKLN_MAXKS 5 /* slices g2k_splitk_resid_ln reads (ks <= this) */
 
 /* The split-K epilogue of the fp32-weight prefill GEMM (g2k_splitk_epi):
  * v[m,n] = (sum over z < ks in order of part[z][m][n]) + bias[n], then epi

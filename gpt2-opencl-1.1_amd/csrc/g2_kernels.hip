@@ -1182,7 +1182,7 @@ G2K void g2k_splitk_resid_ln(const g2_skred_args a)
      * first sum (unconditional, clamped into the row), so the row costs
      * one memory latency instead of one per group */
     constexpr int PG = G2_SKLN_MAXN / 1024; /* groups per thread */
-    constexpr int ZMAX = 8;                  /* slices read at once (ks <= ZMAX) */
+    constexpr int ZMAX = G2_SKLN_MAXKS;      /* slices read at once (ks <= ZMAX) */
     __shared__ float red4[4];
     const int m = blockIdx.x, N = a.N, NG = N >> 2;
     if (m >= a.M) return;
@@ -1235,9 +1235,17 @@ G2K void g2k_splitk_resid_ln(const g2_skred_args a)
     for (int k = 0; k < PG; ++k) {
         const int g = (int)threadIdx.x + 256 * k;
         if (g < NG) {
+            /* the group's four outputs as one 8-byte store per half */
+            float y[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                split_store(a.hi, a.lo, row + 4 * g + e, fmaf((xv[k][e] - mean) * inv, gv[k][e], ev[k][e]));
+            for (int e = 0; e < 4; ++e) y[e] = fmaf((xv[k][e] - mean) * inv, gv[k][e], ev[k][e]);
+            uint2 hv, lv;
+            hv.x = pk16(hi16(y[0]), hi16(y[1]));
+            hv.y = pk16(hi16(y[2]), hi16(y[3]));
+            lv.x = pk16(lo16(y[0]), lo16(y[1]));
+            lv.y = pk16(lo16(y[2]), lo16(y[3]));
+            *(uint2 *)(a.hi + row + 4 * g) = hv;
+            *(uint2 *)(a.lo + row + 4 * g) = lv;
         }
     }
 }

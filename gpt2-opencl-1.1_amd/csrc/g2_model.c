@@ -876,7 +876,7 @@ static int prefill_resid(g2_model *m, const float *A, const uint16_t *Ah, const 
     g.part = m->pf_part; g.ksplit = ks;
     int rc = g2i_launch3(big ? G2F_HGEMM2_PARTIAL : G2F_HGEMM_PARTIAL, bx, by, (unsigned)ks, big ? 1024 : 256, &g);
     g2_skred_args r = { m->pf_part, bias, C, P, N, ks, ln_g, ln_b, hi, lo };
-    if (!rc && ln_g && big && N <= G2_SKLN_MAXN && N % 4 == 0 && ks <= 8) {
+    if (!rc && ln_g && big && N <= G2_SKLN_MAXN && N % 4 == 0 && ks <= G2_SKLN_MAXKS) {
         *ln_done = 1;
         return g2i_launch(G2F_SPLITK_RESID_LN, (unsigned)P, 1, 256, &r);
     }
