@@ -275,13 +275,15 @@ typedef struct {
 #define G2X_DECISION 1      /* header word: a plain launch's residency verdict */
 /* Word offsets inside one layer region (E = n_embd, NH heads, F = ffn):
  * QKV outputs [3E], attention chunk partials [NH][G2_STEP_MAXCH][66],
- * merged attention O [E], X1 = x + proj [E], H = gelu(fc) [F],
- * X2 = X1 + fc2 [E]; regions are padded to 32 words. */
+ * merged attention O [E], X1 = x + proj [E], H = gelu(fc) [F, padded to an
+ * even count], X2 = X1 + fc2 [E]; regions are padded to 32 words.  Every
+ * vector starts at an even word (E is a multiple of 64), so the step
+ * kernel reads them as 16-byte word pairs. */
 #define G2X_ATT(E) (3 * (E))
 #define G2X_O(E, NH) (3 * (E) + (NH) * G2_STEP_MAXCH * 66)
 #define G2X_X1(E, NH) (G2X_O(E, NH) + (E))
 #define G2X_H(E, NH) (G2X_X1(E, NH) + (E))
-#define G2X_X2(E, NH, F) (G2X_H(E, NH) + (F))
+#define G2X_X2(E, NH, F) (G2X_H(E, NH) + (((F) + 1) & ~1))
 #define G2X_LAYER_WORDS(E, NH, F) ((G2X_X2(E, NH, F) + (E) + 31) & ~31)
 /* Total words: header, L layer regions, 2 argmax words per work-group, 32
  * spare words, 1 arrival word per work-group. */

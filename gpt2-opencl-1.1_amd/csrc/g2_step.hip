@@ -59,6 +59,7 @@ constexpr int UMAX = 4;                                 /* units per wave, main 
 constexpr int UPROJ = 1;                                /* units per wave, proj set */
 constexpr int SEGC = 256;                               /* chunks per unit: 64 lanes x 4 */
 constexpr int PMAX = (G2_STEP_MAXF + NT - 1) / NT;      /* exchange words per thread */
+constexpr int PMAX2 = (G2_STEP_MAXF + 2 * NT - 1) / (2 * NT); /* word pairs per thread */
 constexpr unsigned long long WAIT_LIMIT = 10000000ull;  /* 100 ms of the 100 MHz clock */
 constexpr unsigned long long ABORT_CHECK_AFTER = 200000ull; /* 2 ms */
 
@@ -223,11 +224,9 @@ __device__ __forceinline__ void settle(const ctx &c, const u64 *src, u64 (&v)[NP
  * with the weight stream), so a work-group that found stale words waits on
  * nsent sentinel words only (word n*k/nsent for k < nsent: the first word
  * of each producer when n is split evenly over nsent producers), then
- * re-reads just its stale words.  SENT selects the sentinel scheme for
- * every size (for a kernel whose polling must leave the memory queue to a
- * weight stream).  Ends with a barrier; `flag` is an LDS word of the
- * caller. */
-template <int NP, typename BAR = wg_bar, bool SENT = false>
+ * re-reads just its stale words.  Ends with a barrier; `flag` is an LDS
+ * word of the caller. */
+template <int NP, typename BAR = wg_bar>
 __device__ __forceinline__ void fetch(int tid, const ctx &c, const u64 *src, int n, int nsent,
                                       float *dst, lds_flag *flag, BAR bar = BAR())
 {
@@ -238,7 +237,7 @@ __device__ __forceinline__ void fetch(int tid, const ctx &c, const u64 *src, int
         const int w = tid + NT * i;
         v[i] = w < n ? ll_get(src + w) : filler;
     }
-    if constexpr (NP <= 4 && !SENT) {
+    if constexpr (NP <= 4) {
         (void)nsent;
         (void)flag;
         settle(c, src, v, [&](int i) { const int w = tid + NT * i; return w < n ? w : -1; });
@@ -270,6 +269,100 @@ __device__ __forceinline__ void fetch(int tid, const ctx &c, const u64 *src, int
     for (int i = 0; i < NP; ++i) {
         const int w = tid + NT * i;
         if (w < n) dst[w] = ll_val(v[i]);
+    }
+    bar();
+}
+
+/* Two tagged words src[w], src[w + 1] (w even) with one 16-byte load, with
+ * the cache policy of ll_get (sc1: read at the coherence point, as the
+ * relaxed agent-scope loads are), through a buffer resource over the
+ * vector; each 8-byte word of the pair is read whole.  The low halves (.x,
+ * .z) are the values, the high halves (.y, .w) the tags.  The pair loads
+ * halve the requests of a vector fetch, which a wave issues at a bounded
+ * rate (the 6400-word H vector is read by every work-group). */
+__device__ __forceinline__ u32x4 ll_get2(__amdgpu_buffer_rsrc_t r, int w)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, w * 8, 0, 16 /* sc1 */);
+}
+__device__ __forceinline__ bool pair_stale(const u32x4 &v, unsigned tag) { return v.y != tag || v.w != tag; }
+
+/* settle (above) for word pairs: pair i starts at word idx(i) (< 0: an
+ * unused slot, which holds a current filler) */
+template <int NP2, typename IDX>
+__device__ __forceinline__ void settle2(const ctx &c, __amdgpu_buffer_rsrc_t r, u32x4 (&v)[NP2], IDX idx)
+{
+    unsigned bad = 0;
+#pragma unroll
+    for (int i = 0; i < NP2; ++i) bad |= (unsigned)pair_stale(v[i], c.tag);
+    if (!bad || *c.dead) return;
+    const u64 t0 = wall_clock64();
+    for (;;) {
+        __builtin_amdgcn_s_sleep(4);
+#pragma unroll
+        for (int i = 0; i < NP2; ++i) {
+            const int w = idx(i);
+            if (w >= 0 && pair_stale(v[i], c.tag)) v[i] = ll_get2(r, w);
+        }
+        bad = 0;
+#pragma unroll
+        for (int i = 0; i < NP2; ++i) bad |= (unsigned)pair_stale(v[i], c.tag);
+        if (!bad || *c.dead) return;
+        /* the abort word is consulted only by waits that already took long */
+        const u64 el = wall_clock64() - t0;
+        if (el > ABORT_CHECK_AFTER) {
+            if (ll_tag(ll_get(c.abort_w)) == c.tag) { *c.dead = 1; return; }
+            if (el > WAIT_LIMIT) { give_up(c); return; }
+        }
+    }
+}
+
+/* fetch (above) by 16-byte word pairs, for a vector of an even number of
+ * words n that starts at an even word (every vector of the exchange area:
+ * n_embd is a multiple of 64 and the step kernel admits only ffn widths
+ * that are multiples of the weight chunk): thread tid takes pairs tid +
+ * NT*i (words 2p, 2p + 1). */
+template <int NP2, typename BAR = wg_bar>
+__device__ __forceinline__ void fetch2(int tid, const ctx &c, const u64 *src, int n, int nsent, float *dst,
+                                       lds_flag *flag, BAR bar = BAR())
+{
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, n * 8, 0x00020000);
+    const u32x4 filler = (u32x4){0u, c.tag, 0u, c.tag};
+    u32x4 v[NP2];
+#pragma unroll
+    for (int i = 0; i < NP2; ++i) {
+        const int w = 2 * (tid + NT * i);
+        v[i] = w < n ? ll_get2(r, w) : filler;
+    }
+    auto idx = [&](int i) { const int w = 2 * (tid + NT * i); return w < n ? w : -1; };
+    if constexpr (NP2 <= 2) {
+        (void)nsent;
+        (void)flag;
+        settle2(c, r, v, idx);
+    } else {
+        if (tid == 0) *flag = 0;
+        bar();
+        unsigned bad = 0;
+#pragma unroll
+        for (int i = 0; i < NP2; ++i) bad |= (unsigned)pair_stale(v[i], c.tag);
+        if (bad) *flag = 1;
+        bar();
+        if (*flag && !*c.dead) {
+            if (tid < nsent) {
+                const int w = (int)(((long)n * tid) / nsent);
+                u64 sv[1] = {ll_get(src + w)};
+                settle(c, src, sv, [&](int) { return w; });
+            }
+            bar();
+            settle2(c, r, v, idx);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NP2; ++i) {
+        const int w = 2 * (tid + NT * i);
+        if (w < n) {
+            dst[w] = __uint_as_float(v[i].x);
+            dst[w + 1] = __uint_as_float(v[i].z);
+        }
     }
     bar();
 }
@@ -823,6 +916,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     __shared__ volatile int flag;
 
     constexpr int NPE = (G2_STEP_MAXE + NT - 1) / NT;              /* words of an E vector */
+    constexpr int NPE2 = (G2_STEP_MAXE + 2 * NT - 1) / (2 * NT);   /* its word pairs       */
     constexpr int NPM = (G2_STEP_MAXCH * 66 + NT - 1) / NT;        /* a head's partials    */
     const int wg = blockIdx.x, nwg = gridDim.x;
     const int E = a.E, F = a.F, NH = a.NH, S = a.S, V = a.V;
@@ -882,7 +976,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             const ln_params<NPE> lp = ln_load<NPE>(tid, gl(y.ln1_w), gl(y.ln1_b), E);
             const float bias = gl(y.qkv_b)[min(p.r0 + tid, 3 * E - 1)]; /* used by tid < nrows */
             if (l > 0) {
-                fetch<NPE>(tid, c, X + (size_t)(l - 1) * a.xlayer + G2X_X2(E, NH, F), E, nwg, xres, (lds_flag *)&flag);
+                fetch2<NPE2>(tid, c, X + (size_t)(l - 1) * a.xlayer + G2X_X2(E, NH, F), E, nwg, xres, (lds_flag *)&flag);
             }
             TRACE(1);
             layernorm(tid, xres, xin, lp, E, red);
@@ -963,7 +1057,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             const int tid = fresh_tid();
             const plan p = make_plan(y.proj_w, sh.proj);
             const float bias = gl(y.proj_b)[min(p.r0 + tid, E - 1)];
-            fetch<NPE>(tid, c, R + G2X_O(E, NH), E, NH, xin, (lds_flag *)&flag);
+            fetch2<NPE2>(tid, c, R + G2X_O(E, NH), E, NH, xin, (lds_flag *)&flag);
             TRACE(5);
             matvec<WT, UPROJ>(tid, wp, p, xin, part);
             if (tid < p.nrows) {
@@ -983,7 +1077,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             const plan p = make_plan(y.fc_w, sh.fc);
             const ln_params<NPE> lp = ln_load<NPE>(tid, gl(y.ln2_w), gl(y.ln2_b), E);
             const float bias = gl(y.fc_b)[min(p.r0 + tid, F - 1)];
-            fetch<NPE>(tid, c, R + G2X_X1(E, NH), E, nwg - NH, xres, (lds_flag *)&flag);
+            fetch2<NPE2>(tid, c, R + G2X_X1(E, NH), E, nwg - NH, xres, (lds_flag *)&flag);
             TRACE(7);
             layernorm(tid, xres, xin, lp, E, red);
             TRACE(13);
@@ -1005,7 +1099,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             const int tid = fresh_tid();
             const plan p = make_plan(y.fc2_w, sh.fc2);
             const float bias = gl(y.fc2_b)[min(p.r0 + tid, E - 1)];
-            fetch<PMAX>(tid, c, R + G2X_H(E, NH), F, nwg, xin, (lds_flag *)&flag);
+            fetch2<PMAX2>(tid, c, R + G2X_H(E, NH), F, nwg, xin, (lds_flag *)&flag);
             TRACE(9);
             matvec<WT, UMAX>(tid, wa, p, xin, part);
             TRACE(15);

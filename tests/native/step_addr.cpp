@@ -124,6 +124,13 @@ int main(int argc, char **argv)
         printf("refused: %s\n", why);
         return 3;
     }
+    /* a vector fetch by 16-byte word pairs: pairs [base + 2p, base + 2p + 2)
+     * for 2p < n, inside [.., end); the vector must start at an even word
+     * and have an even length */
+    auto pairs = [&](const char *what, long base, int n, long end) {
+        if ((base & 1) || (n & 1)) chk("vector of word pairs", 0, 1, 0);
+        for (int w = 0; w < n; w += 2) chk(what, base + w, base + w + 2, end);
+    };
     long proj_rows = 0; /* rows of proj over all work-groups and layers */
     for (long wg = 0; wg < nwg; ++wg) {
         /* embedding of the token at pos, LayerNorm parameters */
@@ -149,8 +156,7 @@ int main(int argc, char **argv)
                 if (r >= 2 * E) chk("V cache store", (long)pos * E + (r - 2 * E), (long)pos * E + (r - 2 * E) + 1, (long)S * E);
                 else if (r >= E) chk("K cache store", (long)(r - E) * S + pos, (long)(r - E) * S + pos + 1, (long)E * S);
             }
-            if (l > 0)
-                for (int w = 0; w < E; ++w) chk("X2 word", R - xlayer + G2X_X2(E, NH, F) + w, R - xlayer + G2X_X2(E, NH, F) + w + 1, R);
+            if (l > 0) pairs("X2 fetch", R - xlayer + G2X_X2(E, NH, F), E, R);
             /* ATTN units */
             const int nunits = NH * nch, rounds = (nunits + 2 * nwg - 1) / (2 * nwg);
             for (int rd = 0; rd < rounds; ++rd)
@@ -183,13 +189,16 @@ int main(int argc, char **argv)
             /* proj: the work-groups merging no head */
             if (wg >= NH) {
                 matrix("proj weights", "b", E, E, VE, 1, wg - NH, nwg - NH);
+                pairs("O fetch", R + G2X_O(E, NH), E, R + G2X_X1(E, NH));
                 const g2p_rows pp = g2p_proj_plan(E, VE, NH, wg, nwg);
                 chk("X1 words", R + G2X_X1(E, NH) + pp.r0, R + G2X_X1(E, NH) + pp.r0 + pp.nrows, R + G2X_H(E, NH));
                 proj_rows += pp.nrows;
             }
+            pairs("X1 fetch", R + G2X_X1(E, NH), E, R + G2X_H(E, NH));
             matrix("fc weights", "b", F, E, VE, 4, wg, nwg);
             const g2p_rows pf = g2p_rows_plan(F, E, VE, wg, nwg);
             chk("H words", R + G2X_H(E, NH) + pf.r0, R + G2X_H(E, NH) + pf.r0 + pf.nrows, R + G2X_X2(E, NH, F));
+            pairs("H fetch", R + G2X_H(E, NH), F, R + G2X_X2(E, NH, F));
             matrix("fc2 weights", "b", E, F, VE, 4, wg, nwg);
             const g2p_rows p2 = g2p_rows_plan(E, F, VE, wg, nwg);
             chk("X2 words", R + G2X_X2(E, NH, F) + p2.r0, R + G2X_X2(E, NH, F) + p2.r0 + p2.nrows, R + xlayer);
