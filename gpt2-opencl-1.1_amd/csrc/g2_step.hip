@@ -96,21 +96,6 @@ __device__ __forceinline__ u64 ll_get(const u64 *p)
 __device__ __forceinline__ unsigned ll_tag(u64 w) { return (unsigned)(w >> 32); }
 __device__ __forceinline__ float ll_val(u64 w) { return __uint_as_float((unsigned)w); }
 
-/* A word for readers on the same XCD only: a plain 64-bit store, which
- * lands in this XCD's L2, where their agent-scope loads find it (readers on
- * other XCDs would not see it before the kernel ends). */
-__device__ __forceinline__ void lx_put(u64 *p, float v, unsigned tag)
-{
-    __hip_atomic_store(p, ((u64)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-template <bool LOCAL>
-__device__ __forceinline__ void put(u64 *p, float v, unsigned tag)
-{
-    if constexpr (LOCAL) lx_put(p, v, tag);
-    else ll_put(p, v, tag);
-}
-
 /* Wave-wide sum / max through DPP lane moves (no LDS traffic): butterfly
  * within quads, rotations within 16-lane rows, then the four row results
  * combined in row order.  Every lane gets the result. */
@@ -159,12 +144,6 @@ __device__ __forceinline__ float wsum4(float a, float b, float c, float d)
     v += dpp<0x122>(v); /* row_ror:2 */
     return v + dpp<0x121>(v); /* row_ror:1 */
 }
-
-/* Work-group barrier of the helpers below; a kernel whose work-group has
- * waves outside the computation passes its own barrier object instead. */
-struct wg_bar {
-    __device__ __forceinline__ void operator()() const { __syncthreads(); }
-};
 
 struct ctx {
     unsigned tag;
@@ -226,9 +205,9 @@ __device__ __forceinline__ void settle(const ctx &c, const u64 *src, u64 (&v)[NP
  * of each producer when n is split evenly over nsent producers), then
  * re-reads just its stale words.  Ends with a barrier; `flag` is an LDS
  * word of the caller. */
-template <int NP, typename BAR = wg_bar>
+template <int NP>
 __device__ __forceinline__ void fetch(int tid, const ctx &c, const u64 *src, int n, int nsent,
-                                      float *dst, lds_flag *flag, BAR bar = BAR())
+                                      float *dst, lds_flag *flag)
 {
     const u64 filler = (u64)c.tag << 32;
     u64 v[NP];
@@ -246,23 +225,23 @@ __device__ __forceinline__ void fetch(int tid, const ctx &c, const u64 *src, int
             const int w = tid + NT * i;
             if (w < n) dst[w] = ll_val(v[i]);
         }
-        bar();
+        __syncthreads();
         return;
     }
     if (tid == 0) *flag = 0;
-    bar();
+    __syncthreads();
     unsigned bad = 0;
 #pragma unroll
     for (int i = 0; i < NP; ++i) bad |= (unsigned)(ll_tag(v[i]) != c.tag);
     if (bad) *flag = 1;
-    bar();
+    __syncthreads();
     if (*flag && !*c.dead) {
         if (tid < nsent) {
             const int w = (int)(((long)n * tid) / nsent);
             u64 sv[1] = {ll_get(src + w)};
             settle(c, src, sv, [&](int) { return w; });
         }
-        bar();
+        __syncthreads();
         settle(c, src, v, [&](int i) { const int w = tid + NT * i; return w < n ? w : -1; });
     }
 #pragma unroll
@@ -270,7 +249,7 @@ __device__ __forceinline__ void fetch(int tid, const ctx &c, const u64 *src, int
         const int w = tid + NT * i;
         if (w < n) dst[w] = ll_val(v[i]);
     }
-    bar();
+    __syncthreads();
 }
 
 /* Two tagged words src[w], src[w + 1] (w even) with one 16-byte load, with
@@ -321,9 +300,9 @@ __device__ __forceinline__ void settle2(const ctx &c, __amdgpu_buffer_rsrc_t r, 
  * n_embd is a multiple of 64 and the step kernel admits only ffn widths
  * that are multiples of the weight chunk): thread tid takes pairs tid +
  * NT*i (words 2p, 2p + 1). */
-template <int NP2, typename BAR = wg_bar>
+template <int NP2>
 __device__ __forceinline__ void fetch2(int tid, const ctx &c, const u64 *src, int n, int nsent, float *dst,
-                                       lds_flag *flag, BAR bar = BAR())
+                                       lds_flag *flag)
 {
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, n * 8, 0x00020000);
     const u32x4 filler = (u32x4){0u, c.tag, 0u, c.tag};
@@ -340,19 +319,19 @@ __device__ __forceinline__ void fetch2(int tid, const ctx &c, const u64 *src, in
         settle2(c, r, v, idx);
     } else {
         if (tid == 0) *flag = 0;
-        bar();
+        __syncthreads();
         unsigned bad = 0;
 #pragma unroll
         for (int i = 0; i < NP2; ++i) bad |= (unsigned)pair_stale(v[i], c.tag);
         if (bad) *flag = 1;
-        bar();
+        __syncthreads();
         if (*flag && !*c.dead) {
             if (tid < nsent) {
                 const int w = (int)(((long)n * tid) / nsent);
                 u64 sv[1] = {ll_get(src + w)};
                 settle(c, src, sv, [&](int) { return w; });
             }
-            bar();
+            __syncthreads();
             settle2(c, r, v, idx);
         }
     }
@@ -364,7 +343,7 @@ __device__ __forceinline__ void fetch2(int tid, const ctx &c, const u64 *src, in
             dst[w + 1] = __uint_as_float(v[i].z);
         }
     }
-    bar();
+    __syncthreads();
 }
 
 /* LayerNorm parameters of the thread's entries i = tid + NT*k, loaded at
@@ -393,9 +372,9 @@ __device__ __forceinline__ ln_params<NE> ln_load(int tid, const G2_GLOBAL float 
  * entries, x0 = x[0] (a shift that keeps the variance E[d^2] - E[d]^2 free
  * of cancellation when |mean| >> std); the two sums are reduced together,
  * wave totals added in wave order.  Ends with a barrier. */
-template <int NE, typename BAR = wg_bar>
+template <int NE>
 __device__ __forceinline__ void layernorm(int tid, const float *x, float *xin, const ln_params<NE> &lp,
-                                          int E, float *red, BAR bar = BAR())
+                                          int E, float *red)
 {
     /* every LDS read issued at once, at a clamped index (a read under a
      * lane condition would be waited for one at a time); entries past E
@@ -417,7 +396,7 @@ __device__ __forceinline__ void layernorm(int tid, const float *x, float *xin, c
         red[tid >> 6] = s;
         red[NW + (tid >> 6)] = q;
     }
-    bar();
+    __syncthreads();
     float S = red[0], Q = red[NW];
 #pragma unroll
     for (int w = 1; w < NW; ++w) {
@@ -433,7 +412,7 @@ __device__ __forceinline__ void layernorm(int tid, const float *x, float *xin, c
         const int i = tid + NT * k;
         if (i < E) xin[i] = fmaf((xv[k] - mean) * inv, lp.g[k], lp.b[k]);
     }
-    bar();
+    __syncthreads();
 }
 
 /* A work-group's share of one packed matrix W[N,K] (output-major): rows
@@ -642,9 +621,8 @@ __device__ __forceinline__ void attn_load(int tid, const g2_step_layer &y, att_r
  * position's key and value taken from L; the chunk's (max, sum, o[64]) go
  * to pout[0..65].  `on` is false for a half without a unit; it still takes
  * part in the three barriers. */
-template <bool LOCAL, typename BAR = wg_bar>
 __device__ __forceinline__ void attn_compute(int tid, const ctx &c, float scale, u64 *pout, att_lds &L,
-                                             const att_regs &r, bool on, int ch, int pos, int T, BAR bar = BAR())
+                                             const att_regs &r, bool on, int ch, int pos, int T)
 {
     const int t = tid & 255;
     const int j0 = ch * 64;
@@ -667,7 +645,7 @@ __device__ __forceinline__ void attn_compute(int tid, const ctx &c, float scale,
 #pragma unroll
         for (int e = 0; e < 4; ++e) L.red[dg][4 * pq + e] = s[e];
     }
-    bar();
+    __syncthreads();
     if (on && t < 64) {
         const bool ok = j0 + t < T;
         float s = 0.f;
@@ -680,7 +658,7 @@ __device__ __forceinline__ void attn_compute(int tid, const ctx &c, float scale,
         L.pr[t] = p;
         if (t == 0) { L.stat[0] = m; L.stat[1] = l; }
     }
-    bar();
+    __syncthreads();
     if (on) {
         float o[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -699,15 +677,15 @@ __device__ __forceinline__ void attn_compute(int tid, const ctx &c, float scale,
 #pragma unroll
         for (int f = 0; f < 4; ++f) L.red[jg][4 * d4 + f] = o[f];
     }
-    bar();
+    __syncthreads();
     if (on && t < 64) {
         float o = 0.f;
 #pragma unroll
         for (int g = 0; g < 16; ++g) o += L.red[g][t];
-        put<LOCAL>(pout + 2 + t, o, c.tag);
+        ll_put(pout + 2 + t, o, c.tag);
         if (t == 0) {
-            put<LOCAL>(pout, L.stat[0], c.tag);
-            put<LOCAL>(pout + 1, L.stat[1], c.tag);
+            ll_put(pout, L.stat[0], c.tag);
+            ll_put(pout + 1, L.stat[1], c.tag);
         }
     }
 }
@@ -719,10 +697,9 @@ __device__ __forceinline__ void attn_compute(int tid, const ctx &c, float scale,
  * taken from the exchange; the chunk's (max, sum, o[64]) go to pout[0..65].
  * `on` is false for a half without a unit; it still takes part in the
  * barriers. */
-template <bool LOCAL, typename BAR = wg_bar>
 __device__ __forceinline__ void attn_chunk(int tid, const ctx &c, float scale, const u64 *src, int qo,
                                            int ko, int vo, u64 *pout, att_lds &L, att_regs &r, bool on,
-                                           int ch, int pos, int T, u64 *trace_slot = nullptr, BAR bar = BAR())
+                                           int ch, int pos, int T)
 {
     const int t = tid & 255;
     /* q, k and v of the head at this position: src[qo + d], src[ko + d],
@@ -735,9 +712,8 @@ __device__ __forceinline__ void attn_chunk(int tid, const ctx &c, float scale, c
         float *dst = part == 0 ? L.q : (part == 1 ? L.kn : L.vn);
         dst[d] = ll_val(v[0]);
     }
-    bar();
-    if (trace_slot && tid == 0) *trace_slot = wall_clock64();
-    attn_compute<LOCAL>(tid, c, scale, pout, L, r, on, ch, pos, T, bar);
+    __syncthreads();
+    attn_compute(tid, c, scale, pout, L, r, on, ch, pos, T);
 }
 
 __device__ __forceinline__ bool am_better2(float v1, int i1, float v2, int i2)
@@ -746,18 +722,17 @@ __device__ __forceinline__ bool am_better2(float v1, int i1, float v2, int i2)
 }
 
 /* First-max over the work-group's (bv, bi); result in amv[0], ami[0]. */
-template <typename BAR = wg_bar>
-__device__ __forceinline__ void blk_argmax(int tid, float bv, int bi, float *amv, int *ami, BAR bar = BAR())
+__device__ __forceinline__ void blk_argmax(int tid, float bv, int bi, float *amv, int *ami)
 {
     amv[tid] = bv;
     ami[tid] = bi;
-    bar();
+    __syncthreads();
     for (int s = NT / 2; s > 0; s >>= 1) {
         if (tid < s && am_better2(amv[tid + s], ami[tid + s], amv[tid], ami[tid])) {
             amv[tid] = amv[tid + s];
             ami[tid] = ami[tid + s];
         }
-        bar();
+        __syncthreads();
     }
 }
 
@@ -1009,7 +984,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 const bool on = u < nunits;
                 const int h = on ? u / nch : 0, ch = on ? u % nch : 0;
                 attn_load(tid, y, ar[0], on, h, ch, pos, T, E, S);
-                attn_chunk<false>(tid, c, a.scale, R, h * 64, E + h * 64, 2 * E + h * 64,
+                attn_chunk(tid, c, a.scale, R, h * 64, E + h * 64, 2 * E + h * 64,
                                   R + G2X_ATT(E) + ((size_t)h * G2_STEP_MAXCH + ch) * 66, att[hf], ar[0],
                                   on, ch, pos, T);
                 __syncthreads();
