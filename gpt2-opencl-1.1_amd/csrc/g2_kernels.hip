@@ -975,7 +975,11 @@ G2K void g2k_splitk_resid(const g2_skred_args a)
  * dwordx4: lane l of an instruction writes 16 bytes at LDS base + 16 l),
  * three steps in a ring, issued two steps ahead; a step waits for its own
  * loads only (vmcnt(3): the 3 loads per wave of the step after it may
- * still be in flight), then one barrier.  The tile needs the 144 KB of LDS
+ * still be in flight), then one barrier.  The barrier sits between a step's
+ * two 32-k halves, so the LDS reads of each half run under the products of
+ * the half before it (the second half's under the first's; the next
+ * step's first half, once the barrier has seen it land, under the second),
+ * instead of every wave reading and then multiplying in lock step.  The tile needs the 144 KB of LDS
  * of a CU, so the work-group is as wide as a work-group can be: the rate
  * at which one CU streams its tiles grew with the number of waves issuing
  * them (4, 8, 16 waves: 11.5, 10.0, 9.1 ms for the 512-token XL prefill).
@@ -996,33 +1000,36 @@ typedef __attribute__((address_space(3))) void lds_t;
  * the next step, 3 per wave, may remain), then wait for every wave. */
 __device__ __forceinline__ void step_barrier() { asm volatile("s_waitcnt vmcnt(3)\n\ts_barrier" ::: "memory"); }
 
-/* The wave's products of one step from the stage at st. */
-__device__ __forceinline__ void mma(f32x4 (&acc)[2][2], const unsigned char *st, int wm, int wn, int lane)
+/* The fragments of one 32-k half of a step: the wave's a_hi, a_lo and
+ * weight rows. */
+struct frags {
+    h16x8 ah[2], al[2], b[2];
+};
+__device__ __forceinline__ void read_half(frags &f, const unsigned char *st, int kk, int wm, int wn, int lane)
 {
     const int fr = lane & 15, g = lane >> 4;
+    const int slot = (((kk + 8 * g) >> 3) ^ (fr >> 1)) << 4;
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += 32) {
-        h16x8 afh[2], afl[2], bf[2];
-        const int slot = (((kk + 8 * g) >> 3) ^ (fr >> 1)) << 4;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const unsigned char *row = st + (wm * 32 + i * 16 + fr) * 128 + slot;
-            afh[i] = *(const h16x8 *)row;
-            afl[i] = *(const h16x8 *)(row + TB);
-        }
-#pragma unroll
-        for (int j = 0; j < 2; ++j) bf[j] = *(const h16x8 *)(st + 2 * TB + (wn * 32 + j * 16 + fr) * 128 + slot);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afh[i], bf[j], acc[i][j], 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afl[i], bf[j], acc[i][j], 0, 0, 0);
+    for (int i = 0; i < 2; ++i) {
+        const unsigned char *row = st + (wm * 32 + i * 16 + fr) * 128 + slot;
+        f.ah[i] = *(const h16x8 *)row;
+        f.al[i] = *(const h16x8 *)(row + TB);
     }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) f.b[j] = *(const h16x8 *)(st + 2 * TB + (wn * 32 + j * 16 + fr) * 128 + slot);
+}
+__device__ __forceinline__ void mma_half(f32x4 (&acc)[2][2], const frags &f)
+{
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.ah[i], f.b[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f.al[i], f.b[j], acc[i][j], 0, 0, 0);
 }
 } /* namespace hg2 */
 
@@ -1085,13 +1092,25 @@ __device__ void hgemm2_impl(const g2_gemm_args &a)
     }
     issue(0, 0);
     issue(1, 1);
+    step_barrier(); /* step 0 has landed */
+    issue(2, 2);
+    frags f0, f1;
+    read_half(f0, lds, 0, wm, wn, lane);
     int cur = 0;
     for (int t = 0; t < nk; ++t) {
-        step_barrier(); /* step t has landed; the buffer of step t-1 is free */
-        const int nb2 = cur == 0 ? 2 : cur - 1;
-        issue(t + 2, nb2);
-        mma(acc, lds + cur * STAGE, wm, wn, lane);
-        cur = cur == 2 ? 0 : cur + 1;
+        const unsigned char *st = lds + cur * STAGE;
+        const int nx = cur == 2 ? 0 : cur + 1;
+        /* second half's reads under the first half's products */
+        read_half(f1, st, 32, wm, wn, lane);
+        mma_half(acc, f0);
+        /* step t + 1 has landed; every wave's reads of step t are done */
+        __builtin_amdgcn_s_waitcnt(0x0073); /* vmcnt(3) lgkmcnt(0) */
+        asm volatile("s_barrier" ::: "memory");
+        /* unconditional: past the last step it reads a reloaded stage */
+        read_half(f0, lds + nx * STAGE, 0, wm, wn, lane);
+        issue(t + 3, cur);
+        mma_half(acc, f1);
+        cur = nx;
     }
     /* no load may land in LDS after the work-group has ended */
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
