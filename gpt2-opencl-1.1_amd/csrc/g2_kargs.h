@@ -230,9 +230,12 @@ typedef struct {
 /* Persistent decode step (one cooperative launch per token, 512 threads per
  * work-group, one work-group per CU).  Per-layer weights come from a device
  * array of g2_step_layer.  Work-groups hand vectors to each other through
- * the exchange area `xbuf` of 64-bit words (value in the low half, the
- * step's tag in the high half); its layout is fixed by the G2X_* offsets
- * below and sized with G2X_TOTAL_WORDS. */
+ * two exchange areas: `xbuf` of 64-bit words (value in the low half, the
+ * step's tag in the high half), laid out by the G2X_* offsets below and
+ * sized with G2X_TOTAL_WORDS, for q/k/v, the attention partials, the
+ * argmax and the arrival words; and `xval` of plain floats, laid out by the
+ * G2V_* offsets and sized with G2V_TOTAL_FLOATS, for the four vectors every
+ * work-group reads whole (O, X1, H, X2). */
 typedef struct {
     const float *ln1_w, *ln1_b, *qkv_b, *proj_b, *ln2_w, *ln2_b, *fc_b, *fc2_b;
     const void *qkv_w, *proj_w, *fc_w, *fc2_w;
@@ -249,6 +252,7 @@ typedef struct {
     float *logits;
     int *state;
     unsigned long long *xbuf;
+    float *xval;
     /* optional phase timestamps (100 MHz clock): work-group w writes
      * trace[w * G2_TRACE_STRIDE(L) + 24*l + k] for phase boundary k of layer
      * l, and 24*L + k for the lm_head and the pick; NULL: off */
@@ -273,22 +277,29 @@ typedef struct {
 #define G2_STEP_MAXCH 16    /* 64-position key chunks per head */
 #define G2X_HEAD 64         /* words before the first layer region (word 0: abort) */
 #define G2X_DECISION 1      /* header word: a plain launch's residency verdict */
-/* Word offsets inside one layer region (E = n_embd, NH heads, F = ffn):
- * QKV outputs [3E], attention chunk partials [NH][G2_STEP_MAXCH][66],
- * merged attention O [E], X1 = x + proj [E], H = gelu(fc) [F, padded to an
- * even count], X2 = X1 + fc2 [E]; regions are padded to 32 words.  Every
- * vector starts at an even word (E is a multiple of 64), so the step
- * kernel reads them as 16-byte word pairs. */
+/* Word offsets inside one layer region (E = n_embd, NH heads): QKV outputs
+ * [3E], attention chunk partials [NH][G2_STEP_MAXCH][66]; regions are
+ * padded to 32 words. */
 #define G2X_ATT(E) (3 * (E))
-#define G2X_O(E, NH) (3 * (E) + (NH) * G2_STEP_MAXCH * 66)
-#define G2X_X1(E, NH) (G2X_O(E, NH) + (E))
-#define G2X_H(E, NH) (G2X_X1(E, NH) + (E))
-#define G2X_X2(E, NH, F) (G2X_H(E, NH) + (((F) + 1) & ~1))
-#define G2X_LAYER_WORDS(E, NH, F) ((G2X_X2(E, NH, F) + (E) + 31) & ~31)
+#define G2X_LAYER_WORDS(E, NH) ((G2X_ATT(E) + (NH) * G2_STEP_MAXCH * 66 + 31) & ~31)
 /* Total words: header, L layer regions, 2 argmax words per work-group, 32
  * spare words, 1 arrival word per work-group. */
-#define G2X_TOTAL_WORDS(L, E, NH, F, nwg) \
-    ((long)G2X_HEAD + (long)(L) * G2X_LAYER_WORDS(E, NH, F) + 3L * (nwg) + 32)
+#define G2X_TOTAL_WORDS(L, E, NH, nwg) ((long)G2X_HEAD + (long)(L) * G2X_LAYER_WORDS(E, NH) + 3L * (nwg) + 32)
+/* Float offsets inside one value region (F = ffn): merged attention O [E],
+ * X1 = x + proj [E], H = gelu(fc) [F, padded to 4], X2 = X1 + fc2 [E];
+ * regions are padded to 64 floats.  Every vector starts at a multiple of 4
+ * floats (E is a multiple of 64), so the step kernel reads them as 16-byte
+ * quads.  Each layer has two regions: the step with tag t writes region
+ * t & 1 and stores G2V_EMPTY into the same entries of the other region,
+ * which the next step writes; a value is present once it differs from
+ * G2V_EMPTY (a signalling NaN, which no arithmetic result equals). */
+#define G2V_O(E) 0
+#define G2V_X1(E) (E)
+#define G2V_H(E) (2 * (E))
+#define G2V_X2(E, F) (2 * (E) + (((F) + 3) & ~3))
+#define G2V_REGION(E, F) ((G2V_X2(E, F) + (E) + 63) & ~63)
+#define G2V_TOTAL_FLOATS(L, E, F) (2L * (L) * G2V_REGION(E, F))
+#define G2V_EMPTY 0x7FA5A5A5u
 /* after the layers: 2 argmax words per work-group, 32 spare words, then one
  * arrival word per work-group (plain launches) */
 #define G2X_ARRIVE(L, xlayer, nwg) ((long)G2X_HEAD + (long)(L) * (xlayer) + 2L * (nwg) + 32)

@@ -52,10 +52,12 @@ struct g2_model {
     /* fused path */
     int *state;
     float *att_part, *am_part;
-    /* persistent step kernel: per-layer pointer table, exchange area */
+    /* persistent step kernel: per-layer pointer table, exchange areas */
     g2_step_layer *step_layers;
     unsigned long long *xbuf;
     size_t xbuf_bytes;
+    float *xval;
+    size_t xval_floats;
     int step_wgs;  /* grid of the step kernel, 0 if this model cannot use it */
     int step_on;   /* decode steps run the step kernel */
     int plain;     /* launches are plain, not cooperative (2-4: test modes of the
@@ -165,6 +167,16 @@ static int check_model_config(const g2_config *c, int dtype, int path)
     return G2_OK;
 }
 
+/* Exchange areas of the step kernel to their empty state: tags 0 (no step
+ * has tag 0) and every value G2V_EMPTY. */
+static int exchange_clear(g2_model *m)
+{
+    int rc = g2i_hip(hipMemsetAsync(m->xbuf, 0, m->xbuf_bytes, g2i_stream()), "exchange clear");
+    if (!rc) rc = g2i_hip(hipMemsetD32Async((hipDeviceptr_t)m->xval, (int)G2V_EMPTY, m->xval_floats, g2i_stream()),
+                          "exchange clear");
+    return rc;
+}
+
 /* Whether the persistent step kernel can run this model: fused path, a
  * device grid and the kernel's own limits (g2p_step_refusal, shared with
  * the kernel's CPU address check).  On refusal `why` names the reason. */
@@ -203,9 +215,11 @@ static int step_setup(g2_model *m)
      * never arrives, 2 arrives 0.5 ms late, 3 arrives 2 ms late */
     const int tw = envw && envw[0] >= '1' && envw[0] <= '3' ? envw[0] - '0' : 0;
     m->plain = envc && envc[0] == '1' ? 0 : (tw ? 1 + tw : 1);
-    m->xbuf_bytes = (size_t)G2X_TOTAL_WORDS(L, c->n_embd, c->n_head, c->ffn_dim, nwg) * 8;
+    m->xbuf_bytes = (size_t)G2X_TOTAL_WORDS(L, c->n_embd, c->n_head, nwg) * 8;
+    m->xval_floats = (size_t)G2V_TOTAL_FLOATS(L, c->n_embd, c->ffn_dim);
     if (!rc) rc = dev_alloc(m, (void **)&m->xbuf, m->xbuf_bytes, 0);
-    if (!rc) rc = g2i_hip(hipMemsetAsync(m->xbuf, 0, m->xbuf_bytes, g2i_stream()), "exchange clear");
+    if (!rc) rc = dev_alloc(m, (void **)&m->xval, m->xval_floats * 4, 0);
+    if (!rc) rc = exchange_clear(m);
     if (rc) return rc;
     m->step_wgs = nwg;
     const char *env = getenv("G2_STEP");
@@ -289,7 +303,7 @@ int g2_model_free(g2_model *m)
     void *bufs[] = { m->wte, m->wpe, m->lnf_w, m->lnf_b, m->lm_head, m->hidden, m->ln_out,
                      m->attn, m->attn_proj, m->ffn1, m->ffn2, m->qkv_new, m->qkv_full,
                      m->last_hidden, m->logits, m->partial, m->scores, m->q, m->ids_dev,
-                     m->state, m->att_part, m->am_part, m->step_layers, m->xbuf, m->trace, m->pf_part,
+                     m->state, m->att_part, m->am_part, m->step_layers, m->xbuf, m->xval, m->trace, m->pf_part,
                      m->pf_kv };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; ++i)
         if (bufs[i]) hipFree(bufs[i]);
@@ -736,12 +750,13 @@ static int step_launch(g2_model *m)
     a.layers = m->step_layers; a.wte = m->wte; a.wpe = m->wpe; a.lm_w = m->lm_w;
     a.lnf_w = m->lnf_w; a.lnf_b = m->lnf_b; a.logits = m->logits; a.state = m->state;
     a.xbuf = m->xbuf;
+    a.xval = m->xval;
     a.trace = m->trace;
     a.L = c->n_layer; a.E = c->n_embd; a.F = c->ffn_dim; a.NH = c->n_head; a.V = c->vocab_size;
     a.S = G2_KV_MAX_SEQ;
     a.scale = 1.0f / sqrtf(64.0f);
     m->step_ran = 1;
-    a.xlayer = G2X_LAYER_WORDS(c->n_embd, c->n_head, c->ffn_dim);
+    a.xlayer = G2X_LAYER_WORDS(c->n_embd, c->n_head);
     const int fid = m->dtype == G2_F16 ? G2F_STEP_F16 : G2F_STEP_F32;
     if (m->plain) {
         a.plain = m->plain;
@@ -770,7 +785,7 @@ static int step_check(g2_model *m, int ngen_target)
     /* a timed-out hand-off (outputs invalid) is reported even if a later
      * launch of the call also found its grid not resident */
     if ((err & G2_ERR_STEP_NOT_RESIDENT) && !(err & G2_ERR_STEP_TIMEOUT)) {
-        rc = g2i_hip(hipMemsetAsync(m->xbuf, 0, m->xbuf_bytes, g2i_stream()), "exchange clear");
+        rc = exchange_clear(m);
         if (!rc) rc = up(m->state + G2S_ERR, &zero, sizeof zero);
         m->plain = 0;
         fprintf(stderr, "g2: decode step kernel: work-groups of a plain launch were not all resident; "
@@ -779,7 +794,7 @@ static int step_check(g2_model *m, int ngen_target)
         return rc ? rc : step_check(m, ngen_target);
     }
     if (!(err & G2_ERR_STEP_TIMEOUT)) return G2_OK;
-    rc = g2i_hip(hipMemsetAsync(m->xbuf, 0, m->xbuf_bytes, g2i_stream()), "exchange clear");
+    rc = exchange_clear(m);
     if (!rc) rc = up(m->state + G2S_ERR, &zero, sizeof zero);
     if (rc) return rc;
     return g2i_err(G2_E_HIP, "decode step kernel: a hand-off between work-groups timed out; "

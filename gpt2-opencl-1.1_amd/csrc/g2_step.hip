@@ -7,19 +7,28 @@
  * 8 XCDs), and the multi-kernel decode crosses five of them per layer.  Here
  * one launch runs every layer: each work-group (one per CU) owns fixed rows
  * of every matrix, and work-groups hand the activation vectors to each other
- * through an exchange area of tagged 64-bit words.
+ * through exchange areas.
  *
- * Exchange protocol: a producer stores (tag << 32 | float bits) with a
- * relaxed agent-scope atomic store; a consumer loads the words with relaxed
- * agent-scope atomic loads (coherent across XCDs) until every tag equals
- * this step's tag.  Each word carries its own validity, so no fence is
- * needed (an agent-scope release/acquire writes back or invalidates the XCD
- * L2 and costs microseconds).  Every word is written at most once per
- * launch; the tag is state[G2S_SEQ] + 1 and work-group 0 advances G2S_SEQ
- * at the end of the step, so words left by earlier steps never match.  The
- * KV cache entries of the current position reach the attention through the
- * exchange area; the cache itself is read only at earlier positions, which
- * earlier launches wrote.
+ * Exchange protocol, tagged words (q/k/v, attention partials, argmax): a
+ * producer stores (tag << 32 | float bits) with a relaxed agent-scope
+ * atomic store; a consumer loads the words with relaxed agent-scope atomic
+ * loads (coherent across XCDs) until every tag equals this step's tag.
+ * Each word carries its own validity, so no fence is needed (an agent-scope
+ * release/acquire writes back or invalidates the XCD L2 and costs
+ * microseconds).  Every word is written at most once per launch; the tag is
+ * state[G2S_SEQ] + 1 and work-group 0 advances G2S_SEQ at the end of the
+ * step, so words left by earlier steps never match.
+ *
+ * Plain values (the O, X1, H and X2 vectors, which every work-group of a
+ * phase reads whole): half the bytes of tagged words.  Each layer has two
+ * value regions; the step with tag t writes region t & 1 and empties the
+ * same entries of the other region (G2V_EMPTY), which the next step
+ * writes.  A consumer re-reads an entry until it is no longer empty.  After
+ * a step that gave up a wait or did not run, the host empties both regions.
+ *
+ * The KV cache entries of the current position reach the attention through
+ * the exchange area; the cache itself is read only at earlier positions,
+ * which earlier launches wrote.
  *
  * Memory-level parallelism: a work-group's weight rows of a matrix are
  * loaded into registers as soon as the previous matrix held by the same
@@ -58,8 +67,7 @@ constexpr int NW = NT / 64;                             /* 8 waves        */
 constexpr int UMAX = 4;                                 /* units per wave, main set */
 constexpr int UPROJ = 1;                                /* units per wave, proj set */
 constexpr int SEGC = 256;                               /* chunks per unit: 64 lanes x 4 */
-constexpr int PMAX = (G2_STEP_MAXF + NT - 1) / NT;      /* exchange words per thread */
-constexpr int PMAX2 = (G2_STEP_MAXF + 2 * NT - 1) / (2 * NT); /* word pairs per thread */
+constexpr int QMAX = (G2_STEP_MAXF + 4 * NT - 1) / (4 * NT); /* value quads per thread */
 constexpr unsigned long long WAIT_LIMIT = 10000000ull;  /* 100 ms of the 100 MHz clock */
 constexpr unsigned long long ABORT_CHECK_AFTER = 200000ull; /* 2 ms */
 
@@ -252,39 +260,55 @@ __device__ __forceinline__ void fetch(int tid, const ctx &c, const u64 *src, int
     __syncthreads();
 }
 
-/* Two tagged words src[w], src[w + 1] (w even) with one 16-byte load, with
- * the cache policy of ll_get (sc1: read at the coherence point, as the
- * relaxed agent-scope loads are), through a buffer resource over the
- * vector; each 8-byte word of the pair is read whole.  The low halves (.x,
- * .z) are the values, the high halves (.y, .w) the tags.  The pair loads
- * halve the requests of a vector fetch, which a wave issues at a bounded
- * rate (the 6400-word H vector is read by every work-group). */
-__device__ __forceinline__ u32x4 ll_get2(__amdgpu_buffer_rsrc_t r, int w)
+/* Plain values (O, X1, H, X2): a producer stores the float of this step
+ * into the region of the step's tag parity and G2V_EMPTY into the same entry
+ * of the other region, which the next step fills; the kernel boundary
+ * between steps makes those stores visible, so a consumer sees the
+ * entries of its region either empty or holding this step's value.  Both
+ * stores are relaxed agent-scope atomics, as ll_put's.  A result whose bits
+ * equal G2V_EMPTY (only a NaN could) is stored as the canonical NaN. */
+__device__ __forceinline__ void vput(float *cur, float *nxt, float v)
 {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, w * 8, 0, 16 /* sc1 */);
+    unsigned b = __float_as_uint(v);
+    b = b == G2V_EMPTY ? 0x7FC00000u : b;
+    __hip_atomic_store((unsigned *)cur, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store((unsigned *)nxt, G2V_EMPTY, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ bool pair_stale(const u32x4 &v, unsigned tag) { return v.y != tag || v.w != tag; }
 
-/* settle (above) for word pairs: pair i starts at word idx(i) (< 0: an
- * unused slot, which holds a current filler) */
-template <int NP2, typename IDX>
-__device__ __forceinline__ void settle2(const ctx &c, __amdgpu_buffer_rsrc_t r, u32x4 (&v)[NP2], IDX idx)
+/* Values 4q .. 4q + 3 with one 16-byte load through a buffer resource over
+ * the vector, with the cache policy of ll_get (sc1: read at the coherence
+ * point, as the relaxed agent-scope loads are); each 4-byte value is read
+ * whole.  Four values per request: a wave issues requests at a bounded
+ * rate, and the 6400-value H vector is read by every work-group. */
+__device__ __forceinline__ u32x4 vq_get(__amdgpu_buffer_rsrc_t r, int q)
+{
+    return __builtin_amdgcn_raw_buffer_load_b128(r, q * 16, 0, 16 /* sc1 */);
+}
+__device__ __forceinline__ bool quad_empty(const u32x4 &v)
+{
+    return v.x == G2V_EMPTY || v.y == G2V_EMPTY || v.z == G2V_EMPTY || v.w == G2V_EMPTY;
+}
+
+/* settle (above) for value quads: slot i holds quad idx(i) (< 0: an unused
+ * slot, which holds a filler) */
+template <int NQ, typename IDX>
+__device__ __forceinline__ void settle4(const ctx &c, __amdgpu_buffer_rsrc_t r, u32x4 (&v)[NQ], IDX idx)
 {
     unsigned bad = 0;
 #pragma unroll
-    for (int i = 0; i < NP2; ++i) bad |= (unsigned)pair_stale(v[i], c.tag);
+    for (int i = 0; i < NQ; ++i) bad |= (unsigned)quad_empty(v[i]);
     if (!bad || *c.dead) return;
     const u64 t0 = wall_clock64();
     for (;;) {
         __builtin_amdgcn_s_sleep(4);
 #pragma unroll
-        for (int i = 0; i < NP2; ++i) {
-            const int w = idx(i);
-            if (w >= 0 && pair_stale(v[i], c.tag)) v[i] = ll_get2(r, w);
+        for (int i = 0; i < NQ; ++i) {
+            const int q = idx(i);
+            if (q >= 0 && quad_empty(v[i])) v[i] = vq_get(r, q);
         }
         bad = 0;
 #pragma unroll
-        for (int i = 0; i < NP2; ++i) bad |= (unsigned)pair_stale(v[i], c.tag);
+        for (int i = 0; i < NQ; ++i) bad |= (unsigned)quad_empty(v[i]);
         if (!bad || *c.dead) return;
         /* the abort word is consulted only by waits that already took long */
         const u64 el = wall_clock64() - t0;
@@ -295,53 +319,52 @@ __device__ __forceinline__ void settle2(const ctx &c, __amdgpu_buffer_rsrc_t r, 
     }
 }
 
-/* fetch (above) by 16-byte word pairs, for a vector of an even number of
- * words n that starts at an even word (every vector of the exchange area:
- * n_embd is a multiple of 64 and the step kernel admits only ffn widths
- * that are multiples of the weight chunk): thread tid takes pairs tid +
- * NT*i (words 2p, 2p + 1). */
-template <int NP2>
-__device__ __forceinline__ void fetch2(int tid, const ctx &c, const u64 *src, int n, int nsent, float *dst,
+/* fetch (above) for a vector of plain values, n a multiple of 4 (n_embd is
+ * a multiple of 64, the ffn width of the weight chunk), src 16-byte
+ * aligned: thread tid takes quads tid + NT*i.  With more than one quad per
+ * thread a work-group that found empty values first waits on the quads
+ * holding value n*k/nsent, k < nsent (the first value of each producer when
+ * n is split evenly over nsent producers), then re-reads its empty quads.
+ * dst (LDS) is 16-byte aligned. */
+template <int NQ>
+__device__ __forceinline__ void fetch4(int tid, const ctx &c, const float *src, int n, int nsent, float *dst,
                                        lds_flag *flag)
 {
-    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, n * 8, 0x00020000);
-    const u32x4 filler = (u32x4){0u, c.tag, 0u, c.tag};
-    u32x4 v[NP2];
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, n * 4, 0x00020000);
+    const u32x4 filler = (u32x4){0u, 0u, 0u, 0u};
+    u32x4 v[NQ];
 #pragma unroll
-    for (int i = 0; i < NP2; ++i) {
-        const int w = 2 * (tid + NT * i);
-        v[i] = w < n ? ll_get2(r, w) : filler;
+    for (int i = 0; i < NQ; ++i) {
+        const int q = tid + NT * i;
+        v[i] = 4 * q < n ? vq_get(r, q) : filler;
     }
-    auto idx = [&](int i) { const int w = 2 * (tid + NT * i); return w < n ? w : -1; };
-    if constexpr (NP2 <= 2) {
+    auto idx = [&](int i) { const int q = tid + NT * i; return 4 * q < n ? q : -1; };
+    if constexpr (NQ <= 1) {
         (void)nsent;
         (void)flag;
-        settle2(c, r, v, idx);
+        settle4(c, r, v, idx);
     } else {
         if (tid == 0) *flag = 0;
         __syncthreads();
         unsigned bad = 0;
 #pragma unroll
-        for (int i = 0; i < NP2; ++i) bad |= (unsigned)pair_stale(v[i], c.tag);
+        for (int i = 0; i < NQ; ++i) bad |= (unsigned)quad_empty(v[i]);
         if (bad) *flag = 1;
         __syncthreads();
         if (*flag && !*c.dead) {
             if (tid < nsent) {
-                const int w = (int)(((long)n * tid) / nsent);
-                u64 sv[1] = {ll_get(src + w)};
-                settle(c, src, sv, [&](int) { return w; });
+                const int q = (int)(((long)n * tid) / nsent) >> 2;
+                u32x4 sv[1] = {vq_get(r, q)};
+                settle4(c, r, sv, [&](int) { return q; });
             }
             __syncthreads();
-            settle2(c, r, v, idx);
+            settle4(c, r, v, idx);
         }
     }
 #pragma unroll
-    for (int i = 0; i < NP2; ++i) {
-        const int w = 2 * (tid + NT * i);
-        if (w < n) {
-            dst[w] = __uint_as_float(v[i].x);
-            dst[w + 1] = __uint_as_float(v[i].z);
-        }
+    for (int i = 0; i < NQ; ++i) {
+        const int q = tid + NT * i;
+        if (4 * q < n) *(u32x4 *)(dst + 4 * q) = v[i];
     }
     __syncthreads();
 }
@@ -807,12 +830,12 @@ __device__ __forceinline__ bool grid_resident(int tid, const ctx &c, const u64 *
 }
 
 /* LM head and greedy pick, the end of every step kernel: X2 of the last
- * layer (xlast: E words from nwg producers) -> LayerNorm_f -> logits of the
+ * layer (xlast: E values from nwg producers) -> LayerNorm_f -> logits of the
  * work-group's head rows -> first-max per work-group (argmax words AM) ->
  * work-group 0 merges them (g2k_argmax_merge with advance) and advances the
  * device state.  All threads of the work-group take part. */
 template <typename WT>
-__device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, const shares &sh, const u64 *xlast, u64 *AM,
+__device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, const shares &sh, const float *xlast, u64 *AM,
                                         u32x4 (&wa)[UMAX][4], bool preloaded, float *xres, float *xin,
                                         float *part, float *red, float *amv, int *ami, lds_flag *flag)
 {
@@ -827,7 +850,7 @@ __device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, con
     const ln_params<NPE> lpf = ln_load<NPE>(tid, gl(a.lnf_w), gl(a.lnf_b), E);
     const plan p = make_plan(a.lm_w, sh.lm);
     if (!preloaded) load_set<UMAX>(tid, wa, p, 0);
-    fetch<NPE>(tid, c, xlast, E, nwg, xres, flag);
+    fetch4<(G2_STEP_MAXE + 4 * NT - 1) / (4 * NT)>(tid, c, xlast, E, nwg, xres, flag);
     TRACE(0);
     layernorm(tid, xres, xin, lpf, E, red);
     matvec<WT, UMAX>(tid, wa, p, xin, part);
@@ -890,8 +913,8 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     __shared__ volatile int dead;
     __shared__ volatile int flag;
 
-    constexpr int NPE = (G2_STEP_MAXE + NT - 1) / NT;              /* words of an E vector */
-    constexpr int NPE2 = (G2_STEP_MAXE + 2 * NT - 1) / (2 * NT);   /* its word pairs       */
+    constexpr int NPE = (G2_STEP_MAXE + NT - 1) / NT;              /* E entries per thread */
+    constexpr int NQE = (G2_STEP_MAXE + 4 * NT - 1) / (4 * NT);    /* its value quads      */
     constexpr int NPM = (G2_STEP_MAXCH * 66 + NT - 1) / NT;        /* a head's partials    */
     const int wg = blockIdx.x, nwg = gridDim.x;
     const int E = a.E, F = a.F, NH = a.NH, S = a.S, V = a.V;
@@ -909,6 +932,10 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     c.dead = (lds_flag *)&dead;
     const int T = pos + 1, nch = (T + 63) >> 6;
     u64 *X = a.xbuf + G2X_HEAD;
+    /* value regions of layer l: this step's at XV + 2*l*VR, the next step's
+     * at XN + 2*l*VR */
+    const size_t VR = G2V_REGION(E, F);
+    float *XV = a.xval + (c.tag & 1u) * VR, *XN = a.xval + ((c.tag & 1u) ^ 1u) * VR;
     att_regs ar[1];
 
     /* register sets: wa carries qkv -> fc -> fc2 -> next qkv (each loaded as
@@ -942,6 +969,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     for (int l = 0; l < a.L; ++l) {
         const g2_step_layer y = LT[l];
         u64 *R = X + (size_t)l * a.xlayer;
+        float *RV = XV + 2 * VR * l, *RN = XN + 2 * VR * l;
 
         /* ---- QKV: LayerNorm(x) . Wqkv + b -> q, k, v (+ KV cache) */
         {
@@ -951,7 +979,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             const ln_params<NPE> lp = ln_load<NPE>(tid, gl(y.ln1_w), gl(y.ln1_b), E);
             const float bias = gl(y.qkv_b)[min(p.r0 + tid, 3 * E - 1)]; /* used by tid < nrows */
             if (l > 0) {
-                fetch2<NPE2>(tid, c, X + (size_t)(l - 1) * a.xlayer + G2X_X2(E, NH, F), E, nwg, xres, (lds_flag *)&flag);
+                fetch4<NQE>(tid, c, RV - 2 * VR + G2V_X2(E, F), E, nwg, xres, (lds_flag *)&flag);
             }
             TRACE(1);
             layernorm(tid, xres, xin, lp, E, red);
@@ -1013,7 +1041,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             if (tid < 64) {
                 float acc = 0.f;
                 for (int ch = 0; ch < nch; ++ch) acc = fmaf(xin[ch * 66 + 2 + tid], cw[ch], acc);
-                ll_put(R + G2X_O(E, NH) + h * 64 + tid, acc / Ls, c.tag);
+                vput(RV + G2V_O(E) + h * 64 + tid, RN + G2V_O(E) + h * 64 + tid, acc / Ls);
             }
             __syncthreads();
         }
@@ -1032,14 +1060,14 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             const int tid = fresh_tid();
             const plan p = make_plan(y.proj_w, sh.proj);
             const float bias = gl(y.proj_b)[min(p.r0 + tid, E - 1)];
-            fetch2<NPE2>(tid, c, R + G2X_O(E, NH), E, NH, xin, (lds_flag *)&flag);
+            fetch4<NQE>(tid, c, RV + G2V_O(E), E, NH, xin, (lds_flag *)&flag);
             TRACE(5);
             matvec<WT, UPROJ>(tid, wp, p, xin, part);
             if (tid < p.nrows) {
                 const int r = p.r0 + tid;
                 float v = row_sum(p, part, tid);
                 v += bias;
-                ll_put(R + G2X_X1(E, NH) + r, v + xres[r], c.tag);
+                vput(RV + G2V_X1(E) + r, RN + G2V_X1(E) + r, v + xres[r]);
             }
             TRACE(6);
             if (l + 1 < a.L) load_set<UPROJ>(tid, wp, make_plan(LT[l + 1].proj_w, sh.proj), 0);
@@ -1052,7 +1080,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             const plan p = make_plan(y.fc_w, sh.fc);
             const ln_params<NPE> lp = ln_load<NPE>(tid, gl(y.ln2_w), gl(y.ln2_b), E);
             const float bias = gl(y.fc_b)[min(p.r0 + tid, F - 1)];
-            fetch2<NPE2>(tid, c, R + G2X_X1(E, NH), E, nwg - NH, xres, (lds_flag *)&flag);
+            fetch4<NQE>(tid, c, RV + G2V_X1(E), E, nwg - NH, xres, (lds_flag *)&flag);
             TRACE(7);
             layernorm(tid, xres, xin, lp, E, red);
             TRACE(13);
@@ -1062,7 +1090,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 const int r = p.r0 + tid;
                 float v = row_sum(p, part, tid);
                 v += bias;
-                ll_put(R + G2X_H(E, NH) + r, gelu_f(v), c.tag);
+                vput(RV + G2V_H(E) + r, RN + G2V_H(E) + r, gelu_f(v));
             }
             TRACE(8);
             load_set<UMAX>(tid, wa, make_plan(y.fc2_w, sh.fc2), 0);
@@ -1074,7 +1102,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             const int tid = fresh_tid();
             const plan p = make_plan(y.fc2_w, sh.fc2);
             const float bias = gl(y.fc2_b)[min(p.r0 + tid, E - 1)];
-            fetch2<PMAX2>(tid, c, R + G2X_H(E, NH), F, nwg, xin, (lds_flag *)&flag);
+            fetch4<QMAX>(tid, c, RV + G2V_H(E), F, nwg, xin, (lds_flag *)&flag);
             TRACE(9);
             matvec<WT, UMAX>(tid, wa, p, xin, part);
             TRACE(15);
@@ -1082,7 +1110,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 const int r = p.r0 + tid;
                 float v = row_sum(p, part, tid);
                 v += bias;
-                ll_put(R + G2X_X2(E, NH, F) + r, v + xres[r], c.tag);
+                vput(RV + G2V_X2(E, F) + r, RN + G2V_X2(E, F) + r, v + xres[r]);
             }
             TRACE(10);
             if (l + 1 < a.L) load_set<UMAX>(tid, wa, make_plan(LT[l + 1].qkv_w, sh.qkv), 0);
@@ -1092,7 +1120,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     }
 
     /* the first batch of lm_head rows was loaded by the last fc2 phase */
-    lm_pick<WT>(a, c, sh, X + (size_t)(a.L - 1) * a.xlayer + G2X_X2(E, NH, F), X + (size_t)a.L * a.xlayer, wa, true,
+    lm_pick<WT>(a, c, sh, XV + 2 * VR * (a.L - 1) + G2V_X2(E, F), X + (size_t)a.L * a.xlayer, wa, true,
                 xres, xin, part, red, amv, ami, (lds_flag *)&flag);
 }
 

@@ -13,7 +13,10 @@
  *   KV cache  the attention units' 16-byte loads of K [E][S] and V [S][E]
  *             and the current position's K/V stores;
  *   exchange  every tagged word read or written: q/k/v, chunk partials,
- *             merged O, X1, H, X2, the argmax words, the arrival words;
+ *             the argmax words, the arrival words; every plain value
+ *             stored (merged O, X1, H, X2, in the region of either tag
+ *             parity, and the emptied entry of the other region) and every
+ *             16-byte quad of them fetched;
  *   LDS       the dot products' x reads and the partial-sum slots.
  * Prints one line of counts; exits 1 if any access is out of bounds, 3 if
  * the host refuses the shape (g2p_step_refusal: it then never launches it).
@@ -110,8 +113,10 @@ int main(int argc, char **argv)
     const int VE = atoi(argv[6]), pos = atoi(argv[7]), nwg = atoi(argv[8]);
     plant = argc > 9 ? atoi(argv[9]) : 0;
     const int S = G2_KV_MAX_SEQ, NT = G2_STEP_THREADS;
-    const long xlayer = G2X_LAYER_WORDS(E, NH, F);
-    const long xtotal = G2X_TOTAL_WORDS(L, E, NH, F, nwg);
+    const long xlayer = G2X_LAYER_WORDS(E, NH);
+    const long xtotal = G2X_TOTAL_WORDS(L, E, NH, nwg);
+    const long att_end = G2X_ATT(E) + (long)NH * G2_STEP_MAXCH * 66; /* end of the partials */
+    const long VR = G2V_REGION(E, F), vtotal = G2V_TOTAL_FLOATS(L, E, F);
     const int T = pos + 1, nch = (T + 63) / 64;
     const int NPE = (G2_STEP_MAXE + NT - 1) / NT;
     if (nch > G2_STEP_MAXCH) {
@@ -124,12 +129,24 @@ int main(int argc, char **argv)
         printf("refused: %s\n", why);
         return 3;
     }
-    /* a vector fetch by 16-byte word pairs: pairs [base + 2p, base + 2p + 2)
-     * for 2p < n, inside [.., end); the vector must start at an even word
-     * and have an even length */
-    auto pairs = [&](const char *what, long base, int n, long end) {
-        if ((base & 1) || (n & 1)) chk("vector of word pairs", 0, 1, 0);
-        for (int w = 0; w < n; w += 2) chk(what, base + w, base + w + 2, end);
+    /* value region of layer l for tag parity b, and the vector offsets in it;
+     * each vector ends where the next one starts */
+    auto vreg = [&](int l, int b) { return (2L * l + b) * VR; };
+    const long vO = G2V_O(E), vX1 = G2V_X1(E), vH = G2V_H(E), vX2 = G2V_X2(E, F);
+    for (int l = 0; l < L; ++l)
+        for (int b = 0; b < 2; ++b) chk("value region", vreg(l, b), vreg(l, b) + VR, vtotal);
+    /* a vector fetch by 16-byte quads: [base + 4q, base + 4q + 4) for 4q < n,
+     * inside [.., end); the vector must start at a multiple of 4 floats and
+     * have a length that is one */
+    auto quads = [&](const char *what, long base, int n, long end) {
+        if ((base & 3) || (n & 3)) chk("vector of value quads", 0, 1, 0);
+        for (int w = 0; w < n; w += 4) chk(what, base + w, base + w + 4, end);
+    };
+    /* stores of values [lo, hi) of a vector at offset off (ending at offset
+     * end) of layer l's region, for either tag parity; each also empties the
+     * same entries of the other region */
+    auto vstore = [&](const char *what, int l, long off, long lo, long hi, long end) {
+        for (int b = 0; b < 2; ++b) chk(what, vreg(l, b) + off + lo, vreg(l, b) + off + hi, vreg(l, b) + end);
     };
     long proj_rows = 0; /* rows of proj over all work-groups and layers */
     for (long wg = 0; wg < nwg; ++wg) {
@@ -156,7 +173,8 @@ int main(int argc, char **argv)
                 if (r >= 2 * E) chk("V cache store", (long)pos * E + (r - 2 * E), (long)pos * E + (r - 2 * E) + 1, (long)S * E);
                 else if (r >= E) chk("K cache store", (long)(r - E) * S + pos, (long)(r - E) * S + pos + 1, (long)E * S);
             }
-            if (l > 0) pairs("X2 fetch", R - xlayer + G2X_X2(E, NH, F), E, R);
+            if (l > 0)
+                for (int b = 0; b < 2; ++b) quads("X2 fetch", vreg(l - 1, b) + vX2, E, vreg(l - 1, b) + VR);
             /* ATTN units */
             const int nunits = NH * nch, rounds = (nunits + 2 * nwg - 1) / (2 * nwg);
             for (int rd = 0; rd < rounds; ++rd)
@@ -176,35 +194,36 @@ int main(int argc, char **argv)
                     }
                     if (on && t < 66) {
                         const long pw = R + G2X_ATT(E) + ((long)h * G2_STEP_MAXCH + ch) * 66 + t;
-                        chk("chunk partial word", pw, pw + 1, R + G2X_O(E, NH));
+                        chk("chunk partial word", pw, pw + 1, R + att_end);
                     }
                 }
             /* MERGE of head h by work-group h */
             for (int h = (int)wg; h < NH; h += nwg) {
                 const long hp = R + G2X_ATT(E) + (long)h * G2_STEP_MAXCH * 66;
-                chk("merge partial reads", hp, hp + (long)nch * 66, R + G2X_O(E, NH));
-                chk("O words", R + G2X_O(E, NH) + h * 64, R + G2X_O(E, NH) + h * 64 + 64, R + G2X_X1(E, NH));
+                chk("merge partial reads", hp, hp + (long)nch * 66, R + att_end);
+                vstore("O values", l, vO, h * 64, h * 64 + 64, vX1);
             }
             /* PROJ, FC, FC2 */
             /* proj: the work-groups merging no head */
             if (wg >= NH) {
                 matrix("proj weights", "b", E, E, VE, 1, wg - NH, nwg - NH);
-                pairs("O fetch", R + G2X_O(E, NH), E, R + G2X_X1(E, NH));
+                for (int b = 0; b < 2; ++b) quads("O fetch", vreg(l, b) + vO, E, vreg(l, b) + vX1);
                 const g2p_rows pp = g2p_proj_plan(E, VE, NH, wg, nwg);
-                chk("X1 words", R + G2X_X1(E, NH) + pp.r0, R + G2X_X1(E, NH) + pp.r0 + pp.nrows, R + G2X_H(E, NH));
+                vstore("X1 values", l, vX1, pp.r0, pp.r0 + pp.nrows, vH);
                 proj_rows += pp.nrows;
             }
-            pairs("X1 fetch", R + G2X_X1(E, NH), E, R + G2X_H(E, NH));
+            for (int b = 0; b < 2; ++b) quads("X1 fetch", vreg(l, b) + vX1, E, vreg(l, b) + vH);
             matrix("fc weights", "b", F, E, VE, 4, wg, nwg);
             const g2p_rows pf = g2p_rows_plan(F, E, VE, wg, nwg);
-            chk("H words", R + G2X_H(E, NH) + pf.r0, R + G2X_H(E, NH) + pf.r0 + pf.nrows, R + G2X_X2(E, NH, F));
-            pairs("H fetch", R + G2X_H(E, NH), F, R + G2X_X2(E, NH, F));
+            vstore("H values", l, vH, pf.r0, pf.r0 + pf.nrows, vX2);
+            for (int b = 0; b < 2; ++b) quads("H fetch", vreg(l, b) + vH, F, vreg(l, b) + vX2);
             matrix("fc2 weights", "b", E, F, VE, 4, wg, nwg);
             const g2p_rows p2 = g2p_rows_plan(E, F, VE, wg, nwg);
-            chk("X2 words", R + G2X_X2(E, NH, F) + p2.r0, R + G2X_X2(E, NH, F) + p2.r0 + p2.nrows, R + xlayer);
+            vstore("X2 values", l, vX2, p2.r0, p2.r0 + p2.nrows, VR);
             chk("fetched vector in LDS", 0, F, G2_STEP_MAXF);
         }
-        /* LM head rows, logits, argmax words */
+        /* LM head: X2 of the last layer, rows, logits, argmax words */
+        for (int b = 0; b < 2; ++b) quads("LM X2 fetch", vreg(L - 1, b) + vX2, E, vreg(L - 1, b) + VR);
         matrix("lm_head weights", nullptr, V, E, VE, 4, wg, nwg);
         const g2p_rows pl = g2p_rows_plan(V, E, VE, wg, nwg);
         chk("logits", pl.r0, pl.r0 + pl.nrows, V);
