@@ -369,47 +369,53 @@ __device__ __forceinline__ void fetch4(int tid, const ctx &c, const float *src, 
     __syncthreads();
 }
 
-/* LayerNorm parameters of the thread's entries i = tid + NT*k, loaded at
- * the start of a phase so their latency overlaps the input wait. */
-template <int NE>
-struct ln_params {
-    float g[NE], b[NE];
-};
-
-template <int NE>
-__device__ __forceinline__ ln_params<NE> ln_load(int tid, const G2_GLOBAL float *g, const G2_GLOBAL float *b, int E)
+/* A vector of n <= 4*NT values with LayerNorm to follow: thread tid takes
+ * quad tid (values 4tid .. 4tid + 3, present when 4tid < n) and keeps it in
+ * registers; it also reads quad 0, whose first value is the shift of the
+ * LayerNorm's sums, so no thread waits for another to learn it.  The quad
+ * is also stored to dst[4tid..] (LDS) for the phase's residual; the
+ * LayerNorm's first barrier makes it visible. */
+__device__ __forceinline__ f32x4 fetch_q(int tid, const ctx &c, const float *src, int n, float *dst, float &x0)
 {
-    ln_params<NE> p;
-#pragma unroll
-    for (int k = 0; k < NE; ++k) {
-        const int i = min(tid + NT * k, E - 1); /* unconditional, as in load_set */
-        p.g[k] = g[i];
-        p.b[k] = b[i];
-    }
-    return p;
+    static_assert(G2_STEP_MAXE <= 4 * NT, "one quad per thread");
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, n * 4, 0x00020000);
+    const bool on = 4 * tid < n;
+    u32x4 v[2];
+    v[0] = on ? vq_get(r, tid) : (u32x4){0u, 0u, 0u, 0u};
+    v[1] = vq_get(r, 0);
+    settle4(c, r, v, [&](int i) { return i == 1 ? 0 : (on ? tid : -1); });
+    if (on) *(u32x4 *)(dst + 4 * tid) = v[0];
+    x0 = __uint_as_float(v[1].x);
+    return __builtin_bit_cast(f32x4, v[0]);
 }
 
-/* xin = LayerNorm(x) over E entries (both in LDS): (x - mean) * inv_std *
- * g + b with the biased variance, eps 1e-5 (layernorm, math.cl:283-311).
- * One block reduction: every thread sums d = x - x0 and d^2 over its
- * entries, x0 = x[0] (a shift that keeps the variance E[d^2] - E[d]^2 free
- * of cancellation when |mean| >> std); the two sums are reduced together,
- * wave totals added in wave order.  Ends with a barrier. */
-template <int NE>
-__device__ __forceinline__ void layernorm(int tid, const float *x, float *xin, const ln_params<NE> &lp,
-                                          int E, float *red)
+/* LayerNorm gain and bias of the thread's quad (clamped: quads past E are
+ * never stored), loaded at the start of a phase so their latency overlaps
+ * the input wait. */
+struct ln_quad {
+    f32x4 g, b;
+};
+__device__ __forceinline__ ln_quad ln_qload(int tid, const float *g, const float *b, int E)
 {
-    /* every LDS read issued at once, at a clamped index (a read under a
-     * lane condition would be waited for one at a time); entries past E
-     * contribute exact zeros */
-    const float x0 = x[0];
-    float xv[NE];
-#pragma unroll
-    for (int k = 0; k < NE; ++k) xv[k] = x[min(tid + NT * k, E - 1)];
+    const int q = min(tid, E / 4 - 1);
+    return ln_quad{gl((const f32x4 *)g)[q], gl((const f32x4 *)b)[q]};
+}
+
+/* xin = LayerNorm(x) over E entries, x held as quads in registers (thread
+ * tid: entries 4tid .. 4tid + 3, x0 = x[0]): (x - mean) * inv_std * g + b
+ * with the biased variance, eps 1e-5 (layernorm, math.cl:283-311).  One
+ * block reduction: every thread sums d = x - x0 and d^2 over its quad (a
+ * shift that keeps the variance E[d^2] - E[d]^2 free of cancellation when
+ * |mean| >> std); the two sums are reduced together, wave totals added in
+ * wave order.  Ends with a barrier. */
+__device__ __forceinline__ void layernorm_q(int tid, const f32x4 &x, float x0, const ln_quad &lp, int E,
+                                            float *xin, float *red)
+{
+    const bool on = 4 * tid < E;
     float s = 0.f, q = 0.f;
 #pragma unroll
-    for (int k = 0; k < NE; ++k) {
-        const float d = tid + NT * k < E ? xv[k] - x0 : 0.f;
+    for (int e = 0; e < 4; ++e) {
+        const float d = on ? x[e] - x0 : 0.f;
         s += d;
         q = fmaf(d, d, q);
     }
@@ -430,10 +436,11 @@ __device__ __forceinline__ void layernorm(int tid, const float *x, float *xin, c
     const float mean = x0 + md;
     const float var = fmaxf(Q / (float)E - md * md, 0.f);
     const float inv = 1.0f / sqrtf(var + 1e-5f);
+    if (on) {
+        f32x4 o;
 #pragma unroll
-    for (int k = 0; k < NE; ++k) {
-        const int i = tid + NT * k;
-        if (i < E) xin[i] = fmaf((xv[k] - mean) * inv, lp.g[k], lp.b[k]);
+        for (int e = 0; e < 4; ++e) o[e] = fmaf((x[e] - mean) * inv, lp.g[e], lp.b[e]);
+        *(f32x4 *)(xin + 4 * tid) = o;
     }
     __syncthreads();
 }
@@ -846,13 +853,13 @@ __device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, con
     const int ngen = a.state[G2S_NGEN], min_new = a.state[G2S_MIN_NEW];
     const int pos = clampi(a.state[G2S_POS], 0, a.S - 1);
     const unsigned seq = (unsigned)a.state[G2S_SEQ];
-    constexpr int NPE = (G2_STEP_MAXE + NT - 1) / NT;
-    const ln_params<NPE> lpf = ln_load<NPE>(tid, gl(a.lnf_w), gl(a.lnf_b), E);
+    const ln_quad lpf = ln_qload(tid, a.lnf_w, a.lnf_b, E);
     const plan p = make_plan(a.lm_w, sh.lm);
     if (!preloaded) load_set<UMAX>(tid, wa, p, 0);
-    fetch4<(G2_STEP_MAXE + 4 * NT - 1) / (4 * NT)>(tid, c, xlast, E, nwg, xres, flag);
+    float x0;
+    const f32x4 xq = fetch_q(tid, c, xlast, E, xres, x0);
     TRACE(0);
-    layernorm(tid, xres, xin, lpf, E, red);
+    layernorm_q(tid, xq, x0, lpf, E, xin, red);
     matvec<WT, UMAX>(tid, wa, p, xin, part);
     const int masked = ngen < min_new ? G2_EOS_ID : -1;
     float bv = -INFINITY;
@@ -913,7 +920,6 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     __shared__ volatile int dead;
     __shared__ volatile int flag;
 
-    constexpr int NPE = (G2_STEP_MAXE + NT - 1) / NT;              /* E entries per thread */
     constexpr int NQE = (G2_STEP_MAXE + 4 * NT - 1) / (4 * NT);    /* its value quads      */
     constexpr int NPM = (G2_STEP_MAXCH * 66 + NT - 1) / NT;        /* a head's partials    */
     const int wg = blockIdx.x, nwg = gridDim.x;
@@ -976,13 +982,18 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             const int tid = fresh_tid();
             TRACE(0);
             const plan p = make_plan(y.qkv_w, sh.qkv);
-            const ln_params<NPE> lp = ln_load<NPE>(tid, gl(y.ln1_w), gl(y.ln1_b), E);
+            const ln_quad lp = ln_qload(tid, y.ln1_w, y.ln1_b, E);
             const float bias = gl(y.qkv_b)[min(p.r0 + tid, 3 * E - 1)]; /* used by tid < nrows */
+            f32x4 xq;
+            float x0;
             if (l > 0) {
-                fetch4<NQE>(tid, c, RV - 2 * VR + G2V_X2(E, F), E, nwg, xres, (lds_flag *)&flag);
+                xq = fetch_q(tid, c, RV - 2 * VR + G2V_X2(E, F), E, xres, x0);
+            } else { /* the embedding, in LDS since the prologue's barrier */
+                xq = *(const f32x4 *)(xres + 4 * min(tid, E / 4 - 1));
+                x0 = xres[0];
             }
             TRACE(1);
-            layernorm(tid, xres, xin, lp, E, red);
+            layernorm_q(tid, xq, x0, lp, E, xin, red);
             TRACE(11);
             matvec<WT, UMAX>(tid, wa, p, xin, part);
             TRACE(12);
@@ -1078,11 +1089,12 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         {
             const int tid = fresh_tid();
             const plan p = make_plan(y.fc_w, sh.fc);
-            const ln_params<NPE> lp = ln_load<NPE>(tid, gl(y.ln2_w), gl(y.ln2_b), E);
+            const ln_quad lp = ln_qload(tid, y.ln2_w, y.ln2_b, E);
             const float bias = gl(y.fc_b)[min(p.r0 + tid, F - 1)];
-            fetch4<NQE>(tid, c, RV + G2V_X1(E), E, nwg - NH, xres, (lds_flag *)&flag);
+            float x0;
+            const f32x4 xq = fetch_q(tid, c, RV + G2V_X1(E), E, xres, x0);
             TRACE(7);
-            layernorm(tid, xres, xin, lp, E, red);
+            layernorm_q(tid, xq, x0, lp, E, xin, red);
             TRACE(13);
             matvec<WT, UMAX>(tid, wa, p, xin, part);
             TRACE(14);

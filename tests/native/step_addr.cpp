@@ -118,7 +118,6 @@ int main(int argc, char **argv)
     const long att_end = G2X_ATT(E) + (long)NH * G2_STEP_MAXCH * 66; /* end of the partials */
     const long VR = G2V_REGION(E, F), vtotal = G2V_TOTAL_FLOATS(L, E, F);
     const int T = pos + 1, nch = (T + 63) / 64;
-    const int NPE = (G2_STEP_MAXE + NT - 1) / NT;
     if (nch > G2_STEP_MAXCH) {
         fprintf(stderr, "position beyond the cache\n");
         return 1;
@@ -156,10 +155,11 @@ int main(int argc, char **argv)
                 chk("wte row", (long)(V - 1) * E + d, (long)(V - 1) * E + d + 1, (long)V * E);
                 chk("wpe row", (long)pos * E + d, (long)pos * E + d + 1, (long)S * E);
             }
-            for (int k = 0; k < NPE; ++k) {
-                const int i = g2p_min(tid + NT * k, E - 1);
-                chk("LayerNorm parameters", i, i + 1, E);
-            }
+            /* gain and bias quads; the fused fetch's own quad and quad 0 are
+             * among the vector quads checked per phase */
+            const int q = g2p_min(tid, E / 4 - 1);
+            chk("LayerNorm parameter quad", 4L * q, 4L * q + 4, E);
+            if (4 * tid < E) chk("fetched quad in LDS", 4L * tid, 4L * tid + 4, G2_STEP_MAXE);
             chk("arrival word", G2X_ARRIVE(L, xlayer, nwg) + wg, G2X_ARRIVE(L, xlayer, nwg) + wg + 1, xtotal);
         }
         for (int l = 0; l < L; ++l) {
