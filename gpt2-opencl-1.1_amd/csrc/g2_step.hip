@@ -610,7 +610,8 @@ struct att_lds {
 };
 
 /* Cached keys and values of one 64-position chunk, loaded into registers
- * ahead of the attention (they do not depend on this position's q).
+ * ahead of their use (they do not depend on this position's q): the keys
+ * before the q/k/v wait (attn_load), the values after it (attn_load_v).
  * Scores: thread (pq = t%16, dg = t/16) of a half takes positions
  * j0+4pq..+3 and dims 4dg..+3 (four 16-byte loads of the transposed K
  * cache); weighted sum: thread (d4 = t%16, jg = t/16) takes dims 4d4..+3
@@ -641,6 +642,15 @@ __device__ __forceinline__ void attn_load(int tid, const g2_step_layer &y, att_r
     const G2_GLOBAL f32x4 *kb = gl((const f32x4 *)(y.k_cache + koff));
 #pragma unroll
     for (int d = 0; d < 4; ++d) r.kv[d] = kb[(size_t)d * kstr];
+}
+/* The values of the same chunk (needed only after the scores and the
+ * softmax): issued once the unit's q/k/v have arrived, so the q/k/v reads
+ * queue behind the keys only. */
+__device__ __forceinline__ void attn_load_v(int tid, const g2_step_layer &y, att_regs &r, bool on, int h,
+                                            int ch, int E, int S)
+{
+    long koff, voff[4];
+    g2p_attn_offsets(tid & 255, on, h, ch, E, S, &koff, voff);
 #pragma unroll
     for (int e = 0; e < 4; ++e) r.vv[e] = *gl((const f32x4 *)(y.v_cache + voff[e]));
 }
@@ -729,7 +739,7 @@ __device__ __forceinline__ void attn_compute(int tid, const ctx &c, float scale,
  * barriers. */
 __device__ __forceinline__ void attn_chunk(int tid, const ctx &c, float scale, const u64 *src, int qo,
                                            int ko, int vo, u64 *pout, att_lds &L, att_regs &r, bool on,
-                                           int ch, int pos, int T)
+                                           int ch, int pos, int T, const g2_step_layer &y, int h, int E, int S)
 {
     const int t = tid & 255;
     /* q, k and v of the head at this position: src[qo + d], src[ko + d],
@@ -743,6 +753,7 @@ __device__ __forceinline__ void attn_chunk(int tid, const ctx &c, float scale, c
         dst[d] = ll_val(v[0]);
     }
     __syncthreads();
+    attn_load_v(tid, y, r, on, h, ch, E, S);
     attn_compute(tid, c, scale, pout, L, r, on, ch, pos, T);
 }
 
@@ -1025,7 +1036,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 attn_load(tid, y, ar[0], on, h, ch, pos, T, E, S);
                 attn_chunk(tid, c, a.scale, R, h * 64, E + h * 64, 2 * E + h * 64,
                                   R + G2X_ATT(E) + ((size_t)h * G2_STEP_MAXCH + ch) * 66, att[hf], ar[0],
-                                  on, ch, pos, T);
+                                  on, ch, pos, T, y, h, E, S);
                 __syncthreads();
             }
             TRACE(3);
