@@ -1069,6 +1069,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         }
         {
             const int tid = fresh_tid();
+            TRACE(16);
             if (wg < NH) load_set<UMAX>(tid, wa, make_plan(y.fc_w, sh.fc), 0);
             TRACE(4);
         }

@@ -23,7 +23,7 @@ SLOTS = {
     0: "layer start (X2 fetch issued)", 1: "X2 in", 11: "LayerNorm 1 done", 12: "qkv dots done",
     2: "q/k/v published", 3: "attention units done", 4: "head merge done", 5: "O in", 6: "X1 published",
     7: "X1 in", 13: "LayerNorm 2 done", 14: "fc dots done", 8: "H published", 9: "H in", 15: "fc2 dots done",
-    10: "X2 published",
+    10: "X2 published", 16: "O published",
 }
 ORDER = [0, 1, 11, 12, 2, 3, 4, 5, 6, 7, 13, 14, 8, 9, 15, 10]
 
@@ -53,10 +53,16 @@ def summary(path, heads):
         out.append(f"  {SLOTS[a]:30s} -> {SLOTS[b]:30s} {d:6.2f}")
     nxt = np.median(f[:, 2:L - 1, 0] - f[:, 1:L - 2, 10])
     out.append(f"  {SLOTS[10]:30s} -> {'next layer start':30s} {nxt:6.2f}")
-    out.append("hand-offs (median consumer in - last producer's publish | last - median producer), us:")
     hops = [("X2 -> qkv", 10, 1, slice(None), 1), ("q/k/v -> attention", 2, 3, slice(None), 0),
-            ("O -> proj", 4, 5, slice(0, heads), 0), ("X1 -> fc", 6, 7, slice(heads, None), 0),
+            ("O -> proj", 16, 5, slice(0, heads), 0), ("X1 -> fc", 6, 7, slice(heads, None), 0),
             ("H -> fc2", 8, 9, slice(None), 0)]
+    # the merging work-groups: their attention units, then the wait for the
+    # head's other chunk partials and the merge, up to O published
+    m = f[:heads, mid]
+    out.append(f"head-merging work-groups (median): attention units done -> O published "
+               f"{np.median(m[..., 16] - m[..., 3]):.2f} us; last attention unit of any work-group -> "
+               f"O published {np.median(f[:heads, mid, 16] - f[:, mid, 3].max(axis=0)):.2f} us")
+    out.append("hand-offs (median consumer in - last producer's publish | last - median producer), us:")
     for name, ps, cs, prod, prev in hops:
         lat, skew = [], []
         for l in range(2, L - 1):

@@ -51,7 +51,7 @@ def run(checker, shape, ve, pos, nwg, plant=0):
 
 @pytest.mark.parametrize("shape", list(SHAPES))
 def test_step_kernel_addresses_in_bounds(checker, shape):
-    jobs = [(shape, ve, pos, nwg) for ve in (8, 4) for pos in (0, 63, 64, 511, 1022, 1023)
+    jobs = [(shape, ve, pos, nwg) for ve in (8, 4) for pos in (0, 1, 5, 63, 64, 511, 767, 1022, 1023)
             for nwg in (256,)] + [(shape, 8, 1023, nwg) for nwg in (80, 104, 304)]
     with ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 2)) as ex:
         results = list(ex.map(lambda j: (j, run(checker, *j)), jobs))
