@@ -200,62 +200,73 @@ __device__ __forceinline__ void settle(const ctx &c, const u64 *src, u64 (&v)[NP
     }
 }
 
-/* All threads: dst[w] = value of src[w] for w < n <= NP*NT once it carries
- * the tag (thread tid takes w = tid + NT*i).
- *
- * Vectors of up to 4 words per thread (n <= 2048): after one speculative
- * read, each thread polls its own stale words until they carry the tag; a
- * word is then seen one round trip after it lands.  Larger vectors must not
- * flood the memory system (a 6400-word vector re-read by every work-group
- * each round trip would be ~13 MB of coherent reads per round, competing
- * with the weight stream), so a work-group that found stale words waits on
- * nsent sentinel words only (word n*k/nsent for k < nsent: the first word
- * of each producer when n is split evenly over nsent producers), then
- * re-reads just its stale words.  Ends with a barrier; `flag` is an LDS
- * word of the caller. */
-template <int NP>
-__device__ __forceinline__ void fetch(int tid, const ctx &c, const u64 *src, int n, int nsent,
-                                      float *dst, lds_flag *flag)
+/* Two tagged words src[w], src[w + 1] (w even) with one 16-byte load, with
+ * the cache policy of ll_get (sc1: read at the coherence point, as the
+ * relaxed agent-scope loads are), through a buffer resource over the
+ * vector; each 8-byte word of the pair is read whole.  The low halves (.x,
+ * .z) are the values, the high halves (.y, .w) the tags: half the requests
+ * of word-wise reads. */
+__device__ __forceinline__ u32x4 ll_get2(__amdgpu_buffer_rsrc_t r, int w)
 {
-    const u64 filler = (u64)c.tag << 32;
-    u64 v[NP];
-#pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        const int w = tid + NT * i;
-        v[i] = w < n ? ll_get(src + w) : filler;
-    }
-    if constexpr (NP <= 4) {
-        (void)nsent;
-        (void)flag;
-        settle(c, src, v, [&](int i) { const int w = tid + NT * i; return w < n ? w : -1; });
-#pragma unroll
-        for (int i = 0; i < NP; ++i) {
-            const int w = tid + NT * i;
-            if (w < n) dst[w] = ll_val(v[i]);
-        }
-        __syncthreads();
-        return;
-    }
-    if (tid == 0) *flag = 0;
-    __syncthreads();
+    return __builtin_amdgcn_raw_buffer_load_b128(r, w * 8, 0, 16 /* sc1 */);
+}
+__device__ __forceinline__ bool pair_stale(const u32x4 &v, unsigned tag) { return v.y != tag || v.w != tag; }
+
+/* settle (above) for word pairs: pair i starts at word idx(i) (< 0: an
+ * unused slot, which holds a current filler) */
+template <int NP2, typename IDX>
+__device__ __forceinline__ void settle2(const ctx &c, __amdgpu_buffer_rsrc_t r, u32x4 (&v)[NP2], IDX idx)
+{
     unsigned bad = 0;
 #pragma unroll
-    for (int i = 0; i < NP; ++i) bad |= (unsigned)(ll_tag(v[i]) != c.tag);
-    if (bad) *flag = 1;
-    __syncthreads();
-    if (*flag && !*c.dead) {
-        if (tid < nsent) {
-            const int w = (int)(((long)n * tid) / nsent);
-            u64 sv[1] = {ll_get(src + w)};
-            settle(c, src, sv, [&](int) { return w; });
-        }
-        __syncthreads();
-        settle(c, src, v, [&](int i) { const int w = tid + NT * i; return w < n ? w : -1; });
-    }
+    for (int i = 0; i < NP2; ++i) bad |= (unsigned)pair_stale(v[i], c.tag);
+    if (!bad || *c.dead) return;
+    const u64 t0 = wall_clock64();
+    for (;;) {
+        __builtin_amdgcn_s_sleep(4);
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-        const int w = tid + NT * i;
-        if (w < n) dst[w] = ll_val(v[i]);
+        for (int i = 0; i < NP2; ++i) {
+            const int w = idx(i);
+            if (w >= 0 && pair_stale(v[i], c.tag)) v[i] = ll_get2(r, w);
+        }
+        bad = 0;
+#pragma unroll
+        for (int i = 0; i < NP2; ++i) bad |= (unsigned)pair_stale(v[i], c.tag);
+        if (!bad || *c.dead) return;
+        /* the abort word is consulted only by waits that already took long */
+        const u64 el = wall_clock64() - t0;
+        if (el > ABORT_CHECK_AFTER) {
+            if (ll_tag(ll_get(c.abort_w)) == c.tag) { *c.dead = 1; return; }
+            if (el > WAIT_LIMIT) { give_up(c); return; }
+        }
+    }
+}
+
+/* All threads: dst[w] = value of src[w] for w < n once it carries the tag,
+ * read by 16-byte word pairs (n <= 2*NT*NP2 <= 4*NT even, src at an even
+ * word): thread tid takes pairs tid + NT*i (words 2p, 2p + 1) after one
+ * speculative read and polls its own stale pairs, so a word is seen one
+ * round trip after it lands.  Ends with a barrier. */
+template <int NP2>
+__device__ __forceinline__ void fetch2(int tid, const ctx &c, const u64 *src, int n, float *dst)
+{
+    static_assert(NP2 <= 2, "small vectors only");
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, n * 8, 0x00020000);
+    const u32x4 filler = (u32x4){0u, c.tag, 0u, c.tag};
+    u32x4 v[NP2];
+#pragma unroll
+    for (int i = 0; i < NP2; ++i) {
+        const int w = 2 * (tid + NT * i);
+        v[i] = w < n ? ll_get2(r, w) : filler;
+    }
+    settle2(c, r, v, [&](int i) { const int w = 2 * (tid + NT * i); return w < n ? w : -1; });
+#pragma unroll
+    for (int i = 0; i < NP2; ++i) {
+        const int w = 2 * (tid + NT * i);
+        if (w < n) {
+            dst[w] = __uint_as_float(v[i].x);
+            dst[w + 1] = __uint_as_float(v[i].z);
+        }
     }
     __syncthreads();
 }
@@ -319,13 +330,16 @@ __device__ __forceinline__ void settle4(const ctx &c, __amdgpu_buffer_rsrc_t r, 
     }
 }
 
-/* fetch (above) for a vector of plain values, n a multiple of 4 (n_embd is
- * a multiple of 64, the ffn width of the weight chunk), src 16-byte
- * aligned: thread tid takes quads tid + NT*i.  With more than one quad per
- * thread a work-group that found empty values first waits on the quads
- * holding value n*k/nsent, k < nsent (the first value of each producer when
- * n is split evenly over nsent producers), then re-reads its empty quads.
- * dst (LDS) is 16-byte aligned. */
+/* All threads: dst[w] = src[w] for w < n once no value is empty, for a
+ * vector of plain values, n a multiple of 4 (n_embd is a multiple of 64,
+ * the ffn width of the weight chunk), src 16-byte aligned: thread tid takes
+ * quads tid + NT*i.  With one quad per thread each thread polls its own
+ * empty quad.  Larger vectors must not flood the memory system (the
+ * 6400-value H vector is read by every work-group), so a work-group that
+ * found empty values first waits on the quads holding value n*k/nsent,
+ * k < nsent (the first value of each producer when n is split evenly over
+ * nsent producers), then re-reads its empty quads.  dst (LDS) is 16-byte
+ * aligned.  Ends with a barrier; `flag` is an LDS word of the caller. */
 template <int NQ>
 __device__ __forceinline__ void fetch4(int tid, const ctx &c, const float *src, int n, int nsent, float *dst,
                                        lds_flag *flag)
@@ -743,14 +757,17 @@ __device__ __forceinline__ void attn_chunk(int tid, const ctx &c, float scale, c
 {
     const int t = tid & 255;
     /* q, k and v of the head at this position: src[qo + d], src[ko + d],
-     * src[vo + d] */
-    if (on && t < 192) {
-        const int part = t >> 6, d = t & 63;
+     * src[vo + d], as word pairs (qo, ko, vo and the region are at even
+     * words) */
+    if (on && t < 96) {
+        const int part = t >> 5, d = 2 * (t & 31);
         const int w = (part == 0 ? qo : (part == 1 ? ko : vo)) + d;
-        u64 v[1] = {ll_get(src + w)};
-        settle(c, src, v, [&](int) { return w; });
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, (vo + 64) * 8, 0x00020000);
+        u32x4 v[1] = {ll_get2(rs, w)};
+        settle2(c, rs, v, [&](int) { return w; });
         float *dst = part == 0 ? L.q : (part == 1 ? L.kn : L.vn);
-        dst[d] = ll_val(v[0]);
+        dst[d] = __uint_as_float(v[0].x);
+        dst[d + 1] = __uint_as_float(v[0].z);
     }
     __syncthreads();
     attn_load_v(tid, y, r, on, h, ch, E, S);
@@ -892,7 +909,7 @@ __device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, con
 
     /* ---- greedy pick (g2k_argmax_merge with advance) */
     __syncthreads();
-    fetch<2>(tid, c, AM, 2 * nwg, nwg, xin, flag);
+    fetch2<1>(tid, c, AM, 2 * nwg, xin); /* nwg <= NT work-groups' word pairs */
     const u64 abort_seen = tid == 0 ? ll_get(c.abort_w) : 0; /* issued ahead of the merge */
     bv = -INFINITY;
     bi = 0x7fffffff;
@@ -932,7 +949,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     __shared__ volatile int flag;
 
     constexpr int NQE = (G2_STEP_MAXE + 4 * NT - 1) / (4 * NT);    /* its value quads      */
-    constexpr int NPM = (G2_STEP_MAXCH * 66 + NT - 1) / NT;        /* a head's partials    */
+    constexpr int NPM2 = (G2_STEP_MAXCH * 66 + 2 * NT - 1) / (2 * NT); /* a head's partials, in pairs */
     const int wg = blockIdx.x, nwg = gridDim.x;
     const int E = a.E, F = a.F, NH = a.NH, S = a.S, V = a.V;
     const int pos = clampi(a.state[G2S_POS], 0, S - 1);
@@ -1049,7 +1066,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         for (int h = wg; h < NH; h += nwg) {
             const int tid = fresh_tid();
             const u64 *hp = R + G2X_ATT(E) + (size_t)h * G2_STEP_MAXCH * 66;
-            fetch<NPM>(tid, c, hp, nch * 66, nch, xin, (lds_flag *)&flag);
+            fetch2<NPM2>(tid, c, hp, nch * 66, xin); /* 66 words per chunk: even, at even words */
             float Ls = 0.f;
             if (tid < 64) {
                 const float mc = tid < nch ? xin[tid * 66] : -INFINITY;

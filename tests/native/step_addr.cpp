@@ -187,10 +187,11 @@ int main(int argc, char **argv)
                     g2p_attn_offsets(t, on, h, ch, E, S, &koff, voff);
                     for (int d = 0; d < 4; ++d) chk("K cache load", koff + (long)d * S, koff + (long)d * S + 4, (long)E * S);
                     for (int e = 0; e < 4; ++e) chk("V cache load", voff[e], voff[e] + 4, (long)S * E);
-                    if (on && t < 192) {
-                        const int part = t >> 6, d = t & 63;
+                    if (on && t < 96) {
+                        const int part = t >> 5, d = 2 * (t & 31);
                         const long w = (part == 0 ? 0 : (part == 1 ? E : 2 * E)) + h * 64 + d;
-                        chk("q/k/v word of a unit", R + w, R + w + 1, R + G2X_ATT(E));
+                        chk("q/k/v word pair of a unit", R + w, R + w + 2, R + G2X_ATT(E));
+                        if ((R + w) & 1) chk("q/k/v word pair at an even word", 0, 1, 0);
                     }
                     if (on && t < 66) {
                         const long pw = R + G2X_ATT(E) + ((long)h * G2_STEP_MAXCH + ch) * 66 + t;
@@ -201,6 +202,7 @@ int main(int argc, char **argv)
             for (int h = (int)wg; h < NH; h += nwg) {
                 const long hp = R + G2X_ATT(E) + (long)h * G2_STEP_MAXCH * 66;
                 chk("merge partial reads", hp, hp + (long)nch * 66, R + att_end);
+                if ((hp & 1) || ((nch * 66) & 1)) chk("merge partials as word pairs", 0, 1, 0);
                 vstore("O values", l, vO, h * 64, h * 64 + 64, vX1);
             }
             /* PROJ, FC, FC2 */
@@ -229,6 +231,8 @@ int main(int argc, char **argv)
         chk("logits", pl.r0, pl.r0 + pl.nrows, V);
         const long AM = G2X_HEAD + (long)L * xlayer;
         chk("argmax words", AM + 2 * wg, AM + 2 * wg + 2, G2X_ARRIVE(L, xlayer, nwg));
+        if (AM & 1) chk("argmax words as word pairs", 0, 1, 0);
+        if (nwg > NT) chk("argmax word pairs, one per thread", 0, 1, 0);
     }
     /* the proj rows of the non-merging work-groups cover every row once */
     if (proj_rows != (long)L * E) chk("proj rows covered once", 0, 1, 0);
