@@ -307,7 +307,9 @@ typedef struct {
 /* Causal attention over a prompt block: rows i < P of q[P,E]; keys/values
  * j <= i, head dim 64: g2k_attn_prefill_mfma reads them from the transposed
  * K cache and the V cache, g2k_attn_prefill_h16 from the fp16 halves the
- * qkv epilogue wrote (kh, kl [S][E]; vth, vtl [E][S]). */
+ * qkv epilogue wrote (kh, kl [S][E]; vth, vtl [E][S]).  Grid: 1-D, 8 *
+ * ceil(NH / 8) * ceil(P / 64) work-groups of 512 threads, every query
+ * block of head h on XCD h % 8. */
 typedef struct {
     const float *q;
     const float *k_cache;

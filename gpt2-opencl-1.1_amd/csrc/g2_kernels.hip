@@ -1309,6 +1309,19 @@ __device__ __forceinline__ float row16_sum(float v)
     return v + apf_dpp<0x121>(v);
 }
 
+/* Work-group -> (head, 64-row query block) of the prompt attention: the
+ * grid is 1-D, 8 * ceil(NH / 8) * nqb work-groups, and work-group w runs on
+ * XCD w % 8 (consecutive work-groups go to consecutive XCDs), so every query
+ * block of head h runs on XCD h % 8, whose L2 then fetches that head's keys
+ * and values once for all of them.  Work-groups past the last head have no
+ * work. */
+__device__ __forceinline__ void attnp_block(const g2_attnp_args &a, int &h, int &qb)
+{
+    const int nqb = (a.P + 63) / 64, k = (int)blockIdx.x >> 3;
+    h = ((int)blockIdx.x & 7) + 8 * (k / nqb);
+    qb = k % nqb;
+}
+
 extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_mfma(const g2_attnp_args a)
 {
     /* The tiles are stored so that a lane's operands of all four 16-wide
@@ -1322,7 +1335,9 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_mfma(const g2
     __shared__ __attribute__((aligned(16))) float Kt[2][64 * LD]; /* per half [dim][pk(key)] */
     __shared__ __attribute__((aligned(16))) float Vs[2][64 * LD]; /* per half [key][pk(dim)] */
     __shared__ __attribute__((aligned(16))) float Ps[8][16 * LDP]; /* per wave [row][pp(key)] */
-    const int h = blockIdx.x, qb = blockIdx.y, tid = threadIdx.x;
+    int h, qb;
+    attnp_block(a, h, qb);
+    const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
     /* wave w: row group rg = w % 4 (query rows 16 rg..16 rg + 15 of the
      * block) over the key blocks of its half hs = w / 4 (kb = hs, hs + 2,
@@ -1572,7 +1587,9 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
     constexpr int TB = 2 * TILE;  /* its bytes */
     /* stage b of half hs: Kh, Kl, Vh, Vl at (4 (2 hs + b) + 0..3) * TILE */
     __shared__ __attribute__((aligned(1024))) _Float16 kvs[16 * TILE];
-    const int h = blockIdx.x, qb = blockIdx.y, tid = threadIdx.x;
+    int h, qb;
+    attnp_block(a, h, qb);
+    const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
     const int rg = wave & 3, hs = wave >> 2;
     if (h >= a.NH || qb * 64 >= a.P) return;

@@ -982,7 +982,9 @@ static int fused_prefill(g2_model *m, int P)
                             : g2i_launch(f_qkv, cdivu(3 * E, 64), cdivu(P, 64), 256, &g);
         g2_attnp_args t = { m->q, y->k_cache, y->v_cache, m->attn, P, E, NH, G2_KV_MAX_SEQ, 1.0f / sqrtf(64.0f),
                             big ? at_h : NULL, big ? at_l : NULL, kv_kh, kv_kl, kv_vh, kv_vl };
-        if (!rc) rc = g2i_launch(attn32 ? G2F_ATTN_PREFILL_MFMA : G2F_ATTN_PREFILL_H16, (unsigned)NH, cdivu(P, 64), 512, &t);
+        /* 1-D grid: 8 XCDs x ceil(NH / 8) heads x query blocks (attnp_block) */
+        if (!rc) rc = g2i_launch(attn32 ? G2F_ATTN_PREFILL_MFMA : G2F_ATTN_PREFILL_H16, 8 * cdivu(NH, 8) * cdivu(P, 64), 1,
+                                 512, &t);
         memset(&g, 0, sizeof g);
         g.A = m->attn; g.B = y->proj_w; g.bias = y->proj_b; g.C = m->hidden; g.M = P; g.N = E; g.K = E;
         int ln2_done = 0;
