@@ -66,7 +66,8 @@ extern "C" {
     X(LAYERNORM_SPLIT, "g2k_layernorm_split") X(SPLITK_RESID_LN, "g2k_splitk_resid_ln") \
     X(SGEMM_GELU, "g2k_sgemm_gelu") X(SGEMM_RESID, "g2k_sgemm_resid")         \
     X(SGEMM_QKV, "g2k_sgemm_qkv") X(SGEMM_PARTIAL, "g2k_sgemm_partial")       \
-    X(SPLITK_EPI, "g2k_splitk_epi")
+    X(SPLITK_EPI, "g2k_splitk_epi")                                           \
+    X(LN_FOLD_F32, "g2k_ln_fold_f32") X(LN_FOLD_F16, "g2k_ln_fold_f16")
 
 #define G2_ENUM_ENTRY(id, name) G2F_##id,
 enum { G2_KERNEL_LIST(G2_ENUM_ENTRY) G2F_COUNT };

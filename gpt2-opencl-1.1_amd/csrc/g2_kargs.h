@@ -237,9 +237,13 @@ typedef struct {
  * G2V_* offsets and sized with G2V_TOTAL_FLOATS, for the four vectors every
  * work-group reads whole (O, X1, H, X2). */
 typedef struct {
-    const float *ln1_w, *ln1_b, *qkv_b, *proj_b, *ln2_w, *ln2_b, *fc_b, *fc2_b;
+    const float *ln1_w, *proj_b, *ln2_w, *fc2_b;
     const void *qkv_w, *proj_w, *fc_w, *fc2_w;
     float *k_cache, *v_cache;
+    /* the LayerNorm folded into the matrix that follows it (g2k_ln_fold):
+     * c1[r] = W[r,:] . gamma, c2[r] = W[r,:] . beta + bias[r] for qkv (ln_1,
+     * qkv bias) and fc (ln_2, fc bias); the gains ln1_w, ln2_w scale x */
+    const float *qkv_c1, *qkv_c2, *fc_c1, *fc_c2;
 } g2_step_layer;
 
 typedef struct {
@@ -248,7 +252,7 @@ typedef struct {
     const void *wpe;
     const void *lm_w;
     const float *lnf_w;
-    const float *lnf_b;
+    const float *lm_c1, *lm_c2; /* ln_f folded into the lm_head (no bias) */
     float *logits;
     int *state;
     unsigned long long *xbuf;
@@ -269,6 +273,20 @@ typedef struct {
 } g2_step_args;
 
 #define G2_TRACE_STRIDE(L) (24 * (L) + 8)
+
+/* A LayerNorm folded into the matrix W[N,K] (output-major, f32 or f16 by
+ * kernel variant) it feeds: c1[r] = sum_k W[r,k] gamma[k] and c2[r] =
+ * sum_k W[r,k] beta[k] + bias[r] (bias may be NULL), each summed in double
+ * in a fixed order and rounded once.  Then W . LayerNorm(x) + bias =
+ * inv * (W . ((x - s) * gamma) - (mean - s) * c1) + c2 for any shift s,
+ * inv = 1 / sqrt(var + eps).  Grid ceil(N / 4), 256 threads (a row per
+ * wave). */
+typedef struct {
+    const void *W;
+    const float *gamma, *beta, *bias;
+    float *c1, *c2;
+    int N, K;
+} g2_lnfold_args;
 
 #define G2_STEP_THREADS 512
 #define G2_STEP_MAXE 1600   /* largest n_embd the step kernel holds in LDS */

@@ -1776,6 +1776,32 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
     }
 }
 
+/* g2_lnfold_args: a row of W per wave, each lane summing k = lane, lane +
+ * 64, ... in double, then the lanes in a fixed butterfly order. */
+template <typename WT>
+__device__ __forceinline__ void ln_fold_impl(const g2_lnfold_args &a)
+{
+    const int lane = threadIdx.x & 63, r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= a.N) return; /* wave-uniform */
+    const WT *w = (const WT *)a.W + (size_t)r * a.K;
+    double s1 = 0.0, s2 = 0.0;
+    for (int k = lane; k < a.K; k += 64) {
+        const double wv = (double)(float)w[k];
+        s1 += wv * (double)a.gamma[k];
+        s2 += wv * (double)a.beta[k];
+    }
+    for (int o = 32; o > 0; o >>= 1) {
+        s1 += __shfl_xor(s1, o);
+        s2 += __shfl_xor(s2, o);
+    }
+    if (lane == 0) {
+        a.c1[r] = (float)s1;
+        a.c2[r] = (float)(s2 + (a.bias ? (double)a.bias[r] : 0.0));
+    }
+}
+G2K void g2k_ln_fold_f32(const g2_lnfold_args a) { ln_fold_impl<float>(a); }
+G2K void g2k_ln_fold_f16(const g2_lnfold_args a) { ln_fold_impl<_Float16>(a); }
+
 /* Fused decode kernels (packed matvecs, single-query attention). */
 #include "g2_decode.hip"
 

@@ -58,6 +58,7 @@ struct g2_model {
     size_t xbuf_bytes;
     float *xval;
     size_t xval_floats;
+    float *lnfold; /* per layer qkv c1, c2 [3E], fc c1, c2 [F]; then lm c1, c2 [V] */
     int step_wgs;  /* grid of the step kernel, 0 if this model cannot use it */
     int step_on;   /* decode steps run the step kernel */
     int plain;     /* launches are plain, not cooperative (2-4: test modes of the
@@ -74,6 +75,8 @@ struct g2_model {
 };
 
 /* ---------------------------------------------------------------- helpers */
+
+static unsigned cdivu(long a, long b) { return (unsigned)((a + b - 1) / b); }
 
 static int dev_alloc(g2_model *m, void **p, size_t bytes, int is_weight)
 {
@@ -195,16 +198,31 @@ static int step_setup(g2_model *m)
     if (!step_supported(m, nwg, &m->step_why)) return G2_OK;
     const g2_config *c = &m->cfg;
     const int L = c->n_layer;
+    const size_t E = (size_t)c->n_embd, F = (size_t)c->ffn_dim, V = (size_t)c->vocab_size;
+    const size_t per_layer = 6 * E + 2 * F;
+    int rc = dev_alloc(m, (void **)&m->lnfold, ((size_t)L * per_layer + 2 * V) * 4, 0);
+    if (rc) return rc;
     g2_step_layer *t = calloc((size_t)L, sizeof *t);
     if (!t) return g2i_err(G2_E_NOMEM, "step layer table");
-    for (int l = 0; l < L; ++l) {
+    const int ffold = m->dtype == G2_F16 ? G2F_LN_FOLD_F16 : G2F_LN_FOLD_F32;
+    for (int l = 0; l < L && !rc; ++l) {
         const g2_layer *y = &m->L[l];
-        t[l].ln1_w = y->ln1_w; t[l].ln1_b = y->ln1_b; t[l].qkv_b = y->qkv_b; t[l].proj_b = y->proj_b;
-        t[l].ln2_w = y->ln2_w; t[l].ln2_b = y->ln2_b; t[l].fc_b = y->fc_b; t[l].fc2_b = y->fc2_b;
+        float *f = m->lnfold + (size_t)l * per_layer;
+        t[l].ln1_w = y->ln1_w; t[l].proj_b = y->proj_b; t[l].ln2_w = y->ln2_w; t[l].fc2_b = y->fc2_b;
         t[l].qkv_w = y->qkv_w; t[l].proj_w = y->proj_w; t[l].fc_w = y->fc_w; t[l].fc2_w = y->fc2_w;
         t[l].k_cache = y->k_cache; t[l].v_cache = y->v_cache;
+        t[l].qkv_c1 = f; t[l].qkv_c2 = f + 3 * E; t[l].fc_c1 = f + 6 * E; t[l].fc_c2 = f + 6 * E + F;
+        g2_lnfold_args q = { y->qkv_w, y->ln1_w, y->ln1_b, y->qkv_b, f, f + 3 * E, (int)(3 * E), (int)E };
+        rc = g2i_launch(ffold, cdivu((long)(3 * E), 4), 1, 256, &q);
+        g2_lnfold_args u = { y->fc_w, y->ln2_w, y->ln2_b, y->fc_b, f + 6 * E, f + 6 * E + F, (int)F, (int)E };
+        if (!rc) rc = g2i_launch(ffold, cdivu((long)F, 4), 1, 256, &u);
     }
-    int rc = dev_alloc(m, (void **)&m->step_layers, (size_t)L * sizeof *t, 0);
+    if (!rc) {
+        float *f = m->lnfold + (size_t)L * per_layer;
+        g2_lnfold_args u = { m->lm_w, m->lnf_w, m->lnf_b, NULL, f, f + V, (int)V, (int)E };
+        rc = g2i_launch(ffold, cdivu((long)V, 4), 1, 256, &u);
+    }
+    if (!rc) rc = dev_alloc(m, (void **)&m->step_layers, (size_t)L * sizeof *t, 0);
     if (!rc) rc = up(m->step_layers, t, (size_t)L * sizeof *t);
     free(t);
     /* A cooperative launch costs ~17 us more than a plain one between
@@ -303,7 +321,7 @@ int g2_model_free(g2_model *m)
     void *bufs[] = { m->wte, m->wpe, m->lnf_w, m->lnf_b, m->lm_head, m->hidden, m->ln_out,
                      m->attn, m->attn_proj, m->ffn1, m->ffn2, m->qkv_new, m->qkv_full,
                      m->last_hidden, m->logits, m->partial, m->scores, m->q, m->ids_dev,
-                     m->state, m->att_part, m->am_part, m->step_layers, m->xbuf, m->xval, m->trace, m->pf_part,
+                     m->state, m->att_part, m->am_part, m->step_layers, m->xbuf, m->xval, m->lnfold, m->trace, m->pf_part,
                      m->pf_kv };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; ++i)
         if (bufs[i]) hipFree(bufs[i]);
@@ -676,7 +694,6 @@ static int ref_decode(g2_model *m, int pos)
 
 /* ------------------------------------------------------------- fused path */
 
-static unsigned cdivu(long a, long b) { return (unsigned)((a + b - 1) / b); }
 
 static int launch_rows(g2_model *m, int fid_f32_64, g2_rows_args *a)
 {
@@ -748,7 +765,9 @@ static int step_launch(g2_model *m)
     g2_step_args a;
     memset(&a, 0, sizeof a);
     a.layers = m->step_layers; a.wte = m->wte; a.wpe = m->wpe; a.lm_w = m->lm_w;
-    a.lnf_w = m->lnf_w; a.lnf_b = m->lnf_b; a.logits = m->logits; a.state = m->state;
+    a.lnf_w = m->lnf_w; a.logits = m->logits; a.state = m->state;
+    a.lm_c1 = m->lnfold + (size_t)c->n_layer * (6 * (size_t)c->n_embd + 2 * (size_t)c->ffn_dim);
+    a.lm_c2 = a.lm_c1 + c->vocab_size;
     a.xbuf = m->xbuf;
     a.xval = m->xval;
     a.trace = m->trace;

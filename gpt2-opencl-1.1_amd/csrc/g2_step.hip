@@ -46,6 +46,10 @@
  *   FC2   H -> fc2 rows + bias + X1 -> X2
  * then LM (LayerNorm + logits over the tied head + per-work-group first-max)
  * and the greedy pick by work-group 0, which advances the device state.
+ * Each LayerNorm is folded into the matrix that follows it (ln_fold_in):
+ * the dot products start on (x - x[0]) * gain while the statistics are
+ * reduced, and each row is corrected after them with the per-row sums
+ * c1 = W . gain, c2 = W . bias_ln + bias computed once per model.
  *
  * Every wait is bounded in time: a wait that runs out (100 ms) sets
  * G2_ERR_STEP_TIMEOUT in the state and raises the abort word, after which
@@ -403,36 +407,38 @@ __device__ __forceinline__ f32x4 fetch_q(int tid, const ctx &c, const float *src
     return __builtin_bit_cast(f32x4, v[0]);
 }
 
-/* LayerNorm gain and bias of the thread's quad (clamped: quads past E are
- * never stored), loaded at the start of a phase so their latency overlaps
- * the input wait. */
-struct ln_quad {
-    f32x4 g, b;
-};
-__device__ __forceinline__ ln_quad ln_qload(int tid, const float *g, const float *b, int E)
+/* LayerNorm gain of the thread's quad (clamped: quads past E are never
+ * stored), loaded at the start of a phase so its latency overlaps the input
+ * wait; the bias is folded into the matrix's c2. */
+__device__ __forceinline__ f32x4 ln_gload(int tid, const float *g, int E)
 {
-    const int q = min(tid, E / 4 - 1);
-    return ln_quad{gl((const f32x4 *)g)[q], gl((const f32x4 *)b)[q]};
+    return gl((const f32x4 *)g)[min(tid, E / 4 - 1)];
 }
 
-/* xin = LayerNorm(x) over E entries, x held as quads in registers (thread
- * tid: entries 4tid .. 4tid + 3, x0 = x[0]): (x - mean) * inv_std * g + b
- * with the biased variance, eps 1e-5 (layernorm, math.cl:283-311).  One
- * block reduction: every thread sums d = x - x0 and d^2 over its quad (a
- * shift that keeps the variance E[d^2] - E[d]^2 free of cancellation when
- * |mean| >> std); the two sums are reduced together, wave totals added in
- * wave order.  Ends with a barrier. */
-__device__ __forceinline__ void layernorm_q(int tid, const f32x4 &x, float x0, const ln_quad &lp, int E,
-                                            float *xin, float *red)
+/* The LayerNorm folded into the matrix that follows it (layernorm,
+ * math.cl:283-311: (x - mean) * inv_std * g + b with the biased variance,
+ * eps 1e-5), by W . LN(x) + bias = inv * (W . ((x - x0) * g) - (mean - x0) *
+ * c1) + c2 with c1 = W . g, c2 = W . b + bias (g2k_ln_fold), x0 = x[0].
+ * ln_fold_in writes the matrix input (x - x0) * g of the thread's quad
+ * (entries 4tid .. 4tid + 3 of x, held in registers) to xin and each wave's
+ * sums of d = x - x0 and d^2 to red (a shift that keeps the variance E[d^2]
+ * - E[d]^2 free of cancellation when |mean| >> std); ends with a barrier,
+ * after which the dot products may start while ln_fold_stats reads the
+ * sums (wave totals added in wave order). */
+__device__ __forceinline__ void ln_fold_in(int tid, const f32x4 &x, float x0, const f32x4 &g, int E, float *xin,
+                                           float *red)
 {
     const bool on = 4 * tid < E;
     float s = 0.f, q = 0.f;
+    f32x4 o;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
         const float d = on ? x[e] - x0 : 0.f;
         s += d;
         q = fmaf(d, d, q);
+        o[e] = d * g[e];
     }
+    if (on) *(f32x4 *)(xin + 4 * tid) = o;
     s = wsum(s);
     q = wsum(q);
     if ((tid & 63) == 0) {
@@ -440,23 +446,28 @@ __device__ __forceinline__ void layernorm_q(int tid, const f32x4 &x, float x0, c
         red[NW + (tid >> 6)] = q;
     }
     __syncthreads();
+}
+struct ln_st {
+    float md, inv; /* mean - x0, 1 / sqrt(var + eps) */
+};
+__device__ __forceinline__ ln_st ln_fold_stats(const float *red, int E)
+{
     float S = red[0], Q = red[NW];
 #pragma unroll
     for (int w = 1; w < NW; ++w) {
         S += red[w];
         Q += red[NW + w];
     }
-    const float md = S / (float)E;
-    const float mean = x0 + md;
-    const float var = fmaxf(Q / (float)E - md * md, 0.f);
-    const float inv = 1.0f / sqrtf(var + 1e-5f);
-    if (on) {
-        f32x4 o;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = fmaf((x[e] - mean) * inv, lp.g[e], lp.b[e]);
-        *(f32x4 *)(xin + 4 * tid) = o;
-    }
-    __syncthreads();
+    ln_st st;
+    st.md = S / (float)E;
+    const float var = fmaxf(Q / (float)E - st.md * st.md, 0.f);
+    st.inv = 1.0f / sqrtf(var + 1e-5f);
+    return st;
+}
+/* row value of a folded LayerNorm from its dot product v with (x - x0) * g */
+__device__ __forceinline__ float ln_fold_out(const ln_st &st, float v, float c1, float c2)
+{
+    return fmaf(st.inv, fmaf(-st.md, c1, v), c2);
 }
 
 /* A work-group's share of one packed matrix W[N,K] (output-major): rows
@@ -881,20 +892,23 @@ __device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, con
     const int ngen = a.state[G2S_NGEN], min_new = a.state[G2S_MIN_NEW];
     const int pos = clampi(a.state[G2S_POS], 0, a.S - 1);
     const unsigned seq = (unsigned)a.state[G2S_SEQ];
-    const ln_quad lpf = ln_qload(tid, a.lnf_w, a.lnf_b, E);
+    const f32x4 gf = ln_gload(tid, a.lnf_w, E);
     const plan p = make_plan(a.lm_w, sh.lm);
+    const int rl = min(p.r0 + tid, V - 1); /* used by tid < nrows */
+    const float c1 = gl(a.lm_c1)[rl], c2 = gl(a.lm_c2)[rl];
     if (!preloaded) load_set<UMAX>(tid, wa, p, 0);
     float x0;
     const f32x4 xq = fetch_q(tid, c, xlast, E, xres, x0);
     TRACE(0);
-    layernorm_q(tid, xq, x0, lpf, E, xin, red);
+    ln_fold_in(tid, xq, x0, gf, E, xin, red);
     matvec<WT, UMAX>(tid, wa, p, xin, part);
+    const ln_st st = ln_fold_stats(red, E);
     const int masked = ngen < min_new ? G2_EOS_ID : -1;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
     if (tid < p.nrows) {
         const int r = p.r0 + tid;
-        const float v = row_sum(p, part, tid);
+        const float v = ln_fold_out(st, row_sum(p, part, tid), c1, c2);
         glw(a.logits)[r] = v;
         bv = r == masked ? -1e30f : v;
         bi = r;
@@ -1005,13 +1019,15 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         u64 *R = X + (size_t)l * a.xlayer;
         float *RV = XV + 2 * VR * l, *RN = XN + 2 * VR * l;
 
-        /* ---- QKV: LayerNorm(x) . Wqkv + b -> q, k, v (+ KV cache) */
+        /* ---- QKV: LayerNorm(x) . Wqkv + b -> q, k, v (+ KV cache), the
+         * LayerNorm folded in */
         {
             const int tid = fresh_tid();
             TRACE(0);
             const plan p = make_plan(y.qkv_w, sh.qkv);
-            const ln_quad lp = ln_qload(tid, y.ln1_w, y.ln1_b, E);
-            const float bias = gl(y.qkv_b)[min(p.r0 + tid, 3 * E - 1)]; /* used by tid < nrows */
+            const f32x4 g = ln_gload(tid, y.ln1_w, E);
+            const int rq = min(p.r0 + tid, 3 * E - 1); /* used by tid < nrows */
+            const float c1 = gl(y.qkv_c1)[rq], c2 = gl(y.qkv_c2)[rq];
             f32x4 xq;
             float x0;
             if (l > 0) {
@@ -1021,9 +1037,10 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 x0 = xres[0];
             }
             TRACE(1);
-            layernorm_q(tid, xq, x0, lp, E, xin, red);
+            ln_fold_in(tid, xq, x0, g, E, xin, red);
             TRACE(11);
             matvec<WT, UMAX>(tid, wa, p, xin, part);
+            const ln_st st = ln_fold_stats(red, E);
             TRACE(12);
             if (l == 0 && a.plain &&
                 !grid_resident(tid, c, a.xbuf + G2X_ARRIVE(a.L, a.xlayer, nwg), a.xbuf + G2X_DECISION, nwg,
@@ -1031,8 +1048,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 return;
             if (tid < p.nrows) {
                 const int r = p.r0 + tid;
-                float v = row_sum(p, part, tid);
-                v += bias;
+                const float v = ln_fold_out(st, row_sum(p, part, tid), c1, c2);
                 ll_put(R + r, v, c.tag);
                 if (r >= 2 * E) glw(y.v_cache)[(size_t)pos * E + (r - 2 * E)] = v;
                 else if (r >= E) glw(y.k_cache)[(size_t)(r - E) * S + pos] = v;
@@ -1114,23 +1130,24 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             __syncthreads();
         }
 
-        /* ---- FC: H = gelu(LayerNorm(X1) . Wfc + b) */
+        /* ---- FC: H = gelu(LayerNorm(X1) . Wfc + b), the LayerNorm folded in */
         {
             const int tid = fresh_tid();
             const plan p = make_plan(y.fc_w, sh.fc);
-            const ln_quad lp = ln_qload(tid, y.ln2_w, y.ln2_b, E);
-            const float bias = gl(y.fc_b)[min(p.r0 + tid, F - 1)];
+            const f32x4 g = ln_gload(tid, y.ln2_w, E);
+            const int rf = min(p.r0 + tid, F - 1); /* used by tid < nrows */
+            const float c1 = gl(y.fc_c1)[rf], c2 = gl(y.fc_c2)[rf];
             float x0;
             const f32x4 xq = fetch_q(tid, c, RV + G2V_X1(E), E, xres, x0);
             TRACE(7);
-            layernorm_q(tid, xq, x0, lp, E, xin, red);
+            ln_fold_in(tid, xq, x0, g, E, xin, red);
             TRACE(13);
             matvec<WT, UMAX>(tid, wa, p, xin, part);
+            const ln_st st = ln_fold_stats(red, E);
             TRACE(14);
             if (tid < p.nrows) {
                 const int r = p.r0 + tid;
-                float v = row_sum(p, part, tid);
-                v += bias;
+                const float v = ln_fold_out(st, row_sum(p, part, tid), c1, c2);
                 vput(RV + G2V_H(E) + r, RN + G2V_H(E) + r, gelu_f(v));
             }
             TRACE(8);

@@ -167,6 +167,10 @@ int main(int argc, char **argv)
             /* QKV: rows, K/V cache stores at pos, q/k/v words */
             matrix("qkv weights", "b", 3 * E, E, VE, 4, wg, nwg);
             const g2p_rows pq = g2p_rows_plan(3 * E, E, VE, wg, nwg);
+            for (int tid = 0; tid < NT; ++tid) {
+                const int rq = g2p_min(pq.r0 + tid, 3 * E - 1);
+                chk("qkv LayerNorm fold sums", rq, rq + 1, 3L * E);
+            }
             for (int t = 0; t < pq.nrows; ++t) {
                 const int r = pq.r0 + t;
                 chk("qkv word", R + r, R + r + 1, R + G2X_ATT(E));
@@ -217,6 +221,10 @@ int main(int argc, char **argv)
             for (int b = 0; b < 2; ++b) quads("X1 fetch", vreg(l, b) + vX1, E, vreg(l, b) + vH);
             matrix("fc weights", "b", F, E, VE, 4, wg, nwg);
             const g2p_rows pf = g2p_rows_plan(F, E, VE, wg, nwg);
+            for (int tid = 0; tid < NT; ++tid) {
+                const int rf = g2p_min(pf.r0 + tid, F - 1);
+                chk("fc LayerNorm fold sums", rf, rf + 1, F);
+            }
             vstore("H values", l, vH, pf.r0, pf.r0 + pf.nrows, vX2);
             for (int b = 0; b < 2; ++b) quads("H fetch", vreg(l, b) + vH, F, vreg(l, b) + vX2);
             matrix("fc2 weights", "b", E, F, VE, 4, wg, nwg);
@@ -229,6 +237,10 @@ int main(int argc, char **argv)
         matrix("lm_head weights", nullptr, V, E, VE, 4, wg, nwg);
         const g2p_rows pl = g2p_rows_plan(V, E, VE, wg, nwg);
         chk("logits", pl.r0, pl.r0 + pl.nrows, V);
+        for (int tid = 0; tid < NT; ++tid) {
+            const int rl = g2p_min(pl.r0 + tid, V - 1);
+            chk("lm_head LayerNorm fold sums", rl, rl + 1, V);
+        }
         const long AM = G2X_HEAD + (long)L * xlayer;
         chk("argmax words", AM + 2 * wg, AM + 2 * wg + 2, G2X_ARRIVE(L, xlayer, nwg));
         if (AM & 1) chk("argmax words as word pairs", 0, 1, 0);
