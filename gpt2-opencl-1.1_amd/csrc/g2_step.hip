@@ -172,38 +172,6 @@ __device__ __noinline__ void give_up(const ctx &c)
     *c.dead = 1;
 }
 
-/* Bounded wait on a list of words already loaded into v[]: reload the ones
- * whose tag is stale (with a short back-off) until all match, the abort
- * word is raised or time runs out.  idx(i) < 0 marks an unused slot. */
-template <int NP, typename IDX>
-__device__ __forceinline__ void settle(const ctx &c, const u64 *src, u64 (&v)[NP], IDX idx)
-{
-    unsigned bad = 0;
-#pragma unroll
-    for (int i = 0; i < NP; ++i) bad |= (unsigned)(ll_tag(v[i]) != c.tag);
-    if (!bad || *c.dead) return;
-    const u64 t0 = wall_clock64();
-    for (;;) {
-        __builtin_amdgcn_s_sleep(4);
-#pragma unroll
-        for (int i = 0; i < NP; ++i) {
-            const int w = idx(i);
-            if (w >= 0 && ll_tag(v[i]) != c.tag) v[i] = ll_get(src + w);
-        }
-        bad = 0;
-#pragma unroll
-        for (int i = 0; i < NP; ++i) bad |= (unsigned)(ll_tag(v[i]) != c.tag);
-        if (!bad || *c.dead) return;
-        /* the abort word is consulted only by waits that already took long
-         * (every waiting thread reading one word would be a hot spot) */
-        const u64 el = wall_clock64() - t0;
-        if (el > ABORT_CHECK_AFTER) {
-            if (ll_tag(ll_get(c.abort_w)) == c.tag) { *c.dead = 1; return; }
-            if (el > WAIT_LIMIT) { give_up(c); return; }
-        }
-    }
-}
-
 /* Two tagged words src[w], src[w + 1] (w even) with one 16-byte load, with
  * the cache policy of ll_get (sc1: read at the coherence point, as the
  * relaxed agent-scope loads are), through a buffer resource over the
@@ -216,8 +184,10 @@ __device__ __forceinline__ u32x4 ll_get2(__amdgpu_buffer_rsrc_t r, int w)
 }
 __device__ __forceinline__ bool pair_stale(const u32x4 &v, unsigned tag) { return v.y != tag || v.w != tag; }
 
-/* settle (above) for word pairs: pair i starts at word idx(i) (< 0: an
- * unused slot, which holds a current filler) */
+/* Bounded wait on word pairs already loaded into v[]: reload the pairs
+ * whose tags are stale (with a short back-off) until all match, the abort
+ * word is raised or time runs out.  Pair i starts at word idx(i) (< 0: an
+ * unused slot, which holds a current filler). */
 template <int NP2, typename IDX>
 __device__ __forceinline__ void settle2(const ctx &c, __amdgpu_buffer_rsrc_t r, u32x4 (&v)[NP2], IDX idx)
 {
@@ -304,8 +274,9 @@ __device__ __forceinline__ bool quad_empty(const u32x4 &v)
     return v.x == G2V_EMPTY || v.y == G2V_EMPTY || v.z == G2V_EMPTY || v.w == G2V_EMPTY;
 }
 
-/* settle (above) for value quads: slot i holds quad idx(i) (< 0: an unused
- * slot, which holds a filler) */
+/* settle2 (above) for value quads, which are present once no value is
+ * G2V_EMPTY: slot i holds quad idx(i) (< 0: an unused slot, which holds a
+ * filler). */
 template <int NQ, typename IDX>
 __device__ __forceinline__ void settle4(const ctx &c, __amdgpu_buffer_rsrc_t r, u32x4 (&v)[NQ], IDX idx)
 {
