@@ -157,6 +157,30 @@ def test_matmul(g2, M, N, K, f16):
     assert_close_bound(dC.download(np.float32, M * N).reshape(M, N), ref, bound, what=f"matmul {M}x{N}x{K}")
 
 
+@pytest.mark.parametrize("f16", [False, True], ids=["f32", "f16"])
+@pytest.mark.parametrize("K", [768, 1600])
+def test_matmul_vocab_rows_sampled(g2, K, f16):
+    """The 1024-row GEMM over the 50257-wide vocabulary (the operator
+    sweep's largest case): every output row depends on its own A row only,
+    so the GPU's full 1024 x 50257 product is checked row for row against
+    the oracle run on a sample of 48 rows (first, last and spread rows,
+    every column), which keeps the oracle to seconds."""
+    M, N = 1024, 50257
+    A, B, bias = rnd((M, K), 54), rnd((K, N), 55), rnd(N, 56)
+    if f16:
+        B = f16_round(B)
+    dC = g2.DevBuf(M * N * 4)
+    g2.matmul(g2.to_device(A), g2.to_device(g2.convert_f16(B) if f16 else B), g2.to_device(bias), dC, M, N, K,
+              f16=f16)
+    got = dC.download(np.float32, M * N).reshape(M, N)
+    rows = np.unique(np.concatenate([[0, 1, 63, 64, 127, 128, 511, 512, 1022, 1023],
+                                     np.random.default_rng(57).choice(M, 38, replace=False)]))
+    ref = oracle.matmul(A[rows], B, bias, len(rows), N, K)
+    bound = dot_bound(np.abs(A[rows]).astype(np.float64), np.abs(B).astype(np.float64), K)
+    assert_close_bound(got[rows], ref, bound, what=f"matmul {M}x{N}x{K} sampled rows")
+    assert np.isfinite(got).all()
+
+
 def test_matmul_sweep_constant(g2):
     """The reference's tile-sweep known answer (main.c:750-753): A=B=0.01
     gives C = K*1e-4."""
