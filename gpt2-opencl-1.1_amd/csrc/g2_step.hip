@@ -547,12 +547,23 @@ __device__ __forceinline__ void dot_set(int tid, const u32x4 (&w)[UM][4], const 
     }
     if constexpr (UM == 4) {
         /* the four units' sums in one transposed reduction: unit j's total
-         * lands in row (0, 2, 1, 3)[j] of the wave */
+         * lands in row (0, 2, 1, 3)[j] of the wave.  Only the wave's units
+         * inside the share are multiplied (nv of its four slots, a
+         * wave-uniform count), so a share of fewer than 32 units costs its
+         * waves no products for their empty slots. */
         float acc[4] = {0.f, 0.f, 0.f, 0.f};
+        const int nv = (p.nunits - batch * NW * UM - wave + NW - 1) / NW; /* >= 1 here */
+        auto prods = [&](auto nvc) {
+            constexpr int NV = decltype(nvc)::value;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[j] = chunk_fma<WT>(w[j][i], xv[i], acc[j]);
+                for (int j = 0; j < NV; ++j) acc[j] = chunk_fma<WT>(w[j][i], xv[i], acc[j]);
+        };
+        if (nv >= 4) prods(std::integral_constant<int, 4>{});
+        else if (nv == 3) prods(std::integral_constant<int, 3>{});
+        else if (nv == 2) prods(std::integral_constant<int, 2>{});
+        else prods(std::integral_constant<int, 1>{});
         const float v = wsum4(acc[0], acc[1], acc[2], acc[3]);
         if ((lane & 15) == 0) {
             const int j = (lane >> 4) == 0 ? 0 : ((lane >> 4) == 1 ? 2 : ((lane >> 4) == 2 ? 1 : 3));
