@@ -313,11 +313,12 @@ __device__ __forceinline__ void settle4(const ctx &c, __amdgpu_buffer_rsrc_t r, 
  * 6400-value H vector is read by every work-group), so a work-group that
  * found empty values first waits on the quads holding value n*k/nsent,
  * k < nsent (the first value of each producer when n is split evenly over
- * nsent producers), then re-reads its empty quads.  dst (LDS) is 16-byte
- * aligned.  Ends with a barrier; `flag` is an LDS word of the caller. */
+ * nsent producers), then re-reads its empty quads.  Quad tid + NT*i goes
+ * to dst + dso[i] (LDS, 16-byte aligned: the padded position of its first
+ * value).  Ends with a barrier; `flag` is an LDS word of the caller. */
 template <int NQ>
 __device__ __forceinline__ void fetch4(int tid, const ctx &c, const float *src, int n, int nsent, float *dst,
-                                       lds_flag *flag)
+                                       const int (&dso)[NQ], lds_flag *flag)
 {
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, n * 4, 0x00020000);
     const u32x4 filler = (u32x4){0u, 0u, 0u, 0u};
@@ -353,7 +354,7 @@ __device__ __forceinline__ void fetch4(int tid, const ctx &c, const float *src, 
 #pragma unroll
     for (int i = 0; i < NQ; ++i) {
         const int q = tid + NT * i;
-        if (4 * q < n) *(u32x4 *)(dst + 4 * q) = v[i];
+        if (4 * q < n) *(u32x4 *)(dst + dso[i]) = v[i];
     }
     __syncthreads();
 }
@@ -391,13 +392,14 @@ __device__ __forceinline__ f32x4 ln_gload(int tid, const float *g, int E)
  * eps 1e-5), by W . LN(x) + bias = inv * (W . ((x - x0) * g) - (mean - x0) *
  * c1) + c2 with c1 = W . g, c2 = W . b + bias (g2k_ln_fold), x0 = x[0].
  * ln_fold_in writes the matrix input (x - x0) * g of the thread's quad
- * (entries 4tid .. 4tid + 3 of x, held in registers) to xin and each wave's
+ * (entries 4tid .. 4tid + 3 of x, held in registers) to xin at xo (their
+ * padded position, g2p_x_slot) and each wave's
  * sums of d = x - x0 and d^2 to red (a shift that keeps the variance E[d^2]
  * - E[d]^2 free of cancellation when |mean| >> std); ends with a barrier,
  * after which the dot products may start while ln_fold_stats reads the
  * sums (wave totals added in wave order). */
 __device__ __forceinline__ void ln_fold_in(int tid, const f32x4 &x, float x0, const f32x4 &g, int E, float *xin,
-                                           float *red)
+                                           int xo, float *red)
 {
     const bool on = 4 * tid < E;
     float s = 0.f, q = 0.f;
@@ -409,7 +411,7 @@ __device__ __forceinline__ void ln_fold_in(int tid, const f32x4 &x, float x0, co
         q = fmaf(d, d, q);
         o[e] = d * g[e];
     }
-    if (on) *(f32x4 *)(xin + 4 * tid) = o;
+    if (on) *(f32x4 *)(xin + xo) = o;
     s = wsum(s);
     q = wsum(q);
     if ((tid & 63) == 0) {
@@ -519,11 +521,12 @@ __device__ __forceinline__ float chunk_fma(const u32x4 &w, const float *x, float
     }
 }
 
-/* Dot products of a loaded batch with xin (LDS); unit sums to part[u].
+/* Dot products of a loaded batch with xin (LDS, the padded layout of
+ * g2p_dot_x: a chunk past the segment holds zeros); unit sums to part[u].
  * Every unit of the wave covers the same chunks of x, so they are read from
- * LDS once (unconditionally, at a clamped index: a read under a lane
- * condition would be waited for on its own).  The units' sums are
- * independent fma chains, interleaved chunk by chunk. */
+ * LDS once, all at once and unconditionally (a read under a lane condition
+ * would be waited for on its own).  The units' sums are independent fma
+ * chains, interleaved chunk by chunk. */
 template <typename WT, int UM>
 __device__ __forceinline__ void dot_set(int tid, const u32x4 (&w)[UM][4], const plan &p, int batch,
                                         const float *xin, float *part)
@@ -532,17 +535,16 @@ __device__ __forceinline__ void dot_set(int tid, const u32x4 (&w)[UM][4], const 
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     if (batch * NW * UM + wave >= p.nunits) return; /* wave-uniform */
     float xv[4][VE];
+    const int xo = g2p_dot_x(&p, VE, wave, lane, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const int cc = g2p_dot_chunk(&p, wave, lane, i);
-        const int ci = cc < 0 ? 0 : cc;
 #pragma unroll
         for (int e = 0; e < VE; e += 4) {
-            const f32x4 v = *(const f32x4 *)(xin + ci * VE + e);
-            xv[i][e] = cc < 0 ? 0.f : v.x;
-            xv[i][e + 1] = cc < 0 ? 0.f : v.y;
-            xv[i][e + 2] = cc < 0 ? 0.f : v.z;
-            xv[i][e + 3] = cc < 0 ? 0.f : v.w;
+            const f32x4 v = *(const f32x4 *)(xin + xo + 64 * VE * i + e);
+            xv[i][e] = v.x;
+            xv[i][e + 1] = v.y;
+            xv[i][e + 2] = v.z;
+            xv[i][e + 3] = v.w;
         }
     }
     if constexpr (UM == 4) {
@@ -864,8 +866,8 @@ __device__ __forceinline__ bool grid_resident(int tid, const ctx &c, const u64 *
  * device state.  All threads of the work-group take part. */
 template <typename WT>
 __device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, const shares &sh, const float *xlast, u64 *AM,
-                                        u32x4 (&wa)[UMAX][4], bool preloaded, float *xres, float *xin,
-                                        float *part, float *red, float *amv, int *ami, lds_flag *flag)
+                                        u32x4 (&wa)[UMAX][4], bool preloaded, float *xres, float *xe, int xeo,
+                                        float *xsc, float *part, float *red, float *amv, int *ami, lds_flag *flag)
 {
     /* ---- LM: logits over the head rows, work-group first-max */
     const int tid = fresh_tid();
@@ -882,8 +884,8 @@ __device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, con
     float x0;
     const f32x4 xq = fetch_q(tid, c, xlast, E, xres, x0);
     TRACE(0);
-    ln_fold_in(tid, xq, x0, gf, E, xin, red);
-    matvec<WT, UMAX>(tid, wa, p, xin, part);
+    ln_fold_in(tid, xq, x0, gf, E, xe, xeo, red);
+    matvec<WT, UMAX>(tid, wa, p, xe, part);
     const ln_st st = ln_fold_stats(red, E);
     const int masked = ngen < min_new ? G2_EOS_ID : -1;
     float bv = -INFINITY;
@@ -905,13 +907,13 @@ __device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, con
 
     /* ---- greedy pick (g2k_argmax_merge with advance) */
     __syncthreads();
-    fetch2<1>(tid, c, AM, 2 * nwg, xin); /* nwg <= NT work-groups' word pairs */
+    fetch2<1>(tid, c, AM, 2 * nwg, xsc); /* nwg <= NT work-groups' word pairs */
     const u64 abort_seen = tid == 0 ? ll_get(c.abort_w) : 0; /* issued ahead of the merge */
     bv = -INFINITY;
     bi = 0x7fffffff;
     for (int b = tid; b < nwg; b += NT) {
-        const float v = xin[2 * b];
-        const int i = __float_as_int(xin[2 * b + 1]);
+        const float v = xsc[2 * b];
+        const int i = __float_as_int(xsc[2 * b + 1]);
         if (am_better2(v, i, bv, bi)) { bv = v; bi = i; }
     }
     blk_argmax(tid, bv, bi, amv, ami);
@@ -933,7 +935,11 @@ template <typename WT>
 __device__ __forceinline__ void step_impl(const g2_step_args &a)
 {
     /* 16-byte alignment: the dot products read 16-byte chunks of these */
-    __shared__ __attribute__((aligned(16))) float xin[G2_STEP_MAXF];
+    /* matrix inputs in the padded layout (g2p_x_slot): K = n_embd, K = ffn */
+    __shared__ __attribute__((aligned(16))) float xe[G2P_XE_FLOATS];
+    __shared__ __attribute__((aligned(16))) float xf[G2P_XF_FLOATS];
+    /* words fetched by the head merge and the pick */
+    __shared__ __attribute__((aligned(16))) float xsc[G2_STEP_MAXCH * 66 > 2 * NT ? G2_STEP_MAXCH * 66 : 2 * NT];
     __shared__ __attribute__((aligned(16))) float xres[G2_STEP_MAXE];
     __shared__ float part[G2_STEP_MAXUNITS];
     __shared__ float red[2 * NW];
@@ -972,6 +978,13 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
      * soon as the previous matrix is consumed), wp the proj rows */
     u32x4 wa[UMAX][4], wp[UPROJ][4];
     const shares sh = make_shares<WT>(E, NH, F, V);
+    /* padded positions of this thread's input quads: quad tid of a K =
+     * n_embd input, quads tid + NT*i of the K = ffn input */
+    constexpr int VE = chunk_t<WT>::V;
+    int xeo[1], xfo[QMAX];
+    xeo[0] = g2p_x_slot(&sh.qkv, VE, 4 * min((int)threadIdx.x, E / 4 - 1));
+#pragma unroll
+    for (int i = 0; i < QMAX; ++i) xfo[i] = g2p_x_slot(&sh.fc2, VE, 4 * min((int)threadIdx.x + NT * i, F / 4 - 1));
     {
         const G2_CONST g2_step_layer *LT0 = (const G2_CONST g2_step_layer *)a.layers;
         const int tid = fresh_tid();
@@ -989,6 +1002,10 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         }
         load_set<UMAX>(tid, wa, make_plan(LT0->qkv_w, sh.qkv), 0);
         if (wg >= NH) load_set<UPROJ>(tid, wp, make_plan(LT0->proj_w, sh.proj), 0);
+        /* the padded matrix inputs: zero everywhere (the fetches write only
+         * the data positions) */
+        for (int q = tid; q < G2P_XE_FLOATS / 4; q += NT) *(f32x4 *)(xe + 4 * q) = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int q = tid; q < G2P_XF_FLOATS / 4; q += NT) *(f32x4 *)(xf + 4 * q) = (f32x4){0.f, 0.f, 0.f, 0.f};
         /* embedding of the token at its position (embed, math.cl:333-350) */
         for (int d = tid; d < E; d += NT)
             xres[d] = ldw((const WT *)a.wte, (size_t)tok * E + d) + ldw((const WT *)a.wpe, (size_t)pos * E + d);
@@ -1019,9 +1036,9 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 x0 = xres[0];
             }
             TRACE(1);
-            ln_fold_in(tid, xq, x0, g, E, xin, red);
+            ln_fold_in(tid, xq, x0, g, E, xe, xeo[0], red);
             TRACE(11);
-            matvec<WT, UMAX>(tid, wa, p, xin, part);
+            matvec<WT, UMAX>(tid, wa, p, xe, part);
             const ln_st st = ln_fold_stats(red, E);
             TRACE(12);
             if (l == 0 && a.plain &&
@@ -1064,11 +1081,11 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         for (int h = wg; h < NH; h += nwg) {
             const int tid = fresh_tid();
             const u64 *hp = R + G2X_ATT(E) + (size_t)h * G2_STEP_MAXCH * 66;
-            fetch2<NPM2>(tid, c, hp, nch * 66, xin); /* 66 words per chunk: even, at even words */
+            fetch2<NPM2>(tid, c, hp, nch * 66, xsc); /* 66 words per chunk: even, at even words */
             float Ls = 0.f;
             if (tid < 64) {
-                const float mc = tid < nch ? xin[tid * 66] : -INFINITY;
-                const float lc = tid < nch ? xin[tid * 66 + 1] : 0.f;
+                const float mc = tid < nch ? xsc[tid * 66] : -INFINITY;
+                const float lc = tid < nch ? xsc[tid * 66 + 1] : 0.f;
                 const float M = wmax(mc);
                 const float w = tid < nch ? expf(mc - M) : 0.f;
                 Ls = wsum(lc * w);
@@ -1077,7 +1094,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             __syncthreads();
             if (tid < 64) {
                 float acc = 0.f;
-                for (int ch = 0; ch < nch; ++ch) acc = fmaf(xin[ch * 66 + 2 + tid], cw[ch], acc);
+                for (int ch = 0; ch < nch; ++ch) acc = fmaf(xsc[ch * 66 + 2 + tid], cw[ch], acc);
                 vput(RV + G2V_O(E) + h * 64 + tid, RN + G2V_O(E) + h * 64 + tid, acc / Ls);
             }
             __syncthreads();
@@ -1098,9 +1115,9 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             const int tid = fresh_tid();
             const plan p = make_plan(y.proj_w, sh.proj);
             const float bias = gl(y.proj_b)[min(p.r0 + tid, E - 1)];
-            fetch4<NQE>(tid, c, RV + G2V_O(E), E, NH, xin, (lds_flag *)&flag);
+            fetch4<NQE>(tid, c, RV + G2V_O(E), E, NH, xe, xeo, (lds_flag *)&flag);
             TRACE(5);
-            matvec<WT, UPROJ>(tid, wp, p, xin, part);
+            matvec<WT, UPROJ>(tid, wp, p, xe, part);
             if (tid < p.nrows) {
                 const int r = p.r0 + tid;
                 float v = row_sum(p, part, tid);
@@ -1122,9 +1139,9 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             float x0;
             const f32x4 xq = fetch_q(tid, c, RV + G2V_X1(E), E, xres, x0);
             TRACE(7);
-            ln_fold_in(tid, xq, x0, g, E, xin, red);
+            ln_fold_in(tid, xq, x0, g, E, xe, xeo[0], red);
             TRACE(13);
-            matvec<WT, UMAX>(tid, wa, p, xin, part);
+            matvec<WT, UMAX>(tid, wa, p, xe, part);
             const ln_st st = ln_fold_stats(red, E);
             TRACE(14);
             if (tid < p.nrows) {
@@ -1142,9 +1159,9 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             const int tid = fresh_tid();
             const plan p = make_plan(y.fc2_w, sh.fc2);
             const float bias = gl(y.fc2_b)[min(p.r0 + tid, E - 1)];
-            fetch4<QMAX>(tid, c, RV + G2V_H(E), F, nwg, xin, (lds_flag *)&flag);
+            fetch4<QMAX>(tid, c, RV + G2V_H(E), F, nwg, xf, xfo, (lds_flag *)&flag);
             TRACE(9);
-            matvec<WT, UMAX>(tid, wa, p, xin, part);
+            matvec<WT, UMAX>(tid, wa, p, xf, part);
             TRACE(15);
             if (tid < p.nrows) {
                 const int r = p.r0 + tid;
@@ -1161,7 +1178,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
 
     /* the first batch of lm_head rows was loaded by the last fc2 phase */
     lm_pick<WT>(a, c, sh, XV + 2 * VR * (a.L - 1) + G2V_X2(E, F), X + (size_t)a.L * a.xlayer, wa, true,
-                xres, xin, part, red, amv, ami, (lds_flag *)&flag);
+                xres, xe, xeo[0], xsc, part, red, amv, ami, (lds_flag *)&flag);
 }
 
 } /* namespace g2step */

@@ -91,15 +91,42 @@ G2P_FN long g2p_unit_chunk(const g2p_unit *a, int lane, int i)
     return a->base + (a->uv ? g2p_min(a->c0 + lane + 64 * i, a->clast) : 0);
 }
 
-/* The x chunk lane `lane` of wave `wave` multiplies in slot i of the dot
- * products (every unit of a wave has segment wave % nseg); -1 when the slot
- * lies past the segment (its product is skipped). */
+/* The input chunk lane `lane` of wave `wave` multiplies in slot i of the
+ * dot products (every unit of a wave has segment wave % nseg); -1 when the
+ * slot lies past the segment (its x is zero).  The kernel reads x at
+ * g2p_dot_x; the CPU address check uses this to confirm that the two agree
+ * with where the fetches write the input (g2p_x_slot). */
 G2P_FN int g2p_dot_chunk(const g2p_rows *p, int wave, int lane, int i)
 {
     const int c0 = (wave & (p->nseg - 1)) * p->SL;
     const int c1 = g2p_min(p->C, c0 + p->SL);
     const int cc = c0 + lane + 64 * i;
     return cc < c1 ? cc : -1;
+}
+
+/* LDS layout of a matrix input for the dot products: the K input values
+ * in the share's segments of SL chunks (VE values each), segment s at
+ * floats [s * G2P_SEGC * VE, s * G2P_SEGC * VE + SL * VE) and zeros after it
+ * up to the next segment, so a lane's x chunk (segment start + lane + 64 i,
+ * i < 4) needs no bound: past the segment's end it reads zeros, which
+ * cancel the clamped weight chunk loaded there.  K = n_embd inputs (qkv,
+ * proj, fc, lm_head) and K = ffn inputs (fc2) have buffers of their own, so
+ * neither layout's data lands in the other's zeros. */
+#define G2P_XE_FLOATS 2048 /* K = n_embd: up to 2 segments of 256 chunks of 4, or 1 of 8 */
+#define G2P_XF_FLOATS 8192 /* K = ffn: up to 8 segments of 256 chunks of 4, or 4 of 8 */
+
+/* the padded position of input value k */
+G2P_FN int g2p_x_slot(const g2p_rows *p, int VE, int k)
+{
+    const int seg = p->SL * VE;
+    return (k / seg) * (G2P_SEGC * VE) + (k % seg);
+}
+
+/* the first x value lane `lane` of wave `wave` multiplies in slot i (its
+ * VE values follow) */
+G2P_FN int g2p_dot_x(const g2p_rows *p, int VE, int wave, int lane, int i)
+{
+    return ((wave & (p->nseg - 1)) * G2P_SEGC + lane + 64 * i) * VE;
 }
 
 /* Attention unit (head h, 64-position chunk ch) by the 256 threads of one
@@ -140,6 +167,8 @@ G2P_FN const char *g2p_step_refusal(int E, int NH, int F, int V, int VE, int nwg
         const int nseg = need <= 1 ? 1 : (need <= 2 ? 2 : (need <= 4 ? 4 : 8));
         if ((long)((dims[i][0] + dims[i][2] - 1) / dims[i][2]) * nseg > G2_STEP_MAXUNITS)
             return "a matrix exceeds the units per work-group";
+        if ((long)nseg * G2P_SEGC * VE > (i == 3 ? G2P_XF_FLOATS : G2P_XE_FLOATS))
+            return "a matrix input exceeds its padded LDS buffer";
     }
     return 0;
 }

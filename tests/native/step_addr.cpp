@@ -17,14 +17,19 @@
  *             stored (merged O, X1, H, X2, in the region of either tag
  *             parity, and the emptied entry of the other region) and every
  *             16-byte quad of them fetched;
- *   LDS       the dot products' x reads and the partial-sum slots.
+ *   LDS       the dot products' x reads and the partial-sum slots; every
+ *             x read inside a segment must be where the fetch wrote that
+ *             chunk's input values (g2p_x_slot), every read past it a zero
+ *             slot no input value is written to, and the input quads the
+ *             fetches write must fit the padded buffer.
  * Prints one line of counts; exits 1 if any access is out of bounds, 3 if
  * the host refuses the shape (g2p_step_refusal: it then never launches it).
  *
  * Usage: step_addr L E NH V F VE POS NWG [plant]
  *   VE: elements per 16-byte chunk (8 fp16, 4 fp32); plant=1 replaces the
- *   clamped chunk of g2p_unit_chunk by the unclamped one (a planted mistake
- *   the check must catch).
+ *   clamped chunk of g2p_unit_chunk by the unclamped one, plant=2 shifts the
+ *   dot products' x reads by one chunk (planted mistakes the check must
+ *   catch).
  */
 #include <cstdio>
 #include <cstdlib>
@@ -66,17 +71,35 @@ static void load_set(const char *what, const g2p_rows &p, int UM, int batch, lon
     (void)VE;
 }
 
-/* dot_set's LDS reads of x (K floats written) and its partial-sum writes */
-static void dot_set(const char *what, const g2p_rows &p, int UM, int batch, int VE, long K)
+/* whether padded slot x holds an input value (k < K) */
+static bool x_is_data(const g2p_rows &p, int VE, long K, long x)
 {
+    const long seg = x / ((long)G2P_SEGC * VE), off = x % ((long)G2P_SEGC * VE);
+    return off < (long)p.SL * VE && seg * p.SL * VE + off < K;
+}
+
+/* dot_set's LDS reads of x (K floats written to a padded buffer of xcap
+ * floats) and its partial-sum writes */
+static void dot_set(const char *what, const g2p_rows &p, int UM, int batch, int VE, long K, long xcap)
+{
+    for (long k = 0; k < K; k += 4) {
+        const long x = g2p_x_slot(&p, VE, (int)k);
+        chk("LDS input quad", x, x + 4, xcap);
+        if (!x_is_data(p, VE, K, x)) chk("LDS input quad outside the data slots", 0, 1, 0);
+    }
     for (int tid = 0; tid < G2_STEP_THREADS; ++tid) {
         const int wave = tid >> 6, lane = tid & 63;
         if (batch * G2P_NW * UM + wave >= p.nunits) continue;
         for (int i = 0; i < 4; ++i) {
+            const long x = g2p_dot_x(&p, VE, wave, lane, i) + (plant == 2 ? VE : 0);
+            chk("LDS x", x, x + VE, xcap);
             const int cc = g2p_dot_chunk(&p, wave, lane, i);
             if (cc >= 0) {
                 chk(what, (long)cc * VE, (long)cc * VE + VE, K);
-                chk("LDS x", (long)cc * VE, (long)cc * VE + VE, G2_STEP_MAXF);
+                if (x != g2p_x_slot(&p, VE, cc * VE)) chk("LDS x slot of a chunk (not where its values are)", 0, 1, 0);
+            } else {
+                for (int e = 0; e < VE; ++e)
+                    if (x_is_data(p, VE, K, x + e)) chk("LDS x past the segment (not a zero slot)", 0, 1, 0);
             }
         }
         for (int j = 0; j < UM; ++j) {
@@ -88,13 +111,14 @@ static void dot_set(const char *what, const g2p_rows &p, int UM, int batch, int 
 
 /* a whole matrix share as matvec<UM> runs it (batch 0 preloaded, later
  * batches loaded on demand), its bias load and the row sums */
-static void matrix(const char *what, const void *bias_tag, int N, int K, int VE, int UM, long wg, long nwg)
+static void matrix(const char *what, const void *bias_tag, int N, int K, int VE, int UM, long wg, long nwg,
+                   long xcap = G2P_XE_FLOATS)
 {
     const g2p_rows p = g2p_rows_plan(N, K, VE, wg, nwg);
     chk("rows per work-group", 0, p.nrows, G2_STEP_THREADS);
     for (int b = 0; b == 0 || b * G2P_NW * UM < p.nunits; ++b) {
         load_set(what, p, UM, b, N, VE);
-        dot_set(what, p, UM, b, VE, K);
+        dot_set(what, p, UM, b, VE, K, xcap);
     }
     if (bias_tag)
         for (int tid = 0; tid < G2_STEP_THREADS; ++tid) {
@@ -227,10 +251,10 @@ int main(int argc, char **argv)
             }
             vstore("H values", l, vH, pf.r0, pf.r0 + pf.nrows, vX2);
             for (int b = 0; b < 2; ++b) quads("H fetch", vreg(l, b) + vH, F, vreg(l, b) + vX2);
-            matrix("fc2 weights", "b", E, F, VE, 4, wg, nwg);
+            matrix("fc2 weights", "b", E, F, VE, 4, wg, nwg, G2P_XF_FLOATS);
             const g2p_rows p2 = g2p_rows_plan(E, F, VE, wg, nwg);
             vstore("X2 values", l, vX2, p2.r0, p2.r0 + p2.nrows, VR);
-            chk("fetched vector in LDS", 0, F, G2_STEP_MAXF);
+
         }
         /* LM head: X2 of the last layer, rows, logits, argmax words */
         for (int b = 0; b < 2; ++b) quads("LM X2 fetch", vreg(L - 1, b) + vX2, E, vreg(L - 1, b) + VR);

@@ -11,8 +11,9 @@ model shape the library serves (GPT-2 small to XL, and the small test
 shapes with fewer heads than XCDs), both weight element sizes and positions
 at chunk boundaries, on MI355X's 256-CU grid (where every shape must be
 admitted) and on other grid sizes (where the host's admission rule,
-g2p_step_refusal in the same header, may refuse a shape instead).  A
-planted mistake (the per-lane chunk clamp removed) must be caught.
+g2p_step_refusal in the same header, may refuse a shape instead).  Planted
+mistakes (the per-lane chunk clamp removed; the dot products' x reads one
+chunk off the padded input layout) must be caught.
 No GPU is involved.
 """
 import os
@@ -60,6 +61,14 @@ def test_step_kernel_addresses_in_bounds(checker, shape):
             assert rc == 0, f"{sh} chunk {ve} elements, position {pos}, {nwg} work-groups: {out}"
         else:  # other grids: refused by the host (and never launched) or in bounds
             assert rc in (0, 3), f"{sh} chunk {ve} elements, position {pos}, {nwg} work-groups: {out}"
+
+
+def test_planted_x_layout_shift_is_caught(checker):
+    """The dot products reading x one chunk off the padded positions the
+    fetches write must be caught, for both weight sizes."""
+    for ve in (8, 4):
+        rc, out = run(checker, "xl", ve, 700, 256, plant=2)
+        assert rc == 1 and "LDS x" in out, out
 
 
 def test_planted_unclamped_chunk_is_caught(checker):
