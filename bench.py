@@ -13,7 +13,7 @@ timed region covers K steps; `value` is decode tokens per second over it.
 Prefill throughput (prompt tokens / prefill time) is reported beside it.
 
 roofline: the dominant kernel is the persistent decode-step kernel
-g2k_step_f16 (one cooperative launch per token running all 48 layers, the
+g2k_step_f16_tail (one cooperative launch per token running all 48 layers, the
 lm_head and the greedy pick); achieved = algorithmic bytes per launch / the
 mean launch duration from HIP events on the library stream around the 511
 launches, bytes per token from the formula
@@ -234,7 +234,7 @@ def run(args, g2):
     achieved = bytes_step / (step_ms_events * 1e-3) / 1e9
 
     kind = m.step_kind()
-    kname = ("g2k_step_f16" if f16 else "g2k_step_f32") if kind else ""
+    kname = m.step_kernel() if kind else ""
     workload = (f"GPT-2 {preset.upper()} {'fp16' if f16 else 'fp32'}-weight batch-1 greedy decode: {P}-token "
                 f"random prompt, {n_dec} decode forwards (positions {P}..{P + n_dec - 1})")
     result = {

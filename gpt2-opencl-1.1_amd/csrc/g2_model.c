@@ -776,7 +776,9 @@ static int step_launch(g2_model *m)
     a.scale = 1.0f / sqrtf(64.0f);
     m->step_ran = 1;
     a.xlayer = G2X_LAYER_WORDS(c->n_embd, c->n_head);
-    const int fid = m->dtype == G2_F16 ? G2F_STEP_F16 : G2F_STEP_F32;
+    /* the tail form where every four-unit plan is a tail plan */
+    const int tail = g2p_step_tail(c->n_embd, c->ffn_dim, m->dtype == G2_F16 ? 8 : 4);
+    const int fid = m->dtype == G2_F16 ? (tail ? G2F_STEP_F16T : G2F_STEP_F16) : (tail ? G2F_STEP_F32T : G2F_STEP_F32);
     if (m->plain) {
         a.plain = m->plain;
         return g2i_launch(fid, (unsigned)m->step_wgs, 1, G2_STEP_THREADS, &a);

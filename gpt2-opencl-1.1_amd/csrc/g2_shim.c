@@ -185,13 +185,15 @@ int g2_init(int device)
      * them co-resident: require cooperative launch support and an occupancy
      * of at least one work-group per CU for both weight types. */
     {
-        int coop = 0, nb[2] = { -1, -1 };
+        int coop = 0, nb[4] = { -1, -1, -1, -1 };
         hipError_t ea = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device);
-        hipError_t eo[2] = { hipSuccess, hipSuccess };
-        const int fids[2] = { G2F_STEP_F32, G2F_STEP_F16 };
-        for (int i = 0; i < 2; ++i)
+        hipError_t eo[4] = { hipSuccess, hipSuccess, hipSuccess, hipSuccess };
+        const int fids[4] = { G2F_STEP_F32, G2F_STEP_F16, G2F_STEP_F32T, G2F_STEP_F16T };
+        int ok = ea == hipSuccess && coop;
+        for (int i = 0; i < 4; ++i) {
             eo[i] = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb[i], G.fn[fids[i]], G2_STEP_THREADS, 0);
-        const int ok = ea == hipSuccess && coop && eo[0] == hipSuccess && eo[1] == hipSuccess && nb[0] >= 1 && nb[1] >= 1;
+            ok = ok && eo[i] == hipSuccess && nb[i] >= 1;
+        }
         G.step_wgs = ok ? prop.multiProcessorCount : 0;
         if (!ok) {
             int rtv = 0;
@@ -200,10 +202,10 @@ int g2_init(int device)
             (void)hipRuntimeGetVersion(&rtv);
             (void)hipFuncGetAttributes(&fa, (const void *)G.fn[G2F_STEP_F16]);
             fprintf(stderr, "g2hip: persistent step kernel unavailable (HIP runtime %d, cooperative launch %d, "
-                            "err %d; work-groups per CU %d/%d, err %d/%d; kernel regs %d lds %zu max threads %d); "
-                            "decode uses per-operator kernels\n",
-                    rtv, coop, (int)ea, nb[0], nb[1], (int)eo[0], (int)eo[1], fa.numRegs, fa.sharedSizeBytes,
-                    fa.maxThreadsPerBlock);
+                            "err %d; work-groups per CU %d/%d/%d/%d, err %d/%d/%d/%d; kernel regs %d lds %zu max "
+                            "threads %d); decode uses per-operator kernels\n",
+                    rtv, coop, (int)ea, nb[0], nb[1], nb[2], nb[3], (int)eo[0], (int)eo[1], (int)eo[2], (int)eo[3],
+                    fa.numRegs, fa.sharedSizeBytes, fa.maxThreadsPerBlock);
         }
         (void)hipGetLastError();
     }

@@ -489,19 +489,24 @@ __device__ __forceinline__ plan make_plan(const void *W, const g2p_rows &r)
  * load under a lane condition makes the compiler wait for every load in
  * flight before the value is first used.  Dot products ignore the clamped
  * chunks (their x is zero) and the units past the share. */
-template <int UM>
+template <int UM, bool TAIL>
 __device__ __forceinline__ void load_set(int tid, u32x4 (&w)[UM][4], const plan &p, int batch)
 {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    /* the tail form (every four-unit plan a tail plan) packs slot 3 of the
+     * four units into w[0][3] */
+    constexpr bool tail = TAIL && UM == 4;
 #pragma unroll
     for (int j = 0; j < UM; ++j) {
         const g2p_unit un = g2p_unit_at(&p, UM, batch, wave, j);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+            if (tail && i == 3) continue;
             /* a unit past the share reads one chunk with every lane (one line) */
             w[j][i] = __builtin_nontemporal_load(gl(p.W) + g2p_unit_chunk(&un, lane, i));
         }
     }
+    if constexpr (tail) w[0][3] = __builtin_nontemporal_load(gl(p.W) + g2p_tail_chunk(&p, batch, wave, lane));
 }
 
 /* acc + (16-byte chunk of weights) . x, as one fma chain element by element */
@@ -527,7 +532,7 @@ __device__ __forceinline__ float chunk_fma(const u32x4 &w, const float *x, float
  * LDS once, all at once and unconditionally (a read under a lane condition
  * would be waited for on its own).  The units' sums are independent fma
  * chains, interleaved chunk by chunk. */
-template <typename WT, int UM>
+template <typename WT, int UM, bool TAIL>
 __device__ __forceinline__ void dot_set(int tid, const u32x4 (&w)[UM][4], const plan &p, int batch,
                                         const float *xin, float *part)
 {
@@ -536,11 +541,13 @@ __device__ __forceinline__ void dot_set(int tid, const u32x4 (&w)[UM][4], const 
     if (batch * NW * UM + wave >= p.nunits) return; /* wave-uniform */
     float xv[4][VE];
     const int xo = g2p_dot_x(&p, VE, wave, lane, 0);
+    /* slot 3 of a tail plan multiplies the packed chunks */
+    const int x3 = (UM == 4 && TAIL) ? g2p_tail_x(&p, VE, wave, lane) : xo + 3 * 64 * VE;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
         for (int e = 0; e < VE; e += 4) {
-            const f32x4 v = *(const f32x4 *)(xin + xo + 64 * VE * i + e);
+            const f32x4 v = *(const f32x4 *)(xin + (i == 3 ? x3 : xo + 64 * VE * i) + e);
             xv[i][e] = v.x;
             xv[i][e + 1] = v.y;
             xv[i][e + 2] = v.z;
@@ -555,12 +562,25 @@ __device__ __forceinline__ void dot_set(int tid, const u32x4 (&w)[UM][4], const 
          * waves no products for their empty slots. */
         float acc[4] = {0.f, 0.f, 0.f, 0.f};
         const int nv = (p.nunits - batch * NW * UM - wave + NW - 1) / NW; /* >= 1 here */
+        /* a tail plan: slots 0-2 per unit, then the packed slot 3 (one
+         * chain for all four units), each lane's sum added to its unit */
         auto prods = [&](auto nvc) {
             constexpr int NV = decltype(nvc)::value;
+            if constexpr (TAIL) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < 3; ++i)
 #pragma unroll
-                for (int j = 0; j < NV; ++j) acc[j] = chunk_fma<WT>(w[j][i], xv[i], acc[j]);
+                    for (int j = 0; j < NV; ++j) acc[j] = chunk_fma<WT>(w[j][i], xv[i], acc[j]);
+                const float tl = chunk_fma<WT>(w[0][3], xv[3], 0.f);
+                const int tj = lane >> 4;
+#pragma unroll
+                for (int j = 0; j < NV; ++j) acc[j] += tj == j ? tl : 0.f;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < NV; ++j) acc[j] = chunk_fma<WT>(w[j][i], xv[i], acc[j]);
+            }
         };
         if (nv >= 4) prods(std::integral_constant<int, 4>{});
         else if (nv == 3) prods(std::integral_constant<int, 3>{});
@@ -590,14 +610,14 @@ __device__ __forceinline__ void dot_set(int tid, const u32x4 (&w)[UM][4], const 
 
 /* The whole matrix share: batch 0 from the preloaded set, later batches
  * loaded on demand into the same set.  Ends with a barrier. */
-template <typename WT, int UM>
+template <typename WT, int UM, bool TAIL>
 __device__ __forceinline__ void matvec(int tid, u32x4 (&w)[UM][4], const plan &p, const float *xin,
                                        float *part)
 {
-    dot_set<WT, UM>(tid, w, p, 0, xin, part);
+    dot_set<WT, UM, TAIL>(tid, w, p, 0, xin, part);
     for (int b = 1; b * NW * UM < p.nunits; ++b) {
-        load_set<UM>(tid, w, p, b);
-        dot_set<WT, UM>(tid, w, p, b, xin, part);
+        load_set<UM, TAIL>(tid, w, p, b);
+        dot_set<WT, UM, TAIL>(tid, w, p, b, xin, part);
     }
     __syncthreads();
 }
@@ -864,7 +884,7 @@ __device__ __forceinline__ bool grid_resident(int tid, const ctx &c, const u64 *
  * work-group's head rows -> first-max per work-group (argmax words AM) ->
  * work-group 0 merges them (g2k_argmax_merge with advance) and advances the
  * device state.  All threads of the work-group take part. */
-template <typename WT>
+template <typename WT, bool TAIL>
 __device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, const shares &sh, const float *xlast, u64 *AM,
                                         u32x4 (&wa)[UMAX][4], bool preloaded, float *xres, float *xe, int xeo,
                                         float *xsc, float *part, float *red, float *amv, int *ami, lds_flag *flag)
@@ -880,12 +900,12 @@ __device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, con
     const plan p = make_plan(a.lm_w, sh.lm);
     const int rl = min(p.r0 + tid, V - 1); /* used by tid < nrows */
     const float c1 = gl(a.lm_c1)[rl], c2 = gl(a.lm_c2)[rl];
-    if (!preloaded) load_set<UMAX>(tid, wa, p, 0);
+    if (!preloaded) load_set<UMAX, TAIL>(tid, wa, p, 0);
     float x0;
     const f32x4 xq = fetch_q(tid, c, xlast, E, xres, x0);
     TRACE(0);
     ln_fold_in(tid, xq, x0, gf, E, xe, xeo, red);
-    matvec<WT, UMAX>(tid, wa, p, xe, part);
+    matvec<WT, UMAX, TAIL>(tid, wa, p, xe, part);
     const ln_st st = ln_fold_stats(red, E);
     const int masked = ngen < min_new ? G2_EOS_ID : -1;
     float bv = -INFINITY;
@@ -931,7 +951,7 @@ __device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, con
     TRACE(2);
 }
 
-template <typename WT>
+template <typename WT, bool TAIL>
 __device__ __forceinline__ void step_impl(const g2_step_args &a)
 {
     /* 16-byte alignment: the dot products read 16-byte chunks of these */
@@ -1000,8 +1020,8 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             if (a.plain && !(a.plain == 2 && wg == 1))
                 ll_put(a.xbuf + G2X_ARRIVE(a.L, a.xlayer, nwg) + wg, 0.f, c.tag);
         }
-        load_set<UMAX>(tid, wa, make_plan(LT0->qkv_w, sh.qkv), 0);
-        if (wg >= NH) load_set<UPROJ>(tid, wp, make_plan(LT0->proj_w, sh.proj), 0);
+        load_set<UMAX, TAIL>(tid, wa, make_plan(LT0->qkv_w, sh.qkv), 0);
+        if (wg >= NH) load_set<UPROJ, TAIL>(tid, wp, make_plan(LT0->proj_w, sh.proj), 0);
         /* the padded matrix inputs: zero everywhere (the fetches write only
          * the data positions) */
         for (int q = tid; q < G2P_XE_FLOATS / 4; q += NT) *(f32x4 *)(xe + 4 * q) = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -1038,7 +1058,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             TRACE(1);
             ln_fold_in(tid, xq, x0, g, E, xe, xeo[0], red);
             TRACE(11);
-            matvec<WT, UMAX>(tid, wa, p, xe, part);
+            matvec<WT, UMAX, TAIL>(tid, wa, p, xe, part);
             const ln_st st = ln_fold_stats(red, E);
             TRACE(12);
             if (l == 0 && a.plain &&
@@ -1074,7 +1094,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             TRACE(3);
             /* the fc rows stream from here on; a work-group that merges a head
              * issues them after its merge, so its merge waits behind nothing */
-            if (wg >= NH) load_set<UMAX>(tid, wa, make_plan(y.fc_w, sh.fc), 0);
+            if (wg >= NH) load_set<UMAX, TAIL>(tid, wa, make_plan(y.fc_w, sh.fc), 0);
         }
 
         /* ---- MERGE: head h by work-group h (g2k_attn_merge) */
@@ -1102,7 +1122,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         {
             const int tid = fresh_tid();
             TRACE(16);
-            if (wg < NH) load_set<UMAX>(tid, wa, make_plan(y.fc_w, sh.fc), 0);
+            if (wg < NH) load_set<UMAX, TAIL>(tid, wa, make_plan(y.fc_w, sh.fc), 0);
             TRACE(4);
         }
 
@@ -1117,7 +1137,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             const float bias = gl(y.proj_b)[min(p.r0 + tid, E - 1)];
             fetch4<NQE>(tid, c, RV + G2V_O(E), E, NH, xe, xeo, (lds_flag *)&flag);
             TRACE(5);
-            matvec<WT, UPROJ>(tid, wp, p, xe, part);
+            matvec<WT, UPROJ, TAIL>(tid, wp, p, xe, part);
             if (tid < p.nrows) {
                 const int r = p.r0 + tid;
                 float v = row_sum(p, part, tid);
@@ -1125,7 +1145,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 vput(RV + G2V_X1(E) + r, RN + G2V_X1(E) + r, v + xres[r]);
             }
             TRACE(6);
-            if (l + 1 < a.L) load_set<UPROJ>(tid, wp, make_plan(LT[l + 1].proj_w, sh.proj), 0);
+            if (l + 1 < a.L) load_set<UPROJ, TAIL>(tid, wp, make_plan(LT[l + 1].proj_w, sh.proj), 0);
             __syncthreads();
         }
 
@@ -1141,7 +1161,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             TRACE(7);
             ln_fold_in(tid, xq, x0, g, E, xe, xeo[0], red);
             TRACE(13);
-            matvec<WT, UMAX>(tid, wa, p, xe, part);
+            matvec<WT, UMAX, TAIL>(tid, wa, p, xe, part);
             const ln_st st = ln_fold_stats(red, E);
             TRACE(14);
             if (tid < p.nrows) {
@@ -1150,7 +1170,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 vput(RV + G2V_H(E) + r, RN + G2V_H(E) + r, gelu_f(v));
             }
             TRACE(8);
-            load_set<UMAX>(tid, wa, make_plan(y.fc2_w, sh.fc2), 0);
+            load_set<UMAX, TAIL>(tid, wa, make_plan(y.fc2_w, sh.fc2), 0);
             __syncthreads();
         }
 
@@ -1161,7 +1181,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             const float bias = gl(y.fc2_b)[min(p.r0 + tid, E - 1)];
             fetch4<QMAX>(tid, c, RV + G2V_H(E), F, nwg, xf, xfo, (lds_flag *)&flag);
             TRACE(9);
-            matvec<WT, UMAX>(tid, wa, p, xf, part);
+            matvec<WT, UMAX, TAIL>(tid, wa, p, xf, part);
             TRACE(15);
             if (tid < p.nrows) {
                 const int r = p.r0 + tid;
@@ -1170,14 +1190,14 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 vput(RV + G2V_X2(E, F) + r, RN + G2V_X2(E, F) + r, v + xres[r]);
             }
             TRACE(10);
-            if (l + 1 < a.L) load_set<UMAX>(tid, wa, make_plan(LT[l + 1].qkv_w, sh.qkv), 0);
-            else load_set<UMAX>(tid, wa, make_plan(a.lm_w, sh.lm), 0);
+            if (l + 1 < a.L) load_set<UMAX, TAIL>(tid, wa, make_plan(LT[l + 1].qkv_w, sh.qkv), 0);
+            else load_set<UMAX, TAIL>(tid, wa, make_plan(a.lm_w, sh.lm), 0);
             __syncthreads();
         }
     }
 
     /* the first batch of lm_head rows was loaded by the last fc2 phase */
-    lm_pick<WT>(a, c, sh, XV + 2 * VR * (a.L - 1) + G2V_X2(E, F), X + (size_t)a.L * a.xlayer, wa, true,
+    lm_pick<WT, TAIL>(a, c, sh, XV + 2 * VR * (a.L - 1) + G2V_X2(E, F), X + (size_t)a.L * a.xlayer, wa, true,
                 xres, xe, xeo[0], xsc, part, red, amv, ami, (lds_flag *)&flag);
 }
 
@@ -1185,9 +1205,20 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
 
 extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f32(const g2_step_args a)
 {
-    g2step::step_impl<float>(a);
+    g2step::step_impl<float, false>(a);
 }
 extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f16(const g2_step_args a)
 {
-    g2step::step_impl<_Float16>(a);
+    g2step::step_impl<_Float16, false>(a);
+}
+/* The tail form, for models whose every four-unit plan is a tail plan
+ * (g2p_step_tail: n_embd 1600, the rows of every matrix 200 chunks per
+ * segment). */
+extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f32_tail(const g2_step_args a)
+{
+    g2step::step_impl<float, true>(a);
+}
+extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f16_tail(const g2_step_args a)
+{
+    g2step::step_impl<_Float16, true>(a);
 }

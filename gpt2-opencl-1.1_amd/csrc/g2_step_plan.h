@@ -29,6 +29,10 @@ G2P_FN int g2p_min(int a, int b) { return a < b ? a : b; }
  * one wave's job, 64 lanes x up to 4 chunks. */
 typedef struct {
     int C, nseg, lseg, SL, r0, nrows, nunits; /* nseg = 1 << lseg */
+    /* the segments end 1..16 chunks into slot 3 (192 < SL <= 208): with four
+     * units per wave, slot 3 of all four is packed into one register (lane l
+     * holding chunk 192 + l % 16 of unit l / 16), see g2p_tail_chunk */
+    int tail;
 } g2p_rows;
 
 G2P_FN g2p_rows g2p_rows_plan(int N, int K, int VE, long wg, long nwg)
@@ -42,6 +46,7 @@ G2P_FN g2p_rows g2p_rows_plan(int N, int K, int VE, long wg, long nwg)
     p.r0 = (int)(((long)N * wg) / nwg);
     p.nrows = (int)(((long)N * (wg + 1)) / nwg) - p.r0;
     p.nunits = p.nrows * p.nseg;
+    p.tail = p.SL > 3 * 64 && p.SL <= 3 * 64 + 16;
     return p;
 }
 
@@ -91,6 +96,23 @@ G2P_FN long g2p_unit_chunk(const g2p_unit *a, int lane, int i)
     return a->base + (a->uv ? g2p_min(a->c0 + lane + 64 * i, a->clast) : 0);
 }
 
+/* Packed slot 3 of a tail plan (four units per wave): the chunk lane
+ * `lane` loads for it, chunk 192 + lane % 16 of the segment of unit lane /
+ * 16, clamped into the segment like g2p_unit_chunk (a unit past the share
+ * reads chunk 0 of the share's first row). */
+G2P_FN long g2p_tail_chunk(const g2p_rows *p, int batch, int wave, int lane)
+{
+    const g2p_unit un = g2p_unit_at(p, 4, batch, wave, lane >> 4);
+    return un.base + (un.uv ? g2p_min(un.c0 + 3 * 64 + (lane & 15), un.clast) : 0);
+}
+
+/* its x: chunk 192 + lane % 16 of the wave's segment (zero past the
+ * segment's end, which cancels the clamped weight chunk) */
+G2P_FN int g2p_tail_x(const g2p_rows *p, int VE, int wave, int lane)
+{
+    return ((wave & (p->nseg - 1)) * G2P_SEGC + 3 * 64 + (lane & 15)) * VE;
+}
+
 /* The input chunk lane `lane` of wave `wave` multiplies in slot i of the
  * dot products (every unit of a wave has segment wave % nseg); -1 when the
  * slot lies past the segment (its x is zero).  The kernel reads x at
@@ -127,6 +149,14 @@ G2P_FN int g2p_x_slot(const g2p_rows *p, int VE, int k)
 G2P_FN int g2p_dot_x(const g2p_rows *p, int VE, int wave, int lane, int i)
 {
     return ((wave & (p->nseg - 1)) * G2P_SEGC + lane + 64 * i) * VE;
+}
+
+/* Whether every four-unit plan of a model (qkv, fc and lm_head with K =
+ * n_embd, fc2 with K = ffn; proj runs one unit per wave) is a tail plan, so
+ * the step kernel's tail form applies to all of them. */
+G2P_FN int g2p_step_tail(int E, int F, int VE)
+{
+    return g2p_rows_plan(1, E, VE, 0, 1).tail && g2p_rows_plan(1, F, VE, 0, 1).tail;
 }
 
 /* Attention unit (head h, 64-position chunk ch) by the 256 threads of one

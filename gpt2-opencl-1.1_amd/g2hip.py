@@ -381,8 +381,9 @@ def swap_slots(weights, a, b, layer=None):
 class Model:
     """A GPT-2 model resident on the GPU (g2_model handle)."""
 
-    def __init__(self, handle):
+    def __init__(self, handle, dtype=F32):
         self.h = handle
+        self.dtype = dtype
         cfg = Config()
         check(_lib.g2_model_config(self.h, C.byref(cfg)))
         self.cfg = cfg
@@ -391,13 +392,13 @@ class Model:
     def synth(cls, cfg, seed, dtype=F32, path=PATH_FUSED):
         h = _vp()
         check(_lib.g2_model_synth(C.byref(cfg), seed, dtype, path, C.byref(h)))
-        return cls(h.value)
+        return cls(h.value, dtype)
 
     @classmethod
     def load(cls, directory, dtype=F32, path=PATH_FUSED):
         h = _vp()
         check(_lib.g2_model_load(directory.encode(), dtype, path, C.byref(h)))
-        return cls(h.value)
+        return cls(h.value, dtype)
 
     @classmethod
     def from_host(cls, cfg, weights, dtype=F32, path=PATH_FUSED):
@@ -416,7 +417,7 @@ class Model:
         check(_lib.g2_model_from_host(C.byref(cfg), ptr(weights["wte"]), ptr(weights["wpe"]),
                                       ptr(weights["lnf_w"]), ptr(weights["lnf_b"]), flat,
                                       dtype, path, C.byref(h)))
-        return cls(h.value)
+        return cls(h.value, dtype)
 
     def free(self):
         if self.h:
@@ -444,6 +445,25 @@ class Model:
 
     def uses_step(self):
         return _lib.g2_model_uses_step(self.h) >= 1
+
+    def step_kernel(self):
+        """Name of the persistent step kernel this model launches ("" when it
+        decodes with per-operator kernels): the tail form when every
+        four-unit row plan ends 1..16 chunks into its last slot (the rule of
+        g2p_step_tail in csrc/g2_step_plan.h)."""
+        if not self.uses_step():
+            return ""
+        ve = 8 if self.dtype == F16 else 4
+
+        def tail(K):
+            C = K // ve
+            need = -(-C // 256)
+            nseg = 1 if need <= 1 else 2 if need <= 2 else 4 if need <= 4 else 8
+            SL = -(-C // nseg)
+            return 192 < SL <= 208
+
+        base = "g2k_step_f16" if self.dtype == F16 else "g2k_step_f32"
+        return base + "_tail" if tail(self.cfg.n_embd) and tail(self.cfg.ffn_dim) else base
 
     def step_kind(self):
         """1: persistent step kernel, 0: per-operator kernels."""

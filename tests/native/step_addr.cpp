@@ -52,6 +52,8 @@ static void chk(const char *what, long lo, long hi_excl, long lim)
 }
 
 static int plant = 0;
+/* the kernel form the host launches for this shape (g2p_step_tail) */
+static int tail_form = 0;
 
 /* load_set<UM>(batch) of a work-group: every lane's 16-byte chunk loads */
 static void load_set(const char *what, const g2p_rows &p, int UM, int batch, long N, long VE)
@@ -63,7 +65,12 @@ static void load_set(const char *what, const g2p_rows &p, int UM, int batch, lon
             const g2p_unit un = g2p_unit_at(&p, UM, batch, wave, j);
             for (int i = 0; i < 4; ++i) {
                 long c = g2p_unit_chunk(&un, lane, i);
-                if (plant && un.uv) c = un.base + un.c0 + lane + 64 * i;
+                if (plant == 1 && un.uv) c = un.base + un.c0 + lane + 64 * i;
+                if (i == 3 && UM == 4 && tail_form) { /* the packed slot 3 */
+                    c = g2p_tail_chunk(&p, batch, wave, lane);
+                    const g2p_unit ut = g2p_unit_at(&p, 4, batch, wave, lane >> 4);
+                    if (plant == 1 && ut.uv) c = ut.base + ut.c0 + 3 * 64 + (lane & 15);
+                }
                 chk(what, c, c + 1, chunks);
             }
         }
@@ -91,12 +98,25 @@ static void dot_set(const char *what, const g2p_rows &p, int UM, int batch, int 
         const int wave = tid >> 6, lane = tid & 63;
         if (batch * G2P_NW * UM + wave >= p.nunits) continue;
         for (int i = 0; i < 4; ++i) {
-            const long x = g2p_dot_x(&p, VE, wave, lane, i) + (plant == 2 ? VE : 0);
+            const bool packed = i == 3 && UM == 4 && tail_form;
+            long x = (packed ? g2p_tail_x(&p, VE, wave, lane) : g2p_dot_x(&p, VE, wave, lane, i)) + (plant == 2 ? VE : 0);
             chk("LDS x", x, x + VE, xcap);
-            const int cc = g2p_dot_chunk(&p, wave, lane, i);
+            int cc = g2p_dot_chunk(&p, wave, lane, i);
+            if (packed) { /* chunk 192 + lane % 16 of the wave's segment */
+                const int c0 = (wave & (p.nseg - 1)) * p.SL, c1 = g2p_min(p.C, c0 + p.SL);
+                cc = c0 + 3 * 64 + (lane & 15) < c1 ? c0 + 3 * 64 + (lane & 15) : -1;
+            }
             if (cc >= 0) {
                 chk(what, (long)cc * VE, (long)cc * VE + VE, K);
                 if (x != g2p_x_slot(&p, VE, cc * VE)) chk("LDS x slot of a chunk (not where its values are)", 0, 1, 0);
+                /* the weight chunk multiplied with it is the same column */
+                for (int j = 0; j < UM; ++j) {
+                    const g2p_unit un = g2p_unit_at(&p, UM, batch, wave, packed ? lane >> 4 : j);
+                    if (!un.uv) continue;
+                    const long wc = packed ? g2p_tail_chunk(&p, batch, wave, lane) : g2p_unit_chunk(&un, lane, i);
+                    if (wc - un.base != cc) chk("weight column of a product (not its x column)", 0, 1, 0);
+                    if (packed) break;
+                }
             } else {
                 for (int e = 0; e < VE; ++e)
                     if (x_is_data(p, VE, K, x + e)) chk("LDS x past the segment (not a zero slot)", 0, 1, 0);
@@ -136,6 +156,7 @@ int main(int argc, char **argv)
     const int L = atoi(argv[1]), E = atoi(argv[2]), NH = atoi(argv[3]), V = atoi(argv[4]), F = atoi(argv[5]);
     const int VE = atoi(argv[6]), pos = atoi(argv[7]), nwg = atoi(argv[8]);
     plant = argc > 9 ? atoi(argv[9]) : 0;
+    tail_form = g2p_step_tail(E, F, VE);
     const int S = G2_KV_MAX_SEQ, NT = G2_STEP_THREADS;
     const long xlayer = G2X_LAYER_WORDS(E, NH);
     const long xtotal = G2X_TOTAL_WORDS(L, E, NH, nwg);
