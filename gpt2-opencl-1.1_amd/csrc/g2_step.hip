@@ -40,6 +40,8 @@
  *   QKV   x (X2 of the layer before, or the embedding) -> LayerNorm ->
  *         qkv rows; writes q/k/v to the exchange and k/v to the KV cache
  *   ATTN  (head, 64-position chunk) units -> (max, sum, o[64]) partials
+ *         (scores scaled by log2(e): the maxima are in base-2 units and the
+ *         exponentials are single v_exp_f32 instructions)
  *   MERGE one work-group per head -> O
  *   PROJ  O -> proj rows + bias + x -> X1
  *   FC    X1 -> LayerNorm -> fc rows + bias -> GELU -> H
@@ -432,9 +434,10 @@ __device__ __forceinline__ ln_st ln_fold_stats(const float *red, int E)
         Q += red[NW + w];
     }
     ln_st st;
-    st.md = S / (float)E;
-    const float var = fmaxf(Q / (float)E - st.md * st.md, 0.f);
-    st.inv = 1.0f / sqrtf(var + 1e-5f);
+    const float rE = 1.0f / (float)E;
+    st.md = S * rE;
+    const float var = fmaxf(Q * rE - st.md * st.md, 0.f);
+    st.inv = __builtin_amdgcn_rsqf(var + 1e-5f); /* v_rsq_f32 */
     return st;
 }
 /* row value of a folded LayerNorm from its dot product v with (x - x0) * g */
@@ -720,9 +723,9 @@ __device__ __forceinline__ void attn_compute(int tid, const ctx &c, float scale,
         float s = 0.f;
 #pragma unroll
         for (int g = 0; g < 16; ++g) s += L.red[g][t];
-        s *= scale;
+        s *= scale; /* scale carries log2(e): scores in base-2 units */
         const float m = wmax(ok ? s : -INFINITY);
-        const float p = ok ? expf(s - m) : 0.f;
+        const float p = ok ? __builtin_amdgcn_exp2f(s - m) : 0.f; /* v_exp_f32 */
         const float l = wsum(p);
         L.pr[t] = p;
         if (t == 0) { L.stat[0] = m; L.stat[1] = l; }
@@ -1086,7 +1089,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 const bool on = u < nunits;
                 const int h = on ? u / nch : 0, ch = on ? u % nch : 0;
                 attn_load(tid, y, ar[0], on, h, ch, pos, T, E, S);
-                attn_chunk(tid, c, a.scale, R, h * 64, E + h * 64, 2 * E + h * 64,
+                attn_chunk(tid, c, a.scale * 1.4426950408889634f, R, h * 64, E + h * 64, 2 * E + h * 64,
                                   R + G2X_ATT(E) + ((size_t)h * G2_STEP_MAXCH + ch) * 66, att[hf], ar[0],
                                   on, ch, pos, T, y, h, E, S);
                 __syncthreads();
@@ -1107,7 +1110,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 const float mc = tid < nch ? xsc[tid * 66] : -INFINITY;
                 const float lc = tid < nch ? xsc[tid * 66 + 1] : 0.f;
                 const float M = wmax(mc);
-                const float w = tid < nch ? expf(mc - M) : 0.f;
+                const float w = tid < nch ? __builtin_amdgcn_exp2f(mc - M) : 0.f; /* base-2 maxima */
                 Ls = wsum(lc * w);
                 if (tid < nch) cw[tid] = w;
             }
