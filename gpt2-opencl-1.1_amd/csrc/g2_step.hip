@@ -636,10 +636,23 @@ __device__ __forceinline__ float row_sum(const plan &p, const float *part, int t
 /* Per-half LDS of the attention phase. */
 struct att_lds {
     float q[64], kn[64], vn[64];
-    float red[16][65];
+    float red[4][64]; /* per wave of the half: its 64 partial sums */
     float pr[64];
     float stat[2];
 };
+
+/* The first step of wsum4: in every lane of row 0 / 1 / 2 / 3 (lanes 0-15,
+ * 16-31, 32-47, 48-63), the sum over the four rows of a / c / b / d at the
+ * lane's position in its row (lane % 16). */
+__device__ __forceinline__ float xsum4(float a, float b, float c, float d)
+{
+    const auto s1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    const float ab = __uint_as_float(s1[0]) + __uint_as_float(s1[1]);
+    const auto s2 = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(d), false, false);
+    const float cd = __uint_as_float(s2[0]) + __uint_as_float(s2[1]);
+    const auto s3 = __builtin_amdgcn_permlane16_swap(__float_as_uint(ab), __float_as_uint(cd), false, false);
+    return __uint_as_float(s3[0]) + __uint_as_float(s3[1]);
+}
 
 /* Cached keys and values of one 64-position chunk, loaded into registers
  * ahead of their use (they do not depend on this position's q): the keys
@@ -714,15 +727,15 @@ __device__ __forceinline__ void attn_compute(int tid, const ctx &c, float scale,
                 s[3] = fmaf(qv, kv.w, s[3]);
             }
         }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) L.red[dg][4 * pq + e] = s[e];
+        /* the wave's four dimension groups (lane rows) summed by lane
+         * swaps: row r holds position 4 pq + (0, 2, 1, 3)[r] */
+        const int rr = (t >> 4) & 3;
+        L.red[t >> 6][4 * pq + (rr == 1 ? 2 : (rr == 2 ? 1 : rr))] = xsum4(s[0], s[1], s[2], s[3]);
     }
     __syncthreads();
     if (on && t < 64) {
         const bool ok = j0 + t < T;
-        float s = 0.f;
-#pragma unroll
-        for (int g = 0; g < 16; ++g) s += L.red[g][t];
+        float s = ((L.red[0][t] + L.red[1][t]) + L.red[2][t]) + L.red[3][t];
         s *= scale; /* scale carries log2(e): scores in base-2 units */
         const float m = wmax(ok ? s : -INFINITY);
         const float p = ok ? __builtin_amdgcn_exp2f(s - m) : 0.f; /* v_exp_f32 */
@@ -746,14 +759,14 @@ __device__ __forceinline__ void attn_compute(int tid, const ctx &c, float scale,
                 o[3] = fmaf(p, v.w, o[3]);
             }
         }
-#pragma unroll
-        for (int f = 0; f < 4; ++f) L.red[jg][4 * d4 + f] = o[f];
+        /* the wave's four position groups summed the same way: row r
+         * holds dimension 4 d4 + (0, 2, 1, 3)[r] */
+        const int rr = (t >> 4) & 3;
+        L.red[t >> 6][4 * d4 + (rr == 1 ? 2 : (rr == 2 ? 1 : rr))] = xsum4(o[0], o[1], o[2], o[3]);
     }
     __syncthreads();
     if (on && t < 64) {
-        float o = 0.f;
-#pragma unroll
-        for (int g = 0; g < 16; ++g) o += L.red[g][t];
+        const float o = ((L.red[0][t] + L.red[1][t]) + L.red[2][t]) + L.red[3][t];
         ll_put(pout + 2 + t, o, c.tag);
         if (t == 0) {
             ll_put(pout, L.stat[0], c.tag);
@@ -967,7 +980,6 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     __shared__ float part[G2_STEP_MAXUNITS];
     __shared__ float red[2 * NW];
     __shared__ att_lds att[2];
-    __shared__ float cw[G2_STEP_MAXCH];
     __shared__ float amv[NT];
     __shared__ int ami[NT];
     __shared__ volatile int dead;
@@ -1105,19 +1117,16 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             const int tid = fresh_tid();
             const u64 *hp = R + G2X_ATT(E) + (size_t)h * G2_STEP_MAXCH * 66;
             fetch2<NPM2>(tid, c, hp, nch * 66, xsc); /* 66 words per chunk: even, at even words */
-            float Ls = 0.f;
+            /* wave 0 alone: lane ch holds chunk ch's weight, which every
+             * lane reads by readlane (no LDS round trip, no barrier) */
             if (tid < 64) {
                 const float mc = tid < nch ? xsc[tid * 66] : -INFINITY;
                 const float lc = tid < nch ? xsc[tid * 66 + 1] : 0.f;
                 const float M = wmax(mc);
                 const float w = tid < nch ? __builtin_amdgcn_exp2f(mc - M) : 0.f; /* base-2 maxima */
-                Ls = wsum(lc * w);
-                if (tid < nch) cw[tid] = w;
-            }
-            __syncthreads();
-            if (tid < 64) {
+                const float Ls = wsum(lc * w);
                 float acc = 0.f;
-                for (int ch = 0; ch < nch; ++ch) acc = fmaf(xsc[ch * 66 + 2 + tid], cw[ch], acc);
+                for (int ch = 0; ch < nch; ++ch) acc = fmaf(xsc[ch * 66 + 2 + tid], row_lane(w, ch), acc);
                 vput(RV + G2V_O(E) + h * 64 + tid, RN + G2V_O(E) + h * 64 + tid, acc / Ls);
             }
             __syncthreads();
