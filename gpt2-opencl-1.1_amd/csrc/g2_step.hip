@@ -545,12 +545,12 @@ __device__ __forceinline__ void dot_set(int tid, const u32x4 (&w)[UM][4], const 
     float xv[4][VE];
     const int xo = g2p_dot_x(&p, VE, wave, lane, 0);
     /* slot 3 of a tail plan multiplies the packed chunks */
-    const int x3 = (UM == 4 && TAIL) ? g2p_tail_x(&p, VE, wave, lane) : xo + 3 * 64 * VE;
+    const int x3 = (UM == 4 && TAIL) ? g2p_tail_x(&p, VE, wave, lane) : xo + 3 * 64 * 4;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
         for (int e = 0; e < VE; e += 4) {
-            const f32x4 v = *(const f32x4 *)(xin + (i == 3 ? x3 : xo + 64 * VE * i) + e);
+            const f32x4 v = *(const f32x4 *)(xin + g2p_x_elem(i == 3 ? x3 : xo + 64 * 4 * i, VE, e));
             xv[i][e] = v.x;
             xv[i][e + 1] = v.y;
             xv[i][e + 2] = v.z;

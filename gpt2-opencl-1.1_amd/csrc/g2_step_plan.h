@@ -110,7 +110,7 @@ G2P_FN long g2p_tail_chunk(const g2p_rows *p, int batch, int wave, int lane)
  * segment's end, which cancels the clamped weight chunk) */
 G2P_FN int g2p_tail_x(const g2p_rows *p, int VE, int wave, int lane)
 {
-    return ((wave & (p->nseg - 1)) * G2P_SEGC + 3 * 64 + (lane & 15)) * VE;
+    return (wave & (p->nseg - 1)) * (G2P_SEGC * VE) + 4 * (3 * 64 + (lane & 15));
 }
 
 /* The input chunk lane `lane` of wave `wave` multiplies in slot i of the
@@ -137,18 +137,29 @@ G2P_FN int g2p_dot_chunk(const g2p_rows *p, int wave, int lane, int i)
 #define G2P_XE_FLOATS 2048 /* K = n_embd: up to 2 segments of 256 chunks of 4, or 1 of 8 */
 #define G2P_XF_FLOATS 8192 /* K = ffn: up to 8 segments of 256 chunks of 4, or 4 of 8 */
 
+/* Within a segment, chunk c's values are 16-byte quads at 4 c: for VE = 4
+ * the chunk itself, for VE = 8 its first four values in one plane of 256
+ * quads and its last four at the same place of a second plane (so the 16-byte
+ * reads of consecutive lanes, which take consecutive chunks, are
+ * consecutive: no bank conflicts).  The position of value e (< VE) of the
+ * chunk whose first value is at x: */
+G2P_FN int g2p_x_elem(int x, int VE, int e)
+{
+    return VE == 8 ? x + (e >> 2) * (G2P_SEGC * 4) + (e & 3) : x + e;
+}
+
 /* the padded position of input value k */
 G2P_FN int g2p_x_slot(const g2p_rows *p, int VE, int k)
 {
-    const int seg = p->SL * VE;
-    return (k / seg) * (G2P_SEGC * VE) + (k % seg);
+    const int seg = p->SL * VE, off = k % seg;
+    return (k / seg) * (G2P_SEGC * VE) + g2p_x_elem(4 * (off / VE), VE, off % VE);
 }
 
-/* the first x value lane `lane` of wave `wave` multiplies in slot i (its
- * VE values follow) */
+/* the first x value lane `lane` of wave `wave` multiplies in slot i (the
+ * others at g2p_x_elem) */
 G2P_FN int g2p_dot_x(const g2p_rows *p, int VE, int wave, int lane, int i)
 {
-    return ((wave & (p->nseg - 1)) * G2P_SEGC + lane + 64 * i) * VE;
+    return (wave & (p->nseg - 1)) * (G2P_SEGC * VE) + 4 * (lane + 64 * i);
 }
 
 /* Whether every four-unit plan of a model (qkv, fc and lm_head with K =

@@ -78,11 +78,14 @@ static void load_set(const char *what, const g2p_rows &p, int UM, int batch, lon
     (void)VE;
 }
 
-/* whether padded slot x holds an input value (k < K) */
+/* whether padded slot x holds an input value (k < K): the inverse of
+ * g2p_x_slot (segment, plane, chunk, value) */
 static bool x_is_data(const g2p_rows &p, int VE, long K, long x)
 {
     const long seg = x / ((long)G2P_SEGC * VE), off = x % ((long)G2P_SEGC * VE);
-    return off < (long)p.SL * VE && seg * p.SL * VE + off < K;
+    const long plane = VE == 8 ? off / (G2P_SEGC * 4) : 0, r = off % (G2P_SEGC * 4);
+    const long c = r / 4, e = 4 * plane + r % 4;
+    return c < p.SL && seg * p.SL * VE + c * VE + e < K;
 }
 
 /* dot_set's LDS reads of x (K floats written to a padded buffer of xcap
@@ -92,7 +95,10 @@ static void dot_set(const char *what, const g2p_rows &p, int UM, int batch, int 
     for (long k = 0; k < K; k += 4) {
         const long x = g2p_x_slot(&p, VE, (int)k);
         chk("LDS input quad", x, x + 4, xcap);
-        if (!x_is_data(p, VE, K, x)) chk("LDS input quad outside the data slots", 0, 1, 0);
+        for (int e = 0; e < 4; ++e)
+            if (!x_is_data(p, VE, K, x + e)) chk("LDS input quad outside the data slots", 0, 1, 0);
+        for (int e = 0; e < 4; ++e)
+            if (g2p_x_slot(&p, VE, (int)k + e) != x + e) chk("LDS input quad not contiguous", 0, 1, 0);
     }
     for (int tid = 0; tid < G2_STEP_THREADS; ++tid) {
         const int wave = tid >> 6, lane = tid & 63;
@@ -100,7 +106,7 @@ static void dot_set(const char *what, const g2p_rows &p, int UM, int batch, int 
         for (int i = 0; i < 4; ++i) {
             const bool packed = i == 3 && UM == 4 && tail_form;
             long x = (packed ? g2p_tail_x(&p, VE, wave, lane) : g2p_dot_x(&p, VE, wave, lane, i)) + (plant == 2 ? VE : 0);
-            chk("LDS x", x, x + VE, xcap);
+            for (int e = 0; e < VE; e += 4) chk("LDS x", g2p_x_elem((int)x, VE, e), g2p_x_elem((int)x, VE, e) + 4, xcap);
             int cc = g2p_dot_chunk(&p, wave, lane, i);
             if (packed) { /* chunk 192 + lane % 16 of the wave's segment */
                 const int c0 = (wave & (p.nseg - 1)) * p.SL, c1 = g2p_min(p.C, c0 + p.SL);
@@ -119,7 +125,7 @@ static void dot_set(const char *what, const g2p_rows &p, int UM, int batch, int 
                 }
             } else {
                 for (int e = 0; e < VE; ++e)
-                    if (x_is_data(p, VE, K, x + e)) chk("LDS x past the segment (not a zero slot)", 0, 1, 0);
+                    if (x_is_data(p, VE, K, g2p_x_elem((int)x, VE, e))) chk("LDS x past the segment (not a zero slot)", 0, 1, 0);
             }
         }
         for (int j = 0; j < UM; ++j) {
