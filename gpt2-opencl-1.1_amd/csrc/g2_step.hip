@@ -810,19 +810,36 @@ __device__ __forceinline__ bool am_better2(float v1, int i1, float v2, int i2)
     return v1 > v2 || (v1 == v2 && i1 < i2);
 }
 
-/* First-max over the work-group's (bv, bi); result in amv[0], ami[0]. */
+/* First-max over the work-group's (bv, bi); result in amv[0], ami[0].  The
+ * order (larger value, then smaller index) is total, so the butterfly within
+ * each wave and the pass over the waves' results find the same element as any
+ * other reduction order; two barriers instead of one per halving. */
 __device__ __forceinline__ void blk_argmax(int tid, float bv, int bi, float *amv, int *ami)
 {
-    amv[tid] = bv;
-    ami[tid] = bi;
-    __syncthreads();
-    for (int s = NT / 2; s > 0; s >>= 1) {
-        if (tid < s && am_better2(amv[tid + s], ami[tid + s], amv[tid], ami[tid])) {
-            amv[tid] = amv[tid + s];
-            ami[tid] = ami[tid + s];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v2 = __shfl_xor(bv, o);
+        const int i2 = __shfl_xor(bi, o);
+        if (am_better2(v2, i2, bv, bi)) {
+            bv = v2;
+            bi = i2;
         }
-        __syncthreads();
     }
+    if ((tid & 63) == 0) {
+        amv[tid >> 6] = bv;
+        ami[tid >> 6] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < NW; ++w)
+            if (am_better2(amv[w], ami[w], bv, bi)) {
+                bv = amv[w];
+                bi = ami[w];
+            }
+        amv[0] = bv;
+        ami[0] = bi;
+    }
+    __syncthreads();
 }
 
 /* Phase timestamps (only when the caller passed a trace buffer). */
