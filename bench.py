@@ -23,8 +23,17 @@ parameters, embedding rows, K/V writes), against MI355X's 8 TB/s HBM peak.
 
 cpu_baseline: the CPU oracle (a C restatement of the reference kernels with
 their accumulation order) on the host's cores, decoding a fixed sample of
-the same workload -- 100 greedy forwards at positions P+1.. over the KV
-cache the GPU prefill produced -- with the CPU model and thread placement.
+the same workload -- 100 greedy forwards at positions spread evenly over the
+GPU run's positions (mean attended length the same as the GPU's), each over
+the KV cache the GPU run wrote and with the GPU run's token for that
+position -- with the CPU model and thread placement.
+
+parity: the prompt is the one of the configuration's oracle fixture
+(tests/golden/model/<config>.npz, written by the CPU oracle from the same
+synthetic weights); after the timed region the timed decode ids are
+compared with the fixture's greedy ids (the first from prefill, then one per
+decode forward) and the bench line reports how many leading ids agree, and
+where they part, the oracle's top-2 logit gap at that step.
 
 traffic: HBM bytes per launch of that kernel from rocprofv3 counter runs
 (FETCH_SIZE and WRITE_SIZE, one run each), each scaled by what the same
@@ -60,6 +69,7 @@ CONFIGS = {"small": ("small", False, 64, 255), "medium": ("medium", False, 128, 
            "large": ("large", False, 256, 511), "large16": ("large", True, 256, 511),
            "xl": ("xl", True, 512, 511)}
 CPU_SAMPLE_FORWARDS = 100
+FIXTURES = os.path.join(ROOT, "tests", "golden", "model")
 
 
 def step_bytes(cfg, w_bytes, kv_bytes, positions):
@@ -125,11 +135,43 @@ def cpu_description():
     return model, allowed
 
 
-def cpu_baseline(g2, m, cfg, f16, P, token, n_forwards=CPU_SAMPLE_FORWARDS):
+def fixture(config, P):
+    """(prompt, greedy ids, top-2 logits) of the configuration's oracle
+    fixture, or None when it is absent or was made for another prompt
+    length."""
+    path = os.path.join(FIXTURES, f"{config}.npz")
+    try:
+        with np.load(path, allow_pickle=False) as z:
+            fx = {k: z[k] for k in ("prompt", "ids", "top2")}
+    except (OSError, KeyError, ValueError):
+        return None
+    return fx if len(fx["prompt"]) == P else None
+
+
+def parity_record(fx, config, first_tok, out):
+    """How many of the timed run's greedy ids (the prefill token, then one
+    per decode forward) agree with the oracle fixture's, leading ones."""
+    got = np.concatenate([[first_tok], out]).astype(np.int64)
+    ref = fx["ids"].astype(np.int64)
+    n = min(len(got), len(ref))
+    diff = np.flatnonzero(got[:n] != ref[:n])
+    rec = {"ids_agree": int(diff[0]) if diff.size else n, "of": n,
+           "fixture": f"tests/golden/model/{config}.npz",
+           "counted": "the prefill token, then one id per timed decode forward"}
+    if diff.size:
+        k = int(diff[0])
+        rec["parts_at"] = {"step": k, "oracle_top2_gap": float(fx["top2"][k, 0] - fx["top2"][k, 1])}
+    return rec
+
+
+def cpu_baseline(g2, m, cfg, f16, P, first_tok, out, n_forwards=CPU_SAMPLE_FORWARDS):
     """Time the oracle on a fixed sample of the same workload: n_forwards
-    greedy decode forwards at positions P+1.. over the GPU-prefilled KV
-    cache (the reference's timing method, main.c:2106-2170: wall clock
-    around the decode loop, sampling included, no printing)."""
+    greedy decode forwards at positions spread evenly over the GPU run's
+    decode positions P..P+len(out)-1, each over the KV cache the GPU run
+    wrote, with the token the GPU run fed at that position (the reference's
+    timing method, main.c:2106-2170: wall clock around the decode loop,
+    sampling included, no printing).  The sample's mean attended length is
+    the GPU run's."""
     sys.path.insert(0, ROOT)
     from oracle import oracle
     t0 = time.perf_counter()
@@ -140,14 +182,18 @@ def cpu_baseline(g2, m, cfg, f16, P, token, n_forwards=CPU_SAMPLE_FORWARDS):
         k, v = m.read_kv(l)
         om.set_kv(l, k, v)
     log(f"cpu oracle ready in {time.perf_counter() - t0:.1f}s")
-    om.decode(token, P)  # untimed first forward (page-in)
-    tok = om.greedy([token], forbid_eos=True)
-    n = min(n_forwards, 1022 - P)
+    n_dec = len(out)
+    toks = np.concatenate([[first_tok], out[:-1]]).astype(np.int64)  # token fed at position P + j
+    n = min(n_forwards, n_dec)
+    js = np.unique(np.linspace(0, n_dec - 1, n).round().astype(int))
+    n = len(js)
+    om.decode(int(toks[js[0]]), P + int(js[0]))  # untimed first forward (page-in)
     t0 = time.perf_counter()
-    for i in range(n):
-        om.decode(tok, P + 1 + i)
-        tok = om.greedy([tok], forbid_eos=True)
+    for j in js:
+        om.decode(int(toks[j]), P + int(j))
+        om.greedy([int(toks[j])], forbid_eos=True)
     dt = time.perf_counter() - t0
+    mean_t = float(np.mean(P + js + 1))
     threads = oracle.num_threads()
     om.close()
     model, allowed = cpu_description()
@@ -157,8 +203,9 @@ def cpu_baseline(g2, m, cfg, f16, P, token, n_forwards=CPU_SAMPLE_FORWARDS):
                         f"no explicit binding; process affinity CPUs {allowed[0]}-{allowed[-1]}"
                         if allowed else "none"),
             "sample": f"{n} greedy decode forwards of GPT-2 {cfg.n_layer}-layer E{cfg.n_embd} "
-                      f"({'fp16-rounded weights held as fp32' if f16 else 'fp32 weights'}) at positions "
-                      f"{P + 1}..{P + n} over the GPU-prefilled KV cache, {threads} OpenMP threads, {dt:.2f} s"}
+                      f"({'fp16-rounded weights held as fp32' if f16 else 'fp32 weights'}) at positions spread "
+                      f"evenly over {P}..{P + n_dec - 1} (mean attended length {mean_t:.0f}, as the GPU run's), "
+                      f"over the GPU run's KV cache, {threads} OpenMP threads, {dt:.2f} s"}
 
 
 def main():
@@ -201,7 +248,12 @@ def run(args, g2):
     m = g2.Model.synth(cfg, SEED, wdtype, g2.PATH_FUSED)
     log(f"{args.config} model on {name} ({cus} CUs) in {time.perf_counter() - t0:.1f}s, "
         f"{m.weight_bytes() / 2**20:.0f} MiB of weights")
-    prompt = np.random.default_rng(SEED).integers(0, cfg.vocab_size, P).astype(np.int32)
+    fx = fixture(args.config, P)
+    if fx is not None:
+        prompt = fx["prompt"].astype(np.int32)
+    else:
+        log(f"no oracle fixture for {args.config}: random prompt, parity not reported")
+        prompt = np.random.default_rng(SEED).integers(0, cfg.vocab_size, P).astype(np.int32)
 
     # prefill: prompt -> first token (device-selected), timed by HIP events
     ids, _ = m.generate(prompt, 2)  # warm-up, builds the decode graph
@@ -241,7 +293,7 @@ def run(args, g2):
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall / args.steps * 1e3, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f32", "data": "synthetic",
+        "dtype": "f16" if f16 else "f32", "data": "synthetic",
         "config": {"workload": workload,
                    "weights": "f16" if f16 else "f32", "kv_cache": "f32", "accumulate": "f32",
                    "decode_engine": "persistent step kernel" if m.uses_step() else
@@ -256,8 +308,9 @@ def run(args, g2):
                                 else "decode step (per-operator kernels)"),
                      "bytes_per_launch": round(bytes_step / n_dec)},
     }
+    result["parity"] = parity_record(fx, args.config, first_tok, ref_ids) if fx is not None else None
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(g2, m, cfg, f16, P, first_tok)
+        result["cpu_baseline"] = cpu_baseline(g2, m, cfg, f16, P, first_tok, ref_ids)
     print(json.dumps(result), flush=True)
     m.free()
 

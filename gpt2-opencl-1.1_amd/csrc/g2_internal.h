@@ -103,6 +103,8 @@ int g2i_launch3(int fid, unsigned gx, unsigned gy, unsigned gz, unsigned bx, voi
 int g2i_coop_launch(int fid, unsigned gx, unsigned bx, void *args);
 /* Work-groups of the persistent step kernel's grid (0: not supported). */
 int g2i_step_wgs(void);
+/* The code-object name of kernel fid ("" out of range). */
+const char *g2i_kernel_name(int fid);
 /* compute units of the device (after g2_init) */
 int g2i_cus(void);
 int g2i_device_alloc(void **p, size_t bytes);

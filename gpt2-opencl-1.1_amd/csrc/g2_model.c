@@ -616,6 +616,14 @@ int g2_model_uses_step(const g2_model *m)
     return m->step_on ? 1 : 0;
 }
 
+static int step_fid(const g2_model *m);
+
+const char *g2_model_step_kernel(const g2_model *m)
+{
+    if (!m || !m->step_on) return "";
+    return g2i_kernel_name(step_fid(m));
+}
+
 int g2_model_uses_graph(const g2_model *m)
 {
     if (!m) return g2i_err(G2_E_ARG, "NULL model");
@@ -757,6 +765,15 @@ static int fused_step_launches(g2_model *m)
     return rc;
 }
 
+/* The step kernel of a model: the tail form where every four-unit plan is
+ * a tail plan. */
+static int step_fid(const g2_model *m)
+{
+    const g2_config *c = &m->cfg;
+    const int tail = g2p_step_tail(c->n_embd, c->ffn_dim, m->dtype == G2_F16 ? 8 : 4);
+    return m->dtype == G2_F16 ? (tail ? G2F_STEP_F16T : G2F_STEP_F16) : (tail ? G2F_STEP_F32T : G2F_STEP_F32);
+}
+
 /* One decode forward at state[POS] as one cooperative launch of the
  * persistent step kernel. */
 static int step_launch(g2_model *m)
@@ -776,9 +793,7 @@ static int step_launch(g2_model *m)
     a.scale = 1.0f / sqrtf(64.0f);
     m->step_ran = 1;
     a.xlayer = G2X_LAYER_WORDS(c->n_embd, c->n_head);
-    /* the tail form where every four-unit plan is a tail plan */
-    const int tail = g2p_step_tail(c->n_embd, c->ffn_dim, m->dtype == G2_F16 ? 8 : 4);
-    const int fid = m->dtype == G2_F16 ? (tail ? G2F_STEP_F16T : G2F_STEP_F16) : (tail ? G2F_STEP_F32T : G2F_STEP_F32);
+    const int fid = step_fid(m);
     if (m->plain) {
         a.plain = m->plain;
         return g2i_launch(fid, (unsigned)m->step_wgs, 1, G2_STEP_THREADS, &a);

@@ -92,6 +92,8 @@ int g2i_coop_launch(int fid, unsigned gx, unsigned bx, void *args)
 }
 
 int g2i_step_wgs(void) { return G.step_wgs; }
+void *g2_stream(void) { return G.ready ? (void *)G.stream : NULL; }
+const char *g2i_kernel_name(int fid) { return fid >= 0 && fid < G2F_COUNT ? g2_kernel_names[fid] : ""; }
 int g2i_cus(void) { return G.cus > 0 ? G.cus : 1; }
 
 int g2i_device_alloc(void **p, size_t bytes)

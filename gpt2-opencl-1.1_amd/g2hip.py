@@ -110,6 +110,8 @@ _sig("g2_synth_normal", None, _vp, _sz, C.c_uint64, C.c_uint32, _f)
 _sig("g2_synth_tensor_id", C.c_uint32, _i, _i)
 _sig("g2_convert_f16", None, _vp, _vp, _sz)
 _sig("g2_model_weight_bytes", _sz, _vp)
+_sig("g2_model_step_kernel", C.c_char_p, _vp)
+_sig("g2_stream", _vp)
 
 
 def last_error():
@@ -447,23 +449,9 @@ class Model:
         return _lib.g2_model_uses_step(self.h) >= 1
 
     def step_kernel(self):
-        """Name of the persistent step kernel this model launches ("" when it
-        decodes with per-operator kernels): the tail form when every
-        four-unit row plan ends 1..16 chunks into its last slot (the rule of
-        g2p_step_tail in csrc/g2_step_plan.h)."""
-        if not self.uses_step():
-            return ""
-        ve = 8 if self.dtype == F16 else 4
-
-        def tail(K):
-            C = K // ve
-            need = -(-C // 256)
-            nseg = 1 if need <= 1 else 2 if need <= 2 else 4 if need <= 4 else 8
-            SL = -(-C // nseg)
-            return 192 < SL <= 208
-
-        base = "g2k_step_f16" if self.dtype == F16 else "g2k_step_f32"
-        return base + "_tail" if tail(self.cfg.n_embd) and tail(self.cfg.ffn_dim) else base
+        """Name of the persistent step kernel this model launches, as the
+        library reports it ("" when it decodes with per-operator kernels)."""
+        return _lib.g2_model_step_kernel(self.h).decode()
 
     def step_kind(self):
         """1: persistent step kernel, 0: per-operator kernels."""

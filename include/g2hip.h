@@ -57,6 +57,12 @@ const char *g2_last_error(void);
 int g2_init(int device);                 /* load the gfx950 code object, make the stream */
 int g2_shutdown(void);                   /* release stream, module, library buffers       */
 int g2_device_name(char *buf, int len, int *compute_units);
+/* The library's HIP stream (a hipStream_t; no counterpart in the
+ * reference, whose queue is main.c:537): every launch of the library goes to
+ * it, so a caller may capture the library's calls into its own HIP graph
+ * (hipStreamBeginCapture on this stream, the calls, hipStreamEndCapture).
+ * NULL before g2_init. */
+void *g2_stream(void);
 
 /* ---- buffers (clCreateBuffer / clEnqueue{Write,Copy,Read}Buffer / clFinish) */
 int g2_alloc(void **dptr, size_t bytes);                       /* main.c:1225, 1460-1486 */
@@ -231,6 +237,12 @@ int g2_model_uses_graph(const g2_model *m);
  * kernel) or 0 (per-operator kernels). */
 int g2_model_set_step(g2_model *m, int on);
 int g2_model_uses_step(const g2_model *m);
+/* Name of the kernel one decode forward launches when the model decodes
+ * with the persistent step kernel (g2k_step_f16 / _f32, or their tail forms
+ * g2k_step_f16_tail / _f32_tail, which the host picks when every matrix row
+ * plan ends 1..16 chunks into its last slot); "" for the per-operator
+ * kernels or a NULL model.  No counterpart in the reference. */
+const char *g2_model_step_kernel(const g2_model *m);
 
 /* prefill, main.c:1739-1790: ids[0..n) at positions 0..n-1, 1 <= n <= 1023;
  * leaves the last row's logits on the device. */

@@ -28,3 +28,16 @@ def g2():
 
     gc.collect()  # models and buffers the tests dropped are freed while the library is up
     g2hip.shutdown()
+
+
+def pytest_terminal_summary(terminalreporter, exitstatus, config):
+    """The greedy-identity record of every full-depth run, so a quiet run
+    (pytest -q) still states how many ids agreed with the oracle."""
+    try:
+        from parity import IDENTITY_RECORDS
+    except ImportError:
+        return
+    if IDENTITY_RECORDS:
+        terminalreporter.section("greedy identity against the oracle (full depth)")
+        for line in IDENTITY_RECORDS:
+            terminalreporter.write_line(line)

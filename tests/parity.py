@@ -30,6 +30,11 @@ def assert_close_bound(got, ref, bound, slack=1e-6, what=""):
 
 TIE_TOL = 1e-4  # largest oracle top-2 logit gap at which the greedy ids may part
 
+# One line per full-depth run (configuration, path, how many free-running
+# greedy ids agreed with the oracle's, teacher-forced agreement, logit
+# error), printed in pytest's terminal summary even under -q.
+IDENTITY_RECORDS = []
+
 
 def greedy_agree(gpu_ids, ref_ids, ref_top2, tie_tol=TIE_TOL):
     """Greedy sequences must be identical, except that they may part at a

@@ -35,6 +35,8 @@ import os
 import numpy as np
 import pytest
 
+from parity import IDENTITY_RECORDS
+
 pytestmark = pytest.mark.gpu
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -84,17 +86,24 @@ def test_full_depth_matches_oracle(g2, name, path):
     else:
         assert m.uses_step(), "the fused path decodes with the step kernel"
 
-    # 1. free-running greedy generation
+    # 1. free-running greedy generation: identical for all n_gen ids, or
+    # parting only at a step where the oracle's own top-2 gap is below
+    # TIE_TOL (after which the contexts differ; step 2 then covers every
+    # later step)
     ids, _ = m.generate(prompt, n_gen, min_new=n_gen)
     assert len(ids) == n_gen
     diff = np.flatnonzero(ids != ref_ids)
+    agree = int(diff[0]) if diff.size else n_gen
     if diff.size:
-        k = int(diff[0])
-        print(f"[full] {name} {path}: free-running ids part at step {k} (oracle top-2 gap {gaps[k]:.3e})",
-              flush=True)
-        assert gaps[k] < TIE_TOL, f"greedy ids differ at step {k} with oracle top-2 gap {gaps[k]:.3e}"
+        k = agree
+        free = (f"free-running ids agree for the first {k} of {n_gen}, parting at step {k} "
+                f"(oracle top-2 gap {gaps[k]:.3e} < {TIE_TOL:g})")
+        print(f"[full] {name} {path}: {free}", flush=True)
+        assert gaps[k] < TIE_TOL, (f"{name} {path}: free-running ids agree for {k} of {n_gen}, then differ at "
+                                   f"step {k} with oracle top-2 gap {gaps[k]:.3e} >= {TIE_TOL:g}")
     else:
-        print(f"[full] {name} {path}: free-running ids identical for all {n_gen} tokens", flush=True)
+        free = f"free-running ids identical for all {n_gen} of {n_gen}"
+        print(f"[full] {name} {path}: {free}", flush=True)
 
     # 2. teacher-forced along the oracle's ids
     ck = {int(s): i for i, s in enumerate(fx["ck_steps"])}
@@ -122,5 +131,9 @@ def test_full_depth_matches_oracle(g2, name, path):
             np.testing.assert_allclose(got, ref, rtol=rtol, atol=atol, err_msg=f"{name} {path} step {k}")
     print(f"[full] {name} {path}: teacher-forced greedy choices agree at {n_gen - len(partings)} of {n_gen} "
           f"steps {partings if partings else ''}; max logit error {max_err:.3e}", flush=True)
+    IDENTITY_RECORDS.append(
+        f"{name} {path} (L{cfg.n_layer} E{cfg.n_embd} {'f16' if f16 else 'f32'}, P {P}): {free}; teacher-forced "
+        f"choices agree at {n_gen - len(partings)} of {n_gen}"
+        f"{' (near ties ' + str(partings) + ')' if partings else ''}; max |logit - oracle| {max_err:.2e}")
     assert max_err < TIE_TOL, f"logit error {max_err:.3e} exceeds the near-tie bound {TIE_TOL}"
     m.free()

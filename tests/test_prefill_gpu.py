@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle
-from parity import random_prompt
+from parity import TIE_TOL, random_prompt
 
 pytestmark = pytest.mark.gpu
 
@@ -39,8 +39,9 @@ def test_prefill_split_fp16_mfma(g2, monkeypatch, P):
     om.close()
     np.testing.assert_allclose(lg_h, ref, rtol=5e-2, atol=5e-2)
     np.testing.assert_allclose(lg_h, lg_f, rtol=1e-3, atol=2e-3)
-    assert int(np.argmax(lg_h)) == int(np.argmax(ref)) or \
-        np.sort(ref)[-1] - np.sort(ref)[-2] < 1e-2
+    top2 = np.sort(ref)[-2:]
+    assert int(np.argmax(lg_h)) == int(np.argmax(ref)) or top2[1] - top2[0] < TIE_TOL, \
+        f"P {P}: gpu argmax {int(np.argmax(lg_h))}, oracle {int(np.argmax(ref))}, oracle top-2 gap {top2[1] - top2[0]:.3e}"
 
 
 @pytest.mark.parametrize("P", [65, 200, 512, 1023])
