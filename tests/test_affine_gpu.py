@@ -88,3 +88,52 @@ def test_affine_parameters(g2, shape, engine, P):
         assert c == ref_ids[k] or gaps[k] < TIE_TOL, f"step {k}: gpu {c} oracle {ref_ids[k]} gap {gaps[k]:.3e}"
     print(f"[affine] {shape} {engine} P {P}: max logit error {max_err:.3e}", flush=True)
     m.free()
+
+
+OUTLIERS = {0: 8.0, 7: -6.0, "mid": 10.0}
+
+
+@pytest.mark.parametrize("engine", ["ops-f32", "step-f32", "ops-f16", "step-f16"])
+@pytest.mark.parametrize("shape", ["small-width", "xl-width"])
+def test_layernorm_fold_outlier_dims(g2, shape, engine):
+    """The step kernel folds each LayerNorm into the matrix after it with a
+    shift x0 = x[0] (W.LN(x) = inv (W.((x - x0) g) - (mean - x0) c1) + c2);
+    its rounding grows with |mean - x0| / std.  Real GPT-2 activations have
+    a few hidden dimensions far larger than the rest.  Here three are
+    planted, dimension 0 (the shift itself) among them: constant offsets of
+    +8, -6 and +10 on every position's embedding in dimensions 0, 7 and E/2
+    (wpe; wte is also the tied lm_head), so at every LayerNorm
+    |x[0] - mean| / std is about 20.  The step kernel
+    (folded) and the per-operator kernels (a direct two-pass LayerNorm) must
+    both stay within the parity bound of the oracle, teacher-forced at every
+    step, with random biases and LayerNorm parameters."""
+    L, E, H, V = SHAPES[shape]
+    cfg = g2.make_config(L, E, H, vocab_size=V)
+    f16 = engine.endswith("f16")
+    w = g2.synth_weights(cfg, SEED, f16_round=f16, affine=True)
+    for d, off in OUTLIERS.items():  # position embeddings: wte is also the lm_head
+        w["wpe"][:, E // 2 if d == "mid" else d] += off
+    if f16:  # the device stores fp16 embeddings: the oracle must hold the same values
+        w["wpe"] = w["wpe"].astype(np.float16).astype(np.float32)
+    om = oracle.Model(cfg, w, kslice=4)
+    P, n_new = 40, 16
+    prompt = random_prompt(P, V, 91)
+    ref_ids, top2, _ = om.generate(prompt, n_new, min_new=n_new)
+    gaps = top2[:, 0] - top2[:, 1]
+    ref_lg = om.teacher_forced(prompt, ref_ids[:-1])
+    om.close()
+    m = g2.Model.from_host(cfg, w, g2.F16 if f16 else g2.F32, g2.PATH_FUSED)
+    m.set_step(engine.startswith("step"))
+    m.prefill(prompt)
+    errs = []
+    for k in range(n_new):
+        if k > 0:
+            m.decode(int(ref_ids[k - 1]), P + k - 1)
+        lg = m.logits()
+        errs.append(float(np.abs(lg - ref_lg[k]).max()))
+        assert errs[-1] < ATOL, f"step {k}: max |logit - oracle| {errs[-1]:.3e}"
+        c = masked_argmax(lg)
+        assert c == ref_ids[k] or gaps[k] < TIE_TOL, f"step {k}: gpu {c} oracle {ref_ids[k]} gap {gaps[k]:.3e}"
+    print(f"\n[outlier] {shape} {engine}: max logit error {max(errs):.3e} over {n_new} steps (prefill "
+          f"{errs[0]:.2e}, decode {max(errs[1:]):.2e}; logits up to {float(np.abs(ref_lg).max()):.1f})", flush=True)
+    m.free()
