@@ -64,7 +64,7 @@ extern "C" {
     X(HGEMM_PARTIAL, "g2k_hgemm_partial") X(SPLITK_RESID, "g2k_splitk_resid") \
     X(HGEMM2_GELU, "g2k_hgemm2_gelu") X(HGEMM2_RESID, "g2k_hgemm2_resid")     \
     X(HGEMM2_QKV, "g2k_hgemm2_qkv") X(HGEMM2_PARTIAL, "g2k_hgemm2_partial")   \
-    X(LAYERNORM_SPLIT, "g2k_layernorm_split") X(SPLITK_RESID_LN, "g2k_splitk_resid_ln") \
+    X(LAYERNORM_SPLIT, "g2k_layernorm_split") X(SPLITK_RESID_LN, "g2k_splitk_resid_ln") X(SPLITK_RESID_LN_F32, "g2k_splitk_resid_ln_f32") \
     X(SGEMM_GELU, "g2k_sgemm_gelu") X(SGEMM_RESID, "g2k_sgemm_resid")         \
     X(SGEMM_QKV, "g2k_sgemm_qkv") X(SGEMM_PARTIAL, "g2k_sgemm_partial")       \
     X(SPLITK_EPI, "g2k_splitk_epi")                                           \

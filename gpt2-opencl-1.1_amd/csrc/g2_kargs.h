@@ -70,7 +70,8 @@ typedef struct {
 /* C[m,n] = C[m,n] + ((sum over z < ks in order of part[z*M*N + m*N + n]) +
  * bias[n]) for m < M, n < N.  g2k_splitk_resid_ln (grid M, N <=
  * G2_SKLN_MAXN) then writes LayerNorm(C[m,:]; ln_g, ln_b) as fp16 halves
- * to hi, lo [M,N] (see g2_lnsplit_args). */
+ * to hi, lo [M,N] (see g2_lnsplit_args); g2k_splitk_resid_ln_f32 writes it
+ * as fp32 to ln_out [M,N] (the operand of the fp32-weight GEMM). */
 typedef struct {
     const float *part;
     const float *bias;
@@ -78,9 +79,11 @@ typedef struct {
     int M, N, ks;
     const float *ln_g, *ln_b;
     uint16_t *hi, *lo;
+    float *ln_out;
 } g2_skred_args;
 #define G2_SKLN_MAXN 2048
-#define G2_SKLN_MAXKS 5 /* slices g2k_splitk_resid_ln reads (ks <= this) */
+#define G2_SKLN_MAXKS 5     /* slices g2k_splitk_resid_ln reads (ks <= this) */
+#define G2_SKLN_F32_MAXKS 8 /* slices g2k_splitk_resid_ln_f32 reads */
 
 /* The split-K epilogue of the fp32-weight prefill GEMM (g2k_splitk_epi):
  * v[m,n] = (sum over z < ks in order of part[z][m][n]) + bias[n], then epi

@@ -1190,10 +1190,13 @@ G2K_HG2 void g2k_hgemm2_partial(const g2_gemm_args a) { hgemm2_impl<GEPI_PARTIAL
 /* The split-K residual epilogue fused with the LayerNorm that follows it
  * in the prefill (proj -> ln_2, fc2 -> the next layer's ln_1): one
  * work-group per row sums the slices, bias and residual as
- * g2k_splitk_resid does, keeps the row in registers, and normalises it as
- * g2k_layernorm does (same sums in the same order), writing the fp16
- * halves of the next GEMM's operand. */
-G2K void g2k_splitk_resid_ln(const g2_skred_args a)
+ * g2k_splitk_resid does, keeps the row in registers, and normalises it
+ * (two-pass mean and biased variance, eps 1e-5, as g2k_layernorm), writing
+ * the next GEMM's operand: its fp16 halves (the fp16-weight GEMMs, at most
+ * G2_SKLN_MAXKS slices) or fp32 (F32OUT: the fp32-weight GEMMs, at most
+ * G2_SKLN_F32_MAXKS slices). */
+template <int ZMAX, bool F32OUT>
+__device__ __forceinline__ void splitk_resid_ln_impl(const g2_skred_args &a)
 {
     /* thread t owns the 4-column groups t and t + 256 of the row (N % 4 ==
      * 0, N <= G2_SKLN_MAXN); every load of both groups -- all slices, the
@@ -1201,7 +1204,6 @@ G2K void g2k_splitk_resid_ln(const g2_skred_args a)
      * first sum (unconditional, clamped into the row), so the row costs
      * one memory latency instead of one per group */
     constexpr int PG = G2_SKLN_MAXN / 1024; /* groups per thread */
-    constexpr int ZMAX = G2_SKLN_MAXKS;      /* slices read at once (ks <= ZMAX) */
     __shared__ float red4[4];
     const int m = blockIdx.x, N = a.N, NG = N >> 2;
     if (m >= a.M) return;
@@ -1258,16 +1260,22 @@ G2K void g2k_splitk_resid_ln(const g2_skred_args a)
             float y[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) y[e] = fmaf((xv[k][e] - mean) * inv, gv[k][e], ev[k][e]);
-            uint2 hv, lv;
-            hv.x = pk16(hi16(y[0]), hi16(y[1]));
-            hv.y = pk16(hi16(y[2]), hi16(y[3]));
-            lv.x = pk16(lo16(y[0]), lo16(y[1]));
-            lv.y = pk16(lo16(y[2]), lo16(y[3]));
-            *(uint2 *)(a.hi + row + 4 * g) = hv;
-            *(uint2 *)(a.lo + row + 4 * g) = lv;
+            if constexpr (F32OUT) {
+                *(f32x4 *)(a.ln_out + row + 4 * g) = (f32x4){y[0], y[1], y[2], y[3]};
+            } else {
+                uint2 hv, lv;
+                hv.x = pk16(hi16(y[0]), hi16(y[1]));
+                hv.y = pk16(hi16(y[2]), hi16(y[3]));
+                lv.x = pk16(lo16(y[0]), lo16(y[1]));
+                lv.y = pk16(lo16(y[2]), lo16(y[3]));
+                *(uint2 *)(a.hi + row + 4 * g) = hv;
+                *(uint2 *)(a.lo + row + 4 * g) = lv;
+            }
         }
     }
 }
+G2K void g2k_splitk_resid_ln(const g2_skred_args a) { splitk_resid_ln_impl<G2_SKLN_MAXKS, false>(a); }
+G2K void g2k_splitk_resid_ln_f32(const g2_skred_args a) { splitk_resid_ln_impl<G2_SKLN_F32_MAXKS, true>(a); }
 
 G2K void g2k_hgemm_store(const g2_gemm_args a) { hgemm_impl<GEPI_STORE>(a); }
 G2K void g2k_hgemm_gelu(const g2_gemm_args a) { hgemm_impl<GEPI_GELU>(a); }

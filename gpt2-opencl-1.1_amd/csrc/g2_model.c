@@ -926,7 +926,7 @@ static int prefill_resid(g2_model *m, const float *A, const uint16_t *Ah, const 
     if (ks == 1) return g2i_launch(big ? G2F_HGEMM2_RESID : G2F_HGEMM_RESID, bx, by, big ? 1024 : 256, &g);
     g.part = m->pf_part; g.ksplit = ks;
     int rc = g2i_launch3(big ? G2F_HGEMM2_PARTIAL : G2F_HGEMM_PARTIAL, bx, by, (unsigned)ks, big ? 1024 : 256, &g);
-    g2_skred_args r = { m->pf_part, bias, C, P, N, ks, ln_g, ln_b, hi, lo };
+    g2_skred_args r = { m->pf_part, bias, C, P, N, ks, ln_g, ln_b, hi, lo, NULL };
     if (!rc && ln_g && big && N <= G2_SKLN_MAXN && N % 4 == 0 && ks <= G2_SKLN_MAXKS) {
         *ln_done = 1;
         return g2i_launch(G2F_SPLITK_RESID_LN, (unsigned)P, 1, 256, &r);
@@ -945,9 +945,13 @@ static int prefill_resid(g2_model *m, const float *A, const uint16_t *Ah, const 
  * Measured at 64..512 rows and n_embd 768..1280, this picks the best or
  * within 10% of the best of 1..8 slices for every GEMM.  ks slices of at
  * most 64 ceil(M/64) x 64 ceil(N/64) floats each fit G2_SG_PART_FLOATS:
- * ks * tiles <= 512. */
-static int prefill_sgemm(g2_model *m, int epi, g2_gemm_args *g)
+ * ks * tiles <= 512.  With ln_g (a residual epilogue followed by a
+ * LayerNorm: proj -> ln_2, fc2 -> the next ln_1) the slice sum is fused
+ * with that LayerNorm (g2k_splitk_resid_ln_f32, writing m->ln_out) and
+ * *ln_done is set; otherwise the caller runs it. */
+static int prefill_sgemm(g2_model *m, int epi, g2_gemm_args *g, const float *ln_g, const float *ln_b, int *ln_done)
 {
+    *ln_done = 0;
     const unsigned gx = cdivu(g->N, 64), gy = cdivu(g->M, 64), tiles = gx * gy;
     const int nk = g->K / 32;
     const unsigned target = nk >= 64 ? 512 : 256;
@@ -960,6 +964,11 @@ static int prefill_sgemm(g2_model *m, int epi, g2_gemm_args *g)
                           gx, gy, 256, g);
     g->part = m->pf_part;
     int rc = g2i_launch3(G2F_SGEMM_PARTIAL, gx, gy, (unsigned)ks, 256, g);
+    if (!rc && epi == G2_SG_RESID && ln_g && g->N <= G2_SKLN_MAXN && g->N % 4 == 0 && ks <= G2_SKLN_F32_MAXKS) {
+        g2_skred_args r = { m->pf_part, g->bias, g->C, g->M, g->N, ks, ln_g, ln_b, NULL, NULL, m->ln_out };
+        *ln_done = 1;
+        return g2i_launch(G2F_SPLITK_RESID_LN_F32, (unsigned)g->M, 1, 256, &r);
+    }
     g2_skepi_args e = { m->pf_part, g->bias, g->C, g->q_out, g->k_cache, g->v_cache, g->M, g->N, ks, epi,
                         g->E, g->S, g->pos0, g->kh, g->kl, g->vth, g->vtl };
     const unsigned n4 = cdivu((unsigned)(g->M * g->N / 4), 256);
@@ -999,6 +1008,7 @@ static int fused_prefill(g2_model *m, int P)
     g2_embed_args e = { m->wte, m->wpe, m->hidden, m->ids_dev, NULL, E, P, 0 };
     int rc = g2i_launch(f16 ? G2F_EMBED_F16 : G2F_EMBED_F32, cdivu(E, 256), (unsigned)P, 256, &e);
     int ln1_done = 0; /* the previous layer's fc2 sum already wrote this layer's ln_1 */
+    int ln_unused = 0;
     const char *ea = getenv("G2_PREFILL_ATTN32");
     const int attn32 = ea && ea[0] == '1'; /* attention on the fp32 matrix cores (reference point) */
     for (int l = 0; l < m->cfg.n_layer && !rc; ++l) {
@@ -1014,7 +1024,7 @@ static int fused_prefill(g2_model *m, int P)
         g.E = E; g.S = G2_KV_MAX_SEQ; g.pos0 = 0;
         g.kh = kv_kh; g.kl = kv_kl; g.vth = kv_vh; g.vtl = kv_vl;
         if (!rc) rc = big ? g2i_launch(f_qkv, 8 * cdivu(cdivu(3 * E, 128), 8) * cdivu(P, 128), 1, 1024, &g)
-                      : sg  ? prefill_sgemm(m, G2_SG_QKV, &g)
+                      : sg  ? prefill_sgemm(m, G2_SG_QKV, &g, NULL, NULL, &ln_unused)
                             : g2i_launch(f_qkv, cdivu(3 * E, 64), cdivu(P, 64), 256, &g);
         g2_attnp_args t = { m->q, y->k_cache, y->v_cache, m->attn, P, E, NH, G2_KV_MAX_SEQ, 1.0f / sqrtf(64.0f),
                             big ? at_h : NULL, big ? at_l : NULL, kv_kh, kv_kl, kv_vh, kv_vl };
@@ -1026,7 +1036,7 @@ static int fused_prefill(g2_model *m, int P)
         int ln2_done = 0;
         if (!rc) rc = h ? prefill_resid(m, m->attn, at_h, at_l, y->proj_w, y->proj_b, m->hidden, P, E, E, big,
                                         y->ln2_w, y->ln2_b, ln_h, ln_l, &ln2_done)
-                      : sg ? prefill_sgemm(m, G2_SG_RESID, &g)
+                      : sg ? prefill_sgemm(m, G2_SG_RESID, &g, y->ln2_w, y->ln2_b, &ln2_done)
                            : g2i_launch(f_resid, cdivu(E, 64), cdivu(P, 64), 256, &g);
         g2_lnsplit_args ls2 = { m->hidden, ln_h, ln_l, y->ln2_w, y->ln2_b, E, P };
         if (!rc && !ln2_done)
@@ -1036,7 +1046,7 @@ static int fused_prefill(g2_model *m, int P)
         g.A = m->ln_out; g.B = y->fc_w; g.bias = y->fc_b; g.C = m->ffn1; g.M = P; g.N = F; g.K = E;
         g.Ah = ln_h; g.Al = ln_l; g.Ch = ff_h; g.Cl = ff_l;
         if (!rc) rc = big ? g2i_launch(f_gelu, 8 * cdivu(cdivu(F, 128), 8) * cdivu(P, 128), 1, 1024, &g)
-                      : sg  ? prefill_sgemm(m, G2_SG_GELU, &g)
+                      : sg  ? prefill_sgemm(m, G2_SG_GELU, &g, NULL, NULL, &ln_unused)
                             : g2i_launch(f_gelu, cdivu(F, 64), cdivu(P, 64), 256, &g);
         memset(&g, 0, sizeof g);
         g.A = m->ffn1; g.B = y->fc2_w; g.bias = y->fc2_b; g.C = m->hidden; g.M = P; g.N = E; g.K = F;
@@ -1044,7 +1054,8 @@ static int fused_prefill(g2_model *m, int P)
         ln1_done = 0;
         if (!rc) rc = h ? prefill_resid(m, m->ffn1, ff_h, ff_l, y->fc2_w, y->fc2_b, m->hidden, P, E, F, big,
                                         yn ? yn->ln1_w : NULL, yn ? yn->ln1_b : NULL, ln_h, ln_l, &ln1_done)
-                      : sg ? prefill_sgemm(m, G2_SG_RESID, &g)
+                      : sg ? prefill_sgemm(m, G2_SG_RESID, &g, yn ? yn->ln1_w : NULL, yn ? yn->ln1_b : NULL,
+                                           &ln1_done)
                            : g2i_launch(f_resid, cdivu(E, 64), cdivu(P, 64), 256, &g);
     }
     if (!rc) rc = fused_lm_head(m, m->hidden + (size_t)(P - 1) * E, 1);
