@@ -32,9 +32,29 @@ def test_step_kernel_is_default(g2):
         m.free()
     m = g2.Model.synth(g2.make_config(2, 128, 2, vocab_size=256), SEED, g2.F32, g2.PATH_REFERENCE)
     assert not m.uses_step()
+    assert m.step_kernel() == ""
     with pytest.raises(g2.G2Error):
         m.set_step(True)
     m.free()
+
+
+def test_step_kernel_names(g2):
+    """The kernel a decode forward launches, as the library reports it
+    (the name bench.py labels its roofline with and picks its traffic
+    profile by): the tail form when every matrix row splits into segments
+    of 193..208 16-byte chunks (GPT-2 XL: rows of n_embd 1600 or ffn 6400
+    inputs split into segments of 200 chunks, in fp16 and in fp32), the
+    plain form otherwise, none with the per-operator kernels."""
+    cases = [("xl", g2.F16, "g2k_step_f16_tail"), ("xl", g2.F32, "g2k_step_f32_tail"),
+             ("large", g2.F16, "g2k_step_f16"), ("large", g2.F32, "g2k_step_f32"),
+             ("small", g2.F32, "g2k_step_f32"), ("medium", g2.F32, "g2k_step_f32")]
+    for preset, dtype, name in cases:
+        m = g2.Model.synth(g2.preset(preset), SEED, dtype, g2.PATH_FUSED)
+        assert m.uses_step()
+        assert m.step_kernel() == name, (preset, dtype, m.step_kernel())
+        m.set_step(False)
+        assert m.step_kernel() == ""
+        m.free()
 
 
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
