@@ -99,6 +99,7 @@ int g2i_launch3(int fid, unsigned gx, unsigned gy, unsigned gz, unsigned bx, voi
 #define G2_SG_GELU 1
 #define G2_SG_RESID 2
 #define G2_SG_QKV 3
+#define G2_SG_GELU_SPLIT 5 /* gelu, written as fp16 halves to Ch, Cl */
 /* Cooperative launch (all gx work-groups co-resident) of a 1-D grid. */
 int g2i_coop_launch(int fid, unsigned gx, unsigned bx, void *args);
 /* Work-groups of the persistent step kernel's grid (0: not supported). */

@@ -85,10 +85,12 @@ typedef struct {
 #define G2_SKLN_MAXKS 5     /* slices g2k_splitk_resid_ln reads (ks <= this) */
 #define G2_SKLN_F32_MAXKS 8 /* slices g2k_splitk_resid_ln_f32 reads */
 
-/* The split-K epilogue of the fp32-weight prefill GEMM (g2k_splitk_epi):
- * v[m,n] = (sum over z < ks in order of part[z][m][n]) + bias[n], then epi
- * 1 gelu (C = gelu(v)), 2 resid (C = C + v), 3 qkv (q_out / k_cache /
- * v_cache as g2_gemm_args' qkv epilogue).  N % 4 == 0. */
+/* The split-K epilogue of the prefill GEMMs (g2k_splitk_epi): v[m,n] =
+ * (sum over z < ks in order of part[z][m][n]) + bias[n], then epi 1 gelu
+ * (C = gelu(v)), 2 resid (C = C + v), 3 qkv (q_out / k_cache / v_cache and
+ * the K/V halves as g2_gemm_args' qkv epilogue), 5 gelu as fp16 halves
+ * (Ch, Cl = the halves of gelu(v), the operand of the next 128x128 GEMM).
+ * N % 4 == 0. */
 typedef struct {
     const float *part;
     const float *bias;
@@ -97,6 +99,7 @@ typedef struct {
     int M, N, ks, epi;
     int E, S, pos0;
     uint16_t *kh, *kl, *vth, *vtl; /* as in g2_gemm_args */
+    uint16_t *Ch, *Cl;
 } g2_skepi_args;
 
 /* Reference-layout matvec, first pass: partial[split*N + n] = sum over the

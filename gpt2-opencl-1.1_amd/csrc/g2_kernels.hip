@@ -783,9 +783,10 @@ G2_SGEMM(g2k_sgemm_resid, GEPI_RESID)
 G2_SGEMM(g2k_sgemm_qkv, GEPI_QKV)
 G2_SGEMM(g2k_sgemm_partial, GEPI_PARTIAL)
 
-/* The split-K epilogue of g2k_sgemm_partial: v = (part[0][m][n] + ... +
- * part[ks-1][m][n]) + bias[n], then by epi: gelu (C = gelu(v)), resid
- * (C = C + v, in place), qkv (the K/V cache scatter of GEPI_QKV).  Four
+/* The split-K epilogue of g2k_sgemm_partial and g2k_hgemm2_partial: v =
+ * (part[0][m][n] + ... + part[ks-1][m][n]) + bias[n], then by epi: gelu
+ * (C = gelu(v)), resid (C = C + v, in place), qkv (the K/V cache scatter
+ * of GEPI_QKV), gelu as fp16 halves (GEPI_GELU_SPLIT: Ch, Cl).  Four
  * consecutive columns per thread (16-byte loads; N % 4 == 0). */
 G2K void g2k_splitk_epi(const g2_skepi_args a)
 {
@@ -803,6 +804,17 @@ G2K void g2k_splitk_epi(const g2_skepi_args a)
         } else if (a.epi == GEPI_RESID) {
             const f32x4 c = *(const f32x4 *)(a.C + o);
             *(f32x4 *)(a.C + o) = c + v;
+        } else if (a.epi == GEPI_GELU_SPLIT) {
+            float y[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = gelu_f(v[e]);
+            uint2 hv, lv;
+            hv.x = pk16(hi16(y[0]), hi16(y[1]));
+            hv.y = pk16(hi16(y[2]), hi16(y[3]));
+            lv.x = pk16(lo16(y[0]), lo16(y[1]));
+            lv.y = pk16(lo16(y[2]), lo16(y[3]));
+            *(uint2 *)(a.Ch + o) = hv;
+            *(uint2 *)(a.Cl + o) = lv;
         } else {
             const qkv_dst d = qkv_of(a);
 #pragma unroll

@@ -970,7 +970,32 @@ static int prefill_sgemm(g2_model *m, int epi, g2_gemm_args *g, const float *ln_
         return g2i_launch(G2F_SPLITK_RESID_LN_F32, (unsigned)g->M, 1, 256, &r);
     }
     g2_skepi_args e = { m->pf_part, g->bias, g->C, g->q_out, g->k_cache, g->v_cache, g->M, g->N, ks, epi,
-                        g->E, g->S, g->pos0, g->kh, g->kl, g->vth, g->vtl };
+                        g->E, g->S, g->pos0, g->kh, g->kl, g->vth, g->vtl, NULL, NULL };
+    const unsigned n4 = cdivu((unsigned)(g->M * g->N / 4), 256);
+    if (!rc) rc = g2i_launch(G2F_SPLITK_EPI, n4 < 2048 ? n4 : 2048, 1, 256, &e);
+    return rc;
+}
+
+/* The 128x128 fp16 GEMM (g2k_hgemm2_*, kernel fid) with its qkv or
+ * GELU-split epilogue (epi G2_SG_QKV or G2_SG_GELU_SPLIT).  When its tiles
+ * fill at most half the CUs (a 256-row prompt at GPT-2 large width: qkv 60,
+ * fc 80 tiles), it runs as K slices (g2k_hgemm2_partial, as many as keep
+ * tiles x slices within the CUs, at most G2_PF_MAXSPLIT and as the slice
+ * buffer holds), summed in order with the bias and the epilogue by
+ * g2k_splitk_epi; GPT-2 XL's 512 rows (qkv 152, fc 200 tiles) run whole. */
+static int prefill_big_epi(g2_model *m, int fid, int epi, g2_gemm_args *g)
+{
+    const unsigned tiles = cdivu(g->N, 128) * cdivu(g->M, 128), cus = (unsigned)g2i_cus();
+    const unsigned bx = 8 * cdivu(cdivu(g->N, 128), 8) * cdivu(g->M, 128);
+    const size_t cap = (size_t)G2_PF_MAXSPLIT * G2_KV_MAX_SEQ * m->cfg.n_embd; /* pf_part floats */
+    int ks = 1;
+    for (int k = G2_PF_MAXSPLIT; k > 1; --k)
+        if (tiles * (unsigned)k <= cus && k <= g->K / 64 && (size_t)k * g->M * g->N <= cap) { ks = k; break; }
+    if (ks == 1) return g2i_launch(fid, bx, 1, 1024, g);
+    g->part = m->pf_part; g->ksplit = ks;
+    int rc = g2i_launch3(G2F_HGEMM2_PARTIAL, bx, 1, (unsigned)ks, 1024, g);
+    g2_skepi_args e = { m->pf_part, g->bias, g->C, g->q_out, g->k_cache, g->v_cache, g->M, g->N, ks, epi,
+                        g->E, g->S, g->pos0, g->kh, g->kl, g->vth, g->vtl, g->Ch, g->Cl };
     const unsigned n4 = cdivu((unsigned)(g->M * g->N / 4), 256);
     if (!rc) rc = g2i_launch(G2F_SPLITK_EPI, n4 < 2048 ? n4 : 2048, 1, 256, &e);
     return rc;
@@ -1023,7 +1048,7 @@ static int fused_prefill(g2_model *m, int P)
         g.k_cache = y->k_cache; g.v_cache = y->v_cache; g.M = P; g.N = 3 * E; g.K = E;
         g.E = E; g.S = G2_KV_MAX_SEQ; g.pos0 = 0;
         g.kh = kv_kh; g.kl = kv_kl; g.vth = kv_vh; g.vtl = kv_vl;
-        if (!rc) rc = big ? g2i_launch(f_qkv, 8 * cdivu(cdivu(3 * E, 128), 8) * cdivu(P, 128), 1, 1024, &g)
+        if (!rc) rc = big ? prefill_big_epi(m, f_qkv, G2_SG_QKV, &g)
                       : sg  ? prefill_sgemm(m, G2_SG_QKV, &g, NULL, NULL, &ln_unused)
                             : g2i_launch(f_qkv, cdivu(3 * E, 64), cdivu(P, 64), 256, &g);
         g2_attnp_args t = { m->q, y->k_cache, y->v_cache, m->attn, P, E, NH, G2_KV_MAX_SEQ, 1.0f / sqrtf(64.0f),
@@ -1045,7 +1070,7 @@ static int fused_prefill(g2_model *m, int P)
         memset(&g, 0, sizeof g);
         g.A = m->ln_out; g.B = y->fc_w; g.bias = y->fc_b; g.C = m->ffn1; g.M = P; g.N = F; g.K = E;
         g.Ah = ln_h; g.Al = ln_l; g.Ch = ff_h; g.Cl = ff_l;
-        if (!rc) rc = big ? g2i_launch(f_gelu, 8 * cdivu(cdivu(F, 128), 8) * cdivu(P, 128), 1, 1024, &g)
+        if (!rc) rc = big ? prefill_big_epi(m, f_gelu, G2_SG_GELU_SPLIT, &g)
                       : sg  ? prefill_sgemm(m, G2_SG_GELU, &g, NULL, NULL, &ln_unused)
                             : g2i_launch(f_gelu, cdivu(F, 64), cdivu(P, 64), 256, &g);
         memset(&g, 0, sizeof g);
