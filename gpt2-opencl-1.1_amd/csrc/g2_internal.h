@@ -91,8 +91,12 @@ int g2i_ready(void);
 hipStream_t g2i_stream(void);
 int g2i_launch(int fid, unsigned gx, unsigned gy, unsigned bx, void *args);
 int g2i_launch3(int fid, unsigned gx, unsigned gy, unsigned gz, unsigned bx, void *args);
-/* largest K split of the fp16 prefill GEMM (its slice buffer holds this many) */
+/* the fp16 prefill's K slices: its slice buffer (pf_part) holds
+ * G2_PF_MAXSPLIT x 1024 x n_embd floats; the 64x64 GEMM splits K in at most
+ * G2_PF_MAXSPLIT slices, the 128x128 one in at most G2_PF_BIGSPLIT (and as
+ * many as the buffer holds) */
 #define G2_PF_MAXSPLIT 5
+#define G2_PF_BIGSPLIT 8
 /* the fp32-weight prefill GEMM's split-K slices (floats; 8 MiB) and its
  * epilogue codes (g2k_sgemm_*, g2k_splitk_epi) */
 #define G2_SG_PART_FLOATS ((size_t)512 * 4096)

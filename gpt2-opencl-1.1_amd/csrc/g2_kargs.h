@@ -82,7 +82,7 @@ typedef struct {
     float *ln_out;
 } g2_skred_args;
 #define G2_SKLN_MAXN 2048
-#define G2_SKLN_MAXKS 5     /* slices g2k_splitk_resid_ln reads (ks <= this) */
+#define G2_SKLN_MAXKS 8     /* slices g2k_splitk_resid_ln reads (ks <= this) */
 #define G2_SKLN_F32_MAXKS 8 /* slices g2k_splitk_resid_ln_f32 reads */
 
 /* The split-K epilogue of the prefill GEMMs (g2k_splitk_epi): v[m,n] =

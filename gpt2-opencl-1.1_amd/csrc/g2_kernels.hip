@@ -1211,10 +1211,10 @@ template <int ZMAX, bool F32OUT>
 __device__ __forceinline__ void splitk_resid_ln_impl(const g2_skred_args &a)
 {
     /* thread t owns the 4-column groups t and t + 256 of the row (N % 4 ==
-     * 0, N <= G2_SKLN_MAXN); every load of both groups -- all slices, the
-     * residual, bias and LayerNorm parameters -- is issued before the
-     * first sum (unconditional, clamped into the row), so the row costs
-     * one memory latency instead of one per group */
+     * 0, N <= G2_SKLN_MAXN); every load of both groups -- the ks slices,
+     * the residual, bias and LayerNorm parameters -- is issued before the
+     * first sum (clamped into the row), so the row costs one memory latency
+     * instead of one per group */
     constexpr int PG = G2_SKLN_MAXN / 1024; /* groups per thread */
     __shared__ float red4[4];
     const int m = blockIdx.x, N = a.N, NG = N >> 2;
@@ -1226,7 +1226,8 @@ __device__ __forceinline__ void splitk_resid_ln_impl(const g2_skred_args &a)
         const int g = min((int)threadIdx.x + 256 * k, NG - 1);
 #pragma unroll
         for (int z = 0; z < ZMAX; ++z)
-            pz[k][z] = *(const f32x4 *)(a.part + (size_t)min(z, a.ks - 1) * MN + row + 4 * g);
+            pz[k][z] = z < a.ks ? *(const f32x4 *)(a.part + (size_t)z * MN + row + 4 * g)
+                                : (f32x4){0.f, 0.f, 0.f, 0.f};
         cv[k] = *(const f32x4 *)(a.C + row + 4 * g);
         bv[k] = a.bias ? *(const f32x4 *)(a.bias + 4 * g) : (f32x4){0.f, 0.f, 0.f, 0.f};
         gv[k] = *(const f32x4 *)(a.ln_g + 4 * g);

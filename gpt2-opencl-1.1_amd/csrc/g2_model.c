@@ -896,8 +896,9 @@ static int set_state(g2_model *m, int pos, int tok, int min_new, int ngen)
  * as split-K slices when a single pass would leave the GPU under-filled.
  * big: the 128x128 kernel, which takes A as its fp16 halves Ah, Al and
  * whose work-groups (one per CU) should all run at once: its slice count
- * is the largest that keeps tiles x slices within the CU count; it splits
- * the K steps into slices that differ by at most one step. */
+ * is the largest that keeps tiles x slices within the CU count, at most
+ * G2_PF_BIGSPLIT and as the slice buffer holds; it splits the K steps into
+ * slices that differ by at most one step. */
 static int prefill_resid(g2_model *m, const float *A, const uint16_t *Ah, const uint16_t *Al, const void *W,
                          const float *bias, float *C, int P, int N, int K, int big, const float *ln_g,
                          const float *ln_b, uint16_t *hi, uint16_t *lo, int *ln_done)
@@ -913,9 +914,10 @@ static int prefill_resid(g2_model *m, const float *A, const uint16_t *Ah, const 
     if (gx * gy >= 512) ks = 1;
     if (big) {
         const unsigned tiles = cdivu(N, 128) * cdivu(P, 128), cus = (unsigned)g2i_cus();
+        const size_t cap = (size_t)G2_PF_MAXSPLIT * G2_KV_MAX_SEQ * m->cfg.n_embd; /* pf_part floats */
         ks = 1;
-        for (int k = G2_PF_MAXSPLIT; k > 1; --k)
-            if (tiles * (unsigned)k <= cus && k <= K / 64) { ks = k; break; }
+        for (int k = G2_PF_BIGSPLIT; k > 1; --k)
+            if (tiles * (unsigned)k <= cus && k <= K / 64 && (size_t)k * P * N <= cap) { ks = k; break; }
     }
     /* the 128x128 kernel: a 1-D grid of 8 * ceil(column blocks / 8) * row blocks */
     const unsigned bx = big ? 8 * cdivu(cdivu(N, 128), 8) * cdivu(P, 128) : gx, by = big ? 1 : gy;
@@ -980,7 +982,7 @@ static int prefill_sgemm(g2_model *m, int epi, g2_gemm_args *g, const float *ln_
  * GELU-split epilogue (epi G2_SG_QKV or G2_SG_GELU_SPLIT).  When its tiles
  * fill at most half the CUs (a 256-row prompt at GPT-2 large width: qkv 60,
  * fc 80 tiles), it runs as K slices (g2k_hgemm2_partial, as many as keep
- * tiles x slices within the CUs, at most G2_PF_MAXSPLIT and as the slice
+ * tiles x slices within the CUs, at most G2_PF_BIGSPLIT and as the slice
  * buffer holds), summed in order with the bias and the epilogue by
  * g2k_splitk_epi; GPT-2 XL's 512 rows (qkv 152, fc 200 tiles) run whole. */
 static int prefill_big_epi(g2_model *m, int fid, int epi, g2_gemm_args *g)
@@ -989,7 +991,7 @@ static int prefill_big_epi(g2_model *m, int fid, int epi, g2_gemm_args *g)
     const unsigned bx = 8 * cdivu(cdivu(g->N, 128), 8) * cdivu(g->M, 128);
     const size_t cap = (size_t)G2_PF_MAXSPLIT * G2_KV_MAX_SEQ * m->cfg.n_embd; /* pf_part floats */
     int ks = 1;
-    for (int k = G2_PF_MAXSPLIT; k > 1; --k)
+    for (int k = G2_PF_BIGSPLIT; k > 1; --k)
         if (tiles * (unsigned)k <= cus && k <= g->K / 64 && (size_t)k * g->M * g->N <= cap) { ks = k; break; }
     if (ks == 1) return g2i_launch(fid, bx, 1, 1024, g);
     g->part = m->pf_part; g->ksplit = ks;
