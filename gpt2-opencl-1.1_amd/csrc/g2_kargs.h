@@ -90,7 +90,7 @@ typedef struct {
  * (C = gelu(v)), 2 resid (C = C + v), 3 qkv (q_out / k_cache / v_cache and
  * the K/V halves as g2_gemm_args' qkv epilogue), 5 gelu as fp16 halves
  * (Ch, Cl = the halves of gelu(v), the operand of the next 128x128 GEMM).
- * N % 4 == 0. */
+ * N % 4 == 0, ks <= G2_SKEPI_MAXKS. */
 typedef struct {
     const float *part;
     const float *bias;
@@ -101,6 +101,7 @@ typedef struct {
     uint16_t *kh, *kl, *vth, *vtl; /* as in g2_gemm_args */
     uint16_t *Ch, *Cl;
 } g2_skepi_args;
+#define G2_SKEPI_MAXKS 8 /* slices g2k_splitk_epi reads */
 
 /* Reference-layout matvec, first pass: partial[split*N + n] = sum over the
  * split's contiguous k-range of A[k] B[k*N + n]; grid (column tiles, splits). */

@@ -245,19 +245,6 @@ struct qkv_dst {
     uint16_t *kh, *kl, *vth, *vtl;
     int E, S, pos0;
 };
-__device__ __forceinline__ void qkv_store(const qkv_dst &d, int m, int n, float v)
-{
-    const int E = d.E, pos = d.pos0 + m;
-    if (n < E) {
-        d.q_out[(size_t)m * E + n] = v;
-    } else if (n < 2 * E) {
-        d.k_cache[(size_t)(n - E) * d.S + pos] = v;
-        if (d.kh) split_store(d.kh, d.kl, (size_t)pos * E + (n - E), v);
-    } else {
-        d.v_cache[(size_t)pos * E + (n - 2 * E)] = v;
-        if (d.kh) split_store(d.vth, d.vtl, (size_t)(n - 2 * E) * d.S + pos, v);
-    }
-}
 template <typename ARGS>
 __device__ __forceinline__ qkv_dst qkv_of(const ARGS &a)
 {
@@ -787,22 +774,77 @@ G2_SGEMM(g2k_sgemm_partial, GEPI_PARTIAL)
  * (part[0][m][n] + ... + part[ks-1][m][n]) + bias[n], then by epi: gelu
  * (C = gelu(v)), resid (C = C + v, in place), qkv (the K/V cache scatter
  * of GEPI_QKV), gelu as fp16 halves (GEPI_GELU_SPLIT: Ch, Cl).  Four
- * consecutive columns per thread (16-byte loads; N % 4 == 0). */
+ * consecutive columns per thread (16-byte loads; N % 4 == 0), except qkv:
+ * four consecutive rows of one column per thread, so that the transposed
+ * K cache and V halves (position-minor) take a lane's four positions with
+ * one store, as the GEMM's own qkv epilogue does, and q, V and the K
+ * halves (column-minor) are stored by consecutive lanes.  The ks slice
+ * loads (ks <= G2_SKEPI_MAXKS) are all issued before the first add, so a
+ * sum costs one memory latency rather than one per slice. */
+/* Four consecutive slice sums at offset o: (part[0][o..o+3] + ... +
+ * part[ks-1][o..o+3]) in order; the ks loads (ks <= G2_SKEPI_MAXKS) are all
+ * issued before the first add, so the sum costs one memory latency rather
+ * than one per slice. */
+__device__ __forceinline__ void slice_loads4(const float *part, size_t MN, size_t o, int ks,
+                                             f32x4 (&p)[G2_SKEPI_MAXKS])
+{
+#pragma unroll
+    for (int z = 0; z < G2_SKEPI_MAXKS; ++z)
+        p[z] = z < ks ? *(const f32x4 *)(part + (size_t)z * MN + o) : (f32x4){0.f, 0.f, 0.f, 0.f};
+}
+__device__ __forceinline__ f32x4 slice_sum4(const f32x4 (&p)[G2_SKEPI_MAXKS], int ks)
+{
+    f32x4 v = p[0];
+#pragma unroll
+    for (int z = 1; z < G2_SKEPI_MAXKS; ++z)
+        if (z < ks) v += p[z];
+    return v;
+}
+
 G2K void g2k_splitk_epi(const g2_skepi_args a)
 {
+    const size_t MN = (size_t)a.M * a.N;
     const int N4 = a.N >> 2;
-    const size_t MN = (size_t)a.M * a.N, n4s = (size_t)a.M * N4;
+    if (a.epi == GEPI_QKV) {
+        const qkv_dst d = qkv_of(a);
+        const size_t n4s = (size_t)((a.M + 3) >> 2) * a.N;
+        for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4s; i += (size_t)gridDim.x * 256) {
+            const int n = (int)(i % a.N), mb = 4 * (int)(i / a.N);
+            float p[4][G2_SKEPI_MAXKS];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const size_t o = (size_t)min(mb + q, a.M - 1) * a.N + n;
+#pragma unroll
+                for (int z = 0; z < G2_SKEPI_MAXKS; ++z) p[q][z] = z < a.ks ? a.part[(size_t)z * MN + o] : 0.f;
+            }
+            const float b = a.bias ? a.bias[n] : 0.f;
+            f32x4 v;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float x = p[q][0];
+#pragma unroll
+                for (int z = 1; z < G2_SKEPI_MAXKS; ++z)
+                    if (z < a.ks) x += p[q][z];
+                v[q] = a.bias ? x + b : x;
+            }
+            qkv_store4(d, mb, a.M, n, v);
+        }
+        return;
+    }
+    const size_t n4s = (size_t)a.M * N4;
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4s; i += (size_t)gridDim.x * 256) {
         const int m = (int)(i / N4), n = (int)(i % N4) * 4;
         const size_t o = (size_t)m * a.N + n;
-        f32x4 v = *(const f32x4 *)(a.part + o);
-        for (int z = 1; z < a.ks; ++z) v += *(const f32x4 *)(a.part + (size_t)z * MN + o);
-        if (a.bias) v += *(const f32x4 *)(a.bias + n);
+        f32x4 p[G2_SKEPI_MAXKS];
+        slice_loads4(a.part, MN, o, a.ks, p);
+        const f32x4 b = a.bias ? *(const f32x4 *)(a.bias + n) : (f32x4){0.f, 0.f, 0.f, 0.f};
+        const f32x4 c = a.epi == GEPI_RESID ? *(const f32x4 *)(a.C + o) : (f32x4){0.f, 0.f, 0.f, 0.f};
+        f32x4 v = slice_sum4(p, a.ks);
+        if (a.bias) v += b;
         if (a.epi == GEPI_GELU) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) a.C[o + e] = gelu_f(v[e]);
         } else if (a.epi == GEPI_RESID) {
-            const f32x4 c = *(const f32x4 *)(a.C + o);
             *(f32x4 *)(a.C + o) = c + v;
         } else if (a.epi == GEPI_GELU_SPLIT) {
             float y[4];
@@ -815,10 +857,6 @@ G2K void g2k_splitk_epi(const g2_skepi_args a)
             lv.y = pk16(lo16(y[2]), lo16(y[3]));
             *(uint2 *)(a.Ch + o) = hv;
             *(uint2 *)(a.Cl + o) = lv;
-        } else {
-            const qkv_dst d = qkv_of(a);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) qkv_store(d, m, n + e, v[e]);
         }
     }
 }
@@ -967,8 +1005,14 @@ G2K void g2k_splitk_resid(const g2_skred_args a)
 {
     const size_t MN = (size_t)a.M * a.N;
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < MN; i += (size_t)gridDim.x * 256) {
-        float v = a.part[i];
-        for (int z = 1; z < a.ks; ++z) v += a.part[(size_t)z * MN + i];
+        /* every slice load issued before the first add (ks <= G2_SKEPI_MAXKS) */
+        float p[G2_SKEPI_MAXKS];
+#pragma unroll
+        for (int z = 0; z < G2_SKEPI_MAXKS; ++z) p[z] = z < a.ks ? a.part[(size_t)z * MN + i] : 0.f;
+        float v = p[0];
+#pragma unroll
+        for (int z = 1; z < G2_SKEPI_MAXKS; ++z)
+            if (z < a.ks) v += p[z];
         const int n = (int)(i % (size_t)a.N);
         if (a.bias) v += a.bias[n];
         a.C[i] = v + a.C[i];

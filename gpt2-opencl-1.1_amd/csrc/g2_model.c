@@ -892,6 +892,15 @@ static int set_state(g2_model *m, int pos, int tok, int min_new, int ngen)
     return up(m->state, h, sizeof h);
 }
 
+/* g2k_splitk_epi over e's M x N outputs: one thread per 4 columns of a
+ * row, or per 4 rows of a column (qkv) */
+static int launch_splitk_epi(g2_skepi_args *e)
+{
+    if (e->ks > G2_SKEPI_MAXKS) return g2i_err(G2_E_LIMIT, "%d split-K slices (at most %d)", e->ks, G2_SKEPI_MAXKS);
+    const unsigned n = cdivu((unsigned)(e->M * e->N / 4), 256);
+    return g2i_launch(G2F_SPLITK_EPI, n < 2048 ? n : 2048, 1, 256, e);
+}
+
 /* C += A . W^T + bias (the residual matmuls of the fp16 prefill: proj, fc2)
  * as split-K slices when a single pass would leave the GPU under-filled.
  * big: the 128x128 kernel, which takes A as its fp16 halves Ah, Al and
@@ -933,6 +942,7 @@ static int prefill_resid(g2_model *m, const float *A, const uint16_t *Ah, const 
         *ln_done = 1;
         return g2i_launch(G2F_SPLITK_RESID_LN, (unsigned)P, 1, 256, &r);
     }
+    if (!rc && ks > G2_SKEPI_MAXKS) rc = g2i_err(G2_E_LIMIT, "%d split-K slices (at most %d)", ks, G2_SKEPI_MAXKS);
     if (!rc) rc = g2i_launch(G2F_SPLITK_RESID, cdivu((unsigned)(P * N), 256) < 2048 ? cdivu((unsigned)(P * N), 256) : 2048,
                              1, 256, &r);
     return rc;
@@ -973,8 +983,7 @@ static int prefill_sgemm(g2_model *m, int epi, g2_gemm_args *g, const float *ln_
     }
     g2_skepi_args e = { m->pf_part, g->bias, g->C, g->q_out, g->k_cache, g->v_cache, g->M, g->N, ks, epi,
                         g->E, g->S, g->pos0, g->kh, g->kl, g->vth, g->vtl, NULL, NULL };
-    const unsigned n4 = cdivu((unsigned)(g->M * g->N / 4), 256);
-    if (!rc) rc = g2i_launch(G2F_SPLITK_EPI, n4 < 2048 ? n4 : 2048, 1, 256, &e);
+    if (!rc) rc = launch_splitk_epi(&e);
     return rc;
 }
 
@@ -998,8 +1007,7 @@ static int prefill_big_epi(g2_model *m, int fid, int epi, g2_gemm_args *g)
     int rc = g2i_launch3(G2F_HGEMM2_PARTIAL, bx, 1, (unsigned)ks, 1024, g);
     g2_skepi_args e = { m->pf_part, g->bias, g->C, g->q_out, g->k_cache, g->v_cache, g->M, g->N, ks, epi,
                         g->E, g->S, g->pos0, g->kh, g->kl, g->vth, g->vtl, g->Ch, g->Cl };
-    const unsigned n4 = cdivu((unsigned)(g->M * g->N / 4), 256);
-    if (!rc) rc = g2i_launch(G2F_SPLITK_EPI, n4 < 2048 ? n4 : 2048, 1, 256, &e);
+    if (!rc) rc = launch_splitk_epi(&e);
     return rc;
 }
 
