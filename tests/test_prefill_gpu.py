@@ -1,10 +1,14 @@
 """GPU parity of the fused prefill with fp16 weights, whose matmuls run on
 the fp16 matrix cores with the fp32 activations split into two fp16 halves
-(g2k_hgemm_*): last-position logits against the CPU oracle (5e-2, as for
-every fp16-weight path) and against the fp32-MFMA GEMM of the same library
-(G2_PREFILL_F32MFMA=1), which the split must match to fp32-level
-accumulation differences, at GPT-2 XL width and for ragged prompt lengths
-(not multiples of the 64-row tile) up to the 1023-position limit.
+(g2k_hgemm_*): last-position logits against the CPU oracle (1e-4: the
+oracle runs in fp32 on the same fp16-rounded weights) and against the
+fp32-MFMA GEMM of the same library (G2_PREFILL_F32MFMA=1), which the split
+must match to fp32-level accumulation differences, at GPT-2 XL width and
+for ragged prompt lengths (not multiples of the 64-row tile) up to the
+1023-position limit.  The lengths cover the 64x64 GEMM (P <= 64), the
+128x128 GEMM with qkv and fc as K slices (100: 6 and 5 slices; 200, 256:
+3 and 2) and run whole (1023 rows), with proj and fc2 as 2 to 8 slices
+summed with the following LayerNorm.
 """
 import numpy as np
 import pytest
@@ -17,7 +21,7 @@ pytestmark = pytest.mark.gpu
 SEED = 0x67707432
 
 
-@pytest.mark.parametrize("P", [1, 37, 64, 200, 1023])
+@pytest.mark.parametrize("P", [1, 37, 64, 100, 200, 256, 1023])
 def test_prefill_split_fp16_mfma(g2, monkeypatch, P):
     cfg = g2.make_config(2, 1600, 25, vocab_size=50257)
     w = g2.synth_weights(cfg, SEED, f16_round=True)
@@ -37,7 +41,7 @@ def test_prefill_split_fp16_mfma(g2, monkeypatch, P):
     om.prefill(prompt)
     ref = om.logits()
     om.close()
-    np.testing.assert_allclose(lg_h, ref, rtol=5e-2, atol=5e-2)
+    np.testing.assert_allclose(lg_h, ref, rtol=0, atol=1e-4)
     np.testing.assert_allclose(lg_h, lg_f, rtol=1e-3, atol=2e-3)
     top2 = np.sort(ref)[-2:]
     assert int(np.argmax(lg_h)) == int(np.argmax(ref)) or top2[1] - top2[0] < TIE_TOL, \
