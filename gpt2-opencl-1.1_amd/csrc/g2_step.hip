@@ -1008,7 +1008,6 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     const int E = a.E, F = a.F, NH = a.NH, S = a.S, V = a.V;
     const int pos = clampi(a.state[G2S_POS], 0, S - 1);
     const int tok = clampi(a.state[G2S_TOK], 0, V - 1);
-    const int ngen = a.state[G2S_NGEN], min_new = a.state[G2S_MIN_NEW];
     const unsigned seq = (unsigned)a.state[G2S_SEQ];
     /* a plain launch earlier in this run found the grid not resident: skip
      * until the host has resumed the run */
