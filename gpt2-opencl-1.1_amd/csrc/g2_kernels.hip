@@ -22,6 +22,7 @@
 #include <hip/hip_runtime.h>
 #include "g2_kargs.h"
 #include "g2_step_plan.h"
+#include "g2_gemm_plan.h"
 
 #define G2K extern "C" __global__ __launch_bounds__(256)
 
@@ -1047,9 +1048,9 @@ G2K void g2k_splitk_resid(const g2_skred_args a)
  * columns >= N are computed from clamped reads and not stored.
  * ==================================================================== */
 namespace hg2 {
-constexpr int BM = 128, BN = 128, BK = 64, NS = 3;
-constexpr int TB = BM * BK * 2;  /* bytes of one 128 x 64 fp16 tile */
-constexpr int STAGE = 3 * TB;    /* a_hi, a_lo, weights: 48 KB */
+constexpr int BM = G2H_BM, BN = G2H_BN, BK = G2H_BK, NS = G2H_NS;
+constexpr int TB = G2H_TB;       /* bytes of one 128 x 64 fp16 tile */
+constexpr int STAGE = G2H_STAGE; /* a_hi, a_lo, weights: 48 KB */
 typedef __attribute__((address_space(3))) void lds_t;
 
 /* Wait until this wave's loads of the current step have landed (those of
@@ -1063,16 +1064,15 @@ struct frags {
 };
 __device__ __forceinline__ void read_half(frags &f, const unsigned char *st, int kk, int wm, int wn, int lane)
 {
-    const int fr = lane & 15, g = lane >> 4;
-    const int slot = (((kk + 8 * g) >> 3) ^ (fr >> 1)) << 4;
+    const int slot = g2h_frag_slot(kk, lane);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const unsigned char *row = st + (wm * 32 + i * 16 + fr) * 128 + slot;
+        const unsigned char *row = st + g2h_frag_row(wm, i, lane) * 128 + slot;
         f.ah[i] = *(const h16x8 *)row;
         f.al[i] = *(const h16x8 *)(row + TB);
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) f.b[j] = *(const h16x8 *)(st + 2 * TB + (wn * 32 + j * 16 + fr) * 128 + slot);
+    for (int j = 0; j < 2; ++j) f.b[j] = *(const h16x8 *)(st + 2 * TB + g2h_frag_row(wn, j, lane) * 128 + slot);
 }
 __device__ __forceinline__ void mma_half(f32x4 (&acc)[2][2], const frags &f)
 {
@@ -1098,22 +1098,16 @@ __device__ void hgemm2_impl(const g2_gemm_args &a)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 2, wn = wave & 3; /* 4 x 4 waves of 32 x 32 */
     const int M = a.M, N = a.N, Kfull = a.K;
-    /* Tile of this work-group.  The grid is 1-D per K slice: work-group w
-     * runs on XCD w % 8 (consecutive work-groups go to consecutive XCDs),
-     * so w -> (column block 8 (s / nmb) + w % 8, row block s % nmb), s =
-     * w / 8, puts all row blocks of a column block on one XCD, whose L2
-     * then fetches that weight block once.  Column blocks past the last
-     * (the grid is padded to a multiple of 8) have no work. */
-    const int nmb = (M + BM - 1) / BM, nnb = (N + BN - 1) / BN;
-    const int sw = (int)blockIdx.x >> 3;
-    const int nb = 8 * (sw / nmb) + ((int)blockIdx.x & 7), mb = sw % nmb;
-    if (nb >= nnb) return;
-    const int m0 = mb * BM, n0 = nb * BN;
+    /* tile of this work-group (the XCD mapping of g2h_tile_of; the grid's
+     * padding work-groups have no work) */
+    const g2h_tile tl = g2h_tile_of((int)blockIdx.x, M, N);
+    if (!tl.on) return;
+    const int m0 = tl.m0, n0 = tl.n0;
     /* split-K (GEPI_PARTIAL): this work-group's K slice, steps [s0, s1) of
-     * the Kfull / 64 (slices differ by at most one step) */
+     * the Kfull / 64 */
     const int nkt = Kfull / BK;
-    const int s0 = EPI == GEPI_PARTIAL ? (int)(((long)nkt * blockIdx.z) / a.ksplit) : 0;
-    const int s1 = EPI == GEPI_PARTIAL ? (int)(((long)nkt * (blockIdx.z + 1)) / a.ksplit) : nkt;
+    const int s0 = EPI == GEPI_PARTIAL ? g2h_slice_start(nkt, (int)blockIdx.z, a.ksplit) : 0;
+    const int s1 = EPI == GEPI_PARTIAL ? g2h_slice_start(nkt, (int)blockIdx.z + 1, a.ksplit) : nkt;
     const int kz0 = s0 * BK, nk = s1 - s0;
     f32x4 acc[2][2];
 #pragma unroll
@@ -1124,15 +1118,15 @@ __device__ void hgemm2_impl(const g2_gemm_args &a)
     /* this lane's load sources: wave w fills rows 8w..8w+7 of each tile
      * with one instruction (lane -> row l/8, slot l%8); each slot holds the
      * chunk that the swizzle puts there */
-    const int row = 8 * wave + (lane >> 3);
-    const int ch = (lane & 7) ^ ((row >> 1) & 7);
+    const int row = g2h_load_row(wave, lane);
+    const int ch = g2h_load_chunk(row, lane);
     const size_t ao = (size_t)min(m0 + row, M - 1) * Kfull + kz0 + 8 * ch;
     const _Float16 *hsrc = (const _Float16 *)a.Ah + ao, *lsrc = (const _Float16 *)a.Al + ao;
     const _Float16 *bsrc = (const _Float16 *)a.B + (size_t)min(n0 + row, N - 1) * Kfull + kz0 + 8 * ch;
     /* step t's loads into stage buffer b (steps past the last reload it) */
     auto issue = [&](int t, int b) {
         const int k = min(t, nk - 1) * BK;
-        unsigned char *st = lds + b * STAGE + (8 * wave) * 128;
+        unsigned char *st = lds + g2h_load_lds(b, wave);
         __builtin_amdgcn_global_load_lds(hsrc + k, (lds_t *)st, 16, 0, 0);
         __builtin_amdgcn_global_load_lds(lsrc + k, (lds_t *)(st + TB), 16, 0, 0);
         __builtin_amdgcn_global_load_lds(bsrc + k, (lds_t *)(st + 2 * TB), 16, 0, 0);
@@ -1144,7 +1138,7 @@ __device__ void hgemm2_impl(const g2_gemm_args &a)
     float bj[2] = {0.f, 0.f};
     if (EPI != GEPI_PARTIAL && a.bias) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) bj[j] = a.bias[min(n0 + wn * 32 + j * 16 + (lane & 15), N - 1)];
+        for (int j = 0; j < 2; ++j) bj[j] = a.bias[min(g2h_out_col(n0, wn, j, lane), N - 1)];
     }
     issue(0, 0);
     issue(1, 1);
@@ -1181,8 +1175,8 @@ __device__ void hgemm2_impl(const g2_gemm_args &a)
             for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const int m = min(m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + q, M - 1);
-                    const int n = min(n0 + wn * 32 + j * 16 + (lane & 15), N - 1);
+                    const int m = min(g2h_out_row(m0, wm, i, lane, q), M - 1);
+                    const int n = min(g2h_out_col(n0, wn, j, lane), N - 1);
                     rv[i][j][q] = a.C[(size_t)m * N + n];
                 }
     }
@@ -1209,8 +1203,8 @@ __device__ void hgemm2_impl(const g2_gemm_args &a)
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const int n = n0 + wn * 32 + j * 16 + (lane & 15);
-                if (n < N) qkv_store4(d, m0 + wm * 32 + i * 16 + 4 * (lane >> 4), M, n, acc[i][j]);
+                const int n = g2h_out_col(n0, wn, j, lane);
+                if (n < N) qkv_store4(d, g2h_out_row(m0, wm, i, lane, 0), M, n, acc[i][j]);
             }
         return;
     }
@@ -1220,8 +1214,8 @@ __device__ void hgemm2_impl(const g2_gemm_args &a)
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int m = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + q;
-                const int n = n0 + wn * 32 + j * 16 + (lane & 15);
+                const int m = g2h_out_row(m0, wm, i, lane, q);
+                const int n = g2h_out_col(n0, wn, j, lane);
                 if (m >= M || n >= N) continue;
                 const float v = acc[i][j][q];
                 if (EPI == GEPI_PARTIAL) {

@@ -27,6 +27,7 @@
 #include "g2_internal.h"
 #include "g2_host.h"
 #include "g2_step_plan.h"
+#include "g2_gemm_plan.h"
 
 typedef struct {
     float *ln1_w, *ln1_b, *qkv_b, *proj_b, *ln2_w, *ln2_b, *fc_b, *fc2_b;
@@ -921,15 +922,10 @@ static int prefill_resid(g2_model *m, const float *A, const uint16_t *Ah, const 
     for (int k = G2_PF_MAXSPLIT; k > 1; --k)
         if ((K / 64) % k == 0 && gx * gy * (unsigned)k <= 1024) { ks = k; break; }
     if (gx * gy >= 512) ks = 1;
-    if (big) {
-        const unsigned tiles = cdivu(N, 128) * cdivu(P, 128), cus = (unsigned)g2i_cus();
-        const size_t cap = (size_t)G2_PF_MAXSPLIT * G2_KV_MAX_SEQ * m->cfg.n_embd; /* pf_part floats */
-        ks = 1;
-        for (int k = G2_PF_BIGSPLIT; k > 1; --k)
-            if (tiles * (unsigned)k <= cus && k <= K / 64 && (size_t)k * P * N <= cap) { ks = k; break; }
-    }
-    /* the 128x128 kernel: a 1-D grid of 8 * ceil(column blocks / 8) * row blocks */
-    const unsigned bx = big ? 8 * cdivu(cdivu(N, 128), 8) * cdivu(P, 128) : gx, by = big ? 1 : gy;
+    if (big) /* slices within the pf_part floats */
+        ks = g2h_slices(P, N, K, g2i_cus(), G2_PF_BIGSPLIT, (long)G2_PF_MAXSPLIT * G2_KV_MAX_SEQ * m->cfg.n_embd);
+    /* the 128x128 kernel: a 1-D grid (g2h_grid) per slice */
+    const unsigned bx = big ? g2h_grid(P, N) : gx, by = big ? 1 : gy;
     g2_gemm_args g;
     memset(&g, 0, sizeof g);
     g.A = A; g.B = W; g.bias = bias; g.C = C; g.M = P; g.N = N; g.K = K;
@@ -996,12 +992,9 @@ static int prefill_sgemm(g2_model *m, int epi, g2_gemm_args *g, const float *ln_
  * g2k_splitk_epi; GPT-2 XL's 512 rows (qkv 152, fc 200 tiles) run whole. */
 static int prefill_big_epi(g2_model *m, int fid, int epi, g2_gemm_args *g)
 {
-    const unsigned tiles = cdivu(g->N, 128) * cdivu(g->M, 128), cus = (unsigned)g2i_cus();
-    const unsigned bx = 8 * cdivu(cdivu(g->N, 128), 8) * cdivu(g->M, 128);
-    const size_t cap = (size_t)G2_PF_MAXSPLIT * G2_KV_MAX_SEQ * m->cfg.n_embd; /* pf_part floats */
-    int ks = 1;
-    for (int k = G2_PF_BIGSPLIT; k > 1; --k)
-        if (tiles * (unsigned)k <= cus && k <= g->K / 64 && (size_t)k * g->M * g->N <= cap) { ks = k; break; }
+    const unsigned bx = g2h_grid(g->M, g->N);
+    const int ks = g2h_slices(g->M, g->N, g->K, g2i_cus(), G2_PF_BIGSPLIT,
+                              (long)G2_PF_MAXSPLIT * G2_KV_MAX_SEQ * m->cfg.n_embd); /* pf_part floats */
     if (ks == 1) return g2i_launch(fid, bx, 1, 1024, g);
     g->part = m->pf_part; g->ksplit = ks;
     int rc = g2i_launch3(G2F_HGEMM2_PARTIAL, bx, 1, (unsigned)ks, 1024, g);
