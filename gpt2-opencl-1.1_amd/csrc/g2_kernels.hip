@@ -23,6 +23,7 @@
 #include "g2_kargs.h"
 #include "g2_step_plan.h"
 #include "g2_gemm_plan.h"
+#include "g2_attn_plan.h"
 
 #define G2K extern "C" __global__ __launch_bounds__(256)
 
@@ -1376,9 +1377,7 @@ __device__ __forceinline__ float row16_sum(float v)
  * work. */
 __device__ __forceinline__ void attnp_block(const g2_attnp_args &a, int &h, int &qb)
 {
-    const int nqb = (a.P + 63) / 64, k = (int)blockIdx.x >> 3;
-    h = ((int)blockIdx.x & 7) + 8 * (k / nqb);
-    qb = k % nqb;
+    g2a_block((int)blockIdx.x, a.P, &h, &qb);
 }
 
 extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_mfma(const g2_attnp_args a)
@@ -1588,7 +1587,7 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_mfma(const g2
  * slot c ^ (r / 2 % 8), so the 16 rows of an operand read fall on distinct
  * banks.  Each half stages its key blocks in a two-stage ring (the next
  * block's loads in flight during the products of the current one). */
-__device__ __forceinline__ int kv_at(int row, int chunk) { return row * 64 + 8 * (chunk ^ ((row >> 1) & 7)); }
+__device__ __forceinline__ int kv_at(int row, int chunk) { return g2a_kv_at(row, chunk); }
 
 /* max / sum over the four 16-lane rows of a wave (lanes l, l^16, l^32,
  * l^48), the same value in every lane */
@@ -1657,7 +1656,7 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
     const float scale2 = a.scale * 1.4426950408889634f;
     const int E = a.E, P = a.P, S = a.S;
     /* this lane's query row */
-    const int i = qb * 64 + 16 * rg + lr;
+    const int i = g2a_query(qb, rg, lane);
     f16x8 qh[2], ql[2];
     {
         const float *qp = a.q + (size_t)min(i, P - 1) * E + h * 64 + 8 * lg;
@@ -1688,11 +1687,11 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
     typedef __attribute__((address_space(3))) void lds_t;
     auto stage = [&](int kb, int b) {
         const int j0 = kb * 64;
-        unsigned char *st = (unsigned char *)(kvs + 4 * (2 * hs + b) * TILE);
+        unsigned char *st = (unsigned char *)(kvs + g2a_array(hs, b, 0));
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-            const int rw = 16 * w4 + 8 * e + (lane >> 3);
-            const int c = (lane & 7) ^ ((rw >> 1) & 7);
+            const int rw = G2A_STAGE_ROW(w4, e, lane);
+            const int c = G2A_STAGE_CHUNK(rw, lane);
             const size_t ko = (size_t)(j0 + rw) * E + h * 64 + 8 * c;
             const size_t vo = (size_t)(h * 64 + rw) * S + j0 + 8 * c;
             unsigned char *dst = st + (16 * w4 + 8 * e) * 128;
@@ -1711,7 +1710,7 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
         asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
         if (kb + 2 <= qb) stage(kb + 2, b ^ 1); /* wave-uniform */
         if (kb > qb) continue;                   /* wave-uniform */
-        const _Float16 *Kh = kvs + 4 * (2 * hs + b) * TILE, *Kl = Kh + TILE;
+        const _Float16 *Kh = kvs + g2a_array(hs, b, 0), *Kl = Kh + TILE;
         const _Float16 *Vh = Kh + 2 * TILE, *Vl = Kh + 3 * TILE;
         /* S^T tiles: keys j0 + 16t + 4lg + r of row i */
         f32x4 sacc[4];
