@@ -237,6 +237,22 @@ __device__ __forceinline__ unsigned pk16(_Float16 a, _Float16 b)
     return (unsigned)__builtin_bit_cast(uint16_t, a) | ((unsigned)__builtin_bit_cast(uint16_t, b) << 16);
 }
 
+/* Two fp32 values as packed fp16 halves, low word first: h holds hi16(a),
+ * hi16(b) and l holds lo16(a), lo16(b), each half rounded to nearest even
+ * from the fp32 value, two per packed v_cvt_pk_f16_f32 (measured equal to
+ * the scalar conversion on 4M values down to fp16 subnormals). */
+__device__ __forceinline__ void split2(float a, float b, unsigned &h, unsigned &l)
+{
+#pragma clang fp contract(off)
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const f2 v = {a, b};
+    const h2 hv = __builtin_convertvector(v, h2);
+    const h2 lv = __builtin_convertvector(v - __builtin_convertvector(hv, f2), h2);
+    h = __builtin_bit_cast(unsigned, hv);
+    l = __builtin_bit_cast(unsigned, lv);
+}
+
 /* The qkv epilogue of output (m, n), v final: columns < E to q_out[m][n];
  * key columns E..2E-1 to the transposed K cache at position pos0 + m and,
  * when kh is set, as fp16 halves to kh/kl [position][E]; value columns
@@ -288,10 +304,8 @@ __device__ __forceinline__ void qkv_store4(const qkv_dst &d, int mb, int M, int 
             const size_t o = (size_t)(n - 2 * E) * d.S + pos;
             if (full) {
                 uint2 hv, lv;
-                hv.x = pk16(hi16(v[0]), hi16(v[1]));
-                hv.y = pk16(hi16(v[2]), hi16(v[3]));
-                lv.x = pk16(lo16(v[0]), lo16(v[1]));
-                lv.y = pk16(lo16(v[2]), lo16(v[3]));
+                split2(v[0], v[1], hv.x, lv.x);
+                split2(v[2], v[3], hv.y, lv.y);
                 *(uint2 *)(d.vth + o) = hv;
                 *(uint2 *)(d.vtl + o) = lv;
             } else {
@@ -853,10 +867,8 @@ G2K void g2k_splitk_epi(const g2_skepi_args a)
 #pragma unroll
             for (int e = 0; e < 4; ++e) y[e] = gelu_f(v[e]);
             uint2 hv, lv;
-            hv.x = pk16(hi16(y[0]), hi16(y[1]));
-            hv.y = pk16(hi16(y[2]), hi16(y[3]));
-            lv.x = pk16(lo16(y[0]), lo16(y[1]));
-            lv.y = pk16(lo16(y[2]), lo16(y[3]));
+            split2(y[0], y[1], hv.x, lv.x);
+            split2(y[2], y[3], hv.y, lv.y);
             *(uint2 *)(a.Ch + o) = hv;
             *(uint2 *)(a.Cl + o) = lv;
         }
@@ -1316,10 +1328,8 @@ __device__ __forceinline__ void splitk_resid_ln_impl(const g2_skred_args &a)
                 *(f32x4 *)(a.ln_out + row + 4 * g) = (f32x4){y[0], y[1], y[2], y[3]};
             } else {
                 uint2 hv, lv;
-                hv.x = pk16(hi16(y[0]), hi16(y[1]));
-                hv.y = pk16(hi16(y[2]), hi16(y[3]));
-                lv.x = pk16(lo16(y[0]), lo16(y[1]));
-                lv.y = pk16(lo16(y[2]), lo16(y[3]));
+                split2(y[0], y[1], hv.x, lv.x);
+                split2(y[2], y[3], hv.y, lv.y);
                 *(uint2 *)(a.hi + row + 4 * g) = hv;
                 *(uint2 *)(a.lo + row + 4 * g) = lv;
             }
@@ -1618,10 +1628,8 @@ __device__ __forceinline__ void pt_operand(const f32x4 &d0, const f32x4 &d1, f16
     unsigned h[2][2], l[2][2]; /* [tile][key pair] */
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-        h[0][q] = pk16(hi16(d0[2 * q]), hi16(d0[2 * q + 1]));
-        l[0][q] = pk16(lo16(d0[2 * q]), lo16(d0[2 * q + 1]));
-        h[1][q] = pk16(hi16(d1[2 * q]), hi16(d1[2 * q + 1]));
-        l[1][q] = pk16(lo16(d1[2 * q]), lo16(d1[2 * q + 1]));
+        split2(d0[2 * q], d0[2 * q + 1], h[0][q], l[0][q]);
+        split2(d1[2 * q], d1[2 * q + 1], h[1][q], l[1][q]);
     }
     u32x4 oh, ol;
 #pragma unroll
@@ -1648,7 +1656,8 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
     int h, qb;
     attnp_block(a, h, qb);
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6, lr = lane & 15, lg = lane >> 4;
+    const int lane = tid & 63, lr = lane & 15, lg = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); /* uniform: key half and row group in SGPRs */
     const int rg = wave & 3, hs = wave >> 2;
     if (h >= a.NH || qb * 64 >= a.P) return;
     /* scores in base-2 units (scaled by log2 e): the softmax's
@@ -1685,20 +1694,28 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
      * < S, dims < E). */
     const int w4 = wave & 3;
     typedef __attribute__((address_space(3))) void lds_t;
+    /* per-lane element offsets of the two staging instructions within a
+     * key block (the block's position part is added to the uniform bases) */
+    unsigned kof[2], vof[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const int rw = G2A_STAGE_ROW(w4, e, lane);
+        const int c = G2A_STAGE_CHUNK(rw, lane);
+        kof[e] = (unsigned)(rw * E + h * 64 + 8 * c);
+        vof[e] = (unsigned)((h * 64 + rw) * S + 8 * c);
+    }
     auto stage = [&](int kb, int b) {
         const int j0 = kb * 64;
         unsigned char *st = (unsigned char *)(kvs + g2a_array(hs, b, 0));
+        const uint16_t *khb = a.kh + (size_t)j0 * E, *klb = a.kl + (size_t)j0 * E;
+        const uint16_t *vhb = a.vth + j0, *vlb = a.vtl + j0;
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-            const int rw = G2A_STAGE_ROW(w4, e, lane);
-            const int c = G2A_STAGE_CHUNK(rw, lane);
-            const size_t ko = (size_t)(j0 + rw) * E + h * 64 + 8 * c;
-            const size_t vo = (size_t)(h * 64 + rw) * S + j0 + 8 * c;
             unsigned char *dst = st + (16 * w4 + 8 * e) * 128;
-            __builtin_amdgcn_global_load_lds(a.kh + ko, (lds_t *)dst, 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(a.kl + ko, (lds_t *)(dst + TB), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(a.vth + vo, (lds_t *)(dst + 2 * TB), 16, 0, 0);
-            __builtin_amdgcn_global_load_lds(a.vtl + vo, (lds_t *)(dst + 3 * TB), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(khb + kof[e], (lds_t *)dst, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(klb + kof[e], (lds_t *)(dst + TB), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vhb + vof[e], (lds_t *)(dst + 2 * TB), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vlb + vof[e], (lds_t *)(dst + 3 * TB), 16, 0, 0);
         }
     };
     const int nit = (qb + 2) >> 1;
@@ -1740,15 +1757,29 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
                     sacc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh[t][s2], qh[s2], sacc[t], 0, 0, 0);
         }
         float bm = -INFINITY;
+        /* wave-uniform: only the diagonal block has keys past a row (rows
+         * past the prompt, in the last block, are masked there only: their
+         * results are never stored) */
+        if (kb == qb) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t)
+            for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int j = j0 + 16 * t + 4 * lg + r;
-                const float v = (i < P && j <= i) ? sacc[t][r] * scale2 : -INFINITY;
-                sacc[t][r] = v;
-                bm = fmaxf(bm, v);
-            }
+                for (int r = 0; r < 4; ++r) {
+                    const int j = j0 + 16 * t + 4 * lg + r;
+                    const float v = (i < P && j <= i) ? sacc[t][r] * scale2 : -INFINITY;
+                    sacc[t][r] = v;
+                    bm = fmaxf(bm, v);
+                }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float v = sacc[t][r] * scale2;
+                    sacc[t][r] = v;
+                    bm = fmaxf(bm, v);
+                }
+        }
         bm = xrow_max(bm);
         const float mn = fmaxf(m, bm);
         const float ms = mn == -INFINITY ? 0.f : mn;
@@ -1822,10 +1853,8 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
         if (a.out_hi) {
             /* the four dims as one 8-byte store per half */
             uint2 hv, lv;
-            hv.x = pk16(hi16(y[0]), hi16(y[1]));
-            hv.y = pk16(hi16(y[2]), hi16(y[3]));
-            lv.x = pk16(lo16(y[0]), lo16(y[1]));
-            lv.y = pk16(lo16(y[2]), lo16(y[3]));
+            split2(y[0], y[1], hv.x, lv.x);
+            split2(y[2], y[3], hv.y, lv.y);
             *(uint2 *)(a.out_hi + idx) = hv;
             *(uint2 *)(a.out_lo + idx) = lv;
         } else {
