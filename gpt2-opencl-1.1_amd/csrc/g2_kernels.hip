@@ -231,12 +231,6 @@ __device__ __forceinline__ _Float16 lo16(float v)
     return (_Float16)(v - (float)(_Float16)v);
 }
 
-/* Two fp16 values packed low-first into one word. */
-__device__ __forceinline__ unsigned pk16(_Float16 a, _Float16 b)
-{
-    return (unsigned)__builtin_bit_cast(uint16_t, a) | ((unsigned)__builtin_bit_cast(uint16_t, b) << 16);
-}
-
 /* Two fp32 values as packed fp16 halves, low word first: h holds hi16(a),
  * hi16(b) and l holds lo16(a), lo16(b), each half rounded to nearest even
  * from the fp32 value, two per packed v_cvt_pk_f16_f32 (measured equal to
