@@ -33,6 +33,8 @@ enum {
 /* a plain (not cooperative) launch of the step kernel found its work-groups
  * not all resident and did nothing; later launches skip until it is cleared */
 #define G2_ERR_STEP_NOT_RESIDENT 8
+/* a step-kernel launch whose grid differs from its row-plan table did nothing */
+#define G2_ERR_STEP_ARGS 16
 
 /* GEMM: C[M,N] = A[M,K] * op(B) with an epilogue.
  * B layout G2_BKN: [K,N] row-major (the reference's device layout);
@@ -277,6 +279,12 @@ typedef struct {
      * withholding its arrival, 3 with it arriving 0.5 ms late (within the
      * limit), 4 with it arriving 2 ms late (after the others gave up) */
     int plain;
+    /* the row plans of every work-group, [nshares][5] g2p_rows (qkv, proj,
+     * fc, fc2, lm_head: g2p_shares in g2_step_plan.h), built by the host for
+     * a grid of nshares work-groups; a launch of another grid size does
+     * nothing but set G2_ERR_STEP_ARGS */
+    const void *shares;
+    int nshares;
 } g2_step_args;
 
 #define G2_TRACE_STRIDE(L) (24 * (L) + 8)

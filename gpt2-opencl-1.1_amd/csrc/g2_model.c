@@ -55,6 +55,7 @@ struct g2_model {
     float *att_part, *am_part;
     /* persistent step kernel: per-layer pointer table, exchange areas */
     g2_step_layer *step_layers;
+    g2p_rows *step_shares; /* row plans [step_wgs][G2P_NSHARES] (g2p_shares) */
     unsigned long long *xbuf;
     size_t xbuf_bytes;
     float *xval;
@@ -226,6 +227,16 @@ static int step_setup(g2_model *m)
     if (!rc) rc = dev_alloc(m, (void **)&m->step_layers, (size_t)L * sizeof *t, 0);
     if (!rc) rc = up(m->step_layers, t, (size_t)L * sizeof *t);
     free(t);
+    /* every work-group's row plans, read by the kernel phase by phase */
+    const size_t nsh = (size_t)nwg * G2P_NSHARES;
+    g2p_rows *sh = rc ? NULL : calloc(nsh, sizeof *sh);
+    if (!rc && !sh) rc = g2i_err(G2_E_NOMEM, "step row-plan table");
+    for (int w = 0; w < nwg && !rc; ++w)
+        g2p_shares(sh + (size_t)w * G2P_NSHARES, c->n_embd, c->n_head, c->ffn_dim, c->vocab_size,
+                   m->dtype == G2_F16 ? 8 : 4, w, nwg);
+    if (!rc) rc = dev_alloc(m, (void **)&m->step_shares, nsh * sizeof *sh, 0);
+    if (!rc) rc = up(m->step_shares, sh, nsh * sizeof *sh);
+    free(sh);
     /* A cooperative launch costs ~17 us more than a plain one between
      * back-to-back steps (1.4% of an XL token); the all-to-all kernel checks
      * residency itself, so it is launched plain unless G2_STEP_COOP=1. */
@@ -323,7 +334,7 @@ int g2_model_free(g2_model *m)
                      m->attn, m->attn_proj, m->ffn1, m->ffn2, m->qkv_new, m->qkv_full,
                      m->last_hidden, m->logits, m->partial, m->scores, m->q, m->ids_dev,
                      m->state, m->att_part, m->am_part, m->step_layers, m->xbuf, m->xval, m->lnfold, m->trace, m->pf_part,
-                     m->pf_kv };
+                     m->pf_kv, m->step_shares };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; ++i)
         if (bufs[i]) hipFree(bufs[i]);
     for (int l = 0; l < m->cfg.n_layer; ++l) {
@@ -794,6 +805,8 @@ static int step_launch(g2_model *m)
     a.scale = 1.0f / sqrtf(64.0f);
     m->step_ran = 1;
     a.xlayer = G2X_LAYER_WORDS(c->n_embd, c->n_head);
+    a.shares = m->step_shares;
+    a.nshares = m->step_wgs;
     const int fid = step_fid(m);
     if (m->plain) {
         a.plain = m->plain;
@@ -819,6 +832,11 @@ static int step_check(g2_model *m, int ngen_target)
     if (!rc) rc = g2i_hip(hipStreamSynchronize(g2i_stream()), "step check sync");
     if (rc) return rc;
     const int err = w[G2S_ERR], zero = 0;
+    if (err & G2_ERR_STEP_ARGS) {
+        rc = up(m->state + G2S_ERR, &zero, sizeof zero);
+        return rc ? rc : g2i_err(G2_E_HIP, "decode step kernel: launched with a grid its row-plan table "
+                                           "was not built for; no step ran");
+    }
     /* a timed-out hand-off (outputs invalid) is reported even if a later
      * launch of the call also found its grid not resident */
     if ((err & G2_ERR_STEP_NOT_RESIDENT) && !(err & G2_ERR_STEP_TIMEOUT)) {

@@ -457,24 +457,15 @@ struct plan : g2p_rows {
     const u32x4 *W;
 };
 
-/* The work-group's row shares of every matrix kind, computed once per
- * launch (they do not change from layer to layer). */
-struct shares {
-    g2p_rows qkv, proj, fc, fc2, lm;
-};
-
-template <typename WT>
-__device__ __forceinline__ shares make_shares(int E, int NH, int F, int V)
+/* Row plan k (G2P_SH_QKV .. G2P_SH_LM) of this work-group, from the host's
+ * per-work-group table (g2p_shares), read where a phase needs it: the table
+ * address is made opaque to the compiler, so each use is one scalar load
+ * instead of all five plans held in scalar registers across the layers. */
+__device__ __forceinline__ g2p_rows row_plan(const g2_step_args &a, int k)
 {
-    constexpr int VE = chunk_t<WT>::V;
-    const long wg = blockIdx.x, nwg = gridDim.x;
-    shares s;
-    s.qkv = g2p_rows_plan(3 * E, E, VE, wg, nwg);
-    s.proj = g2p_proj_plan(E, VE, NH, wg, nwg); /* none for a head-merging work-group */
-    s.fc = g2p_rows_plan(F, E, VE, wg, nwg);
-    s.fc2 = g2p_rows_plan(E, F, VE, wg, nwg);
-    s.lm = g2p_rows_plan(V, E, VE, wg, nwg);
-    return s;
+    const G2_CONST g2p_rows *p = (const G2_CONST g2p_rows *)a.shares + (size_t)blockIdx.x * G2P_NSHARES + k;
+    asm volatile("" : "+s"(p));
+    return *p;
 }
 
 __device__ __forceinline__ plan make_plan(const void *W, const g2p_rows &r)
@@ -918,7 +909,7 @@ __device__ __forceinline__ bool grid_resident(int tid, const ctx &c, const u64 *
  * work-group 0 merges them (g2k_argmax_merge with advance) and advances the
  * device state.  All threads of the work-group take part. */
 template <typename WT, bool TAIL>
-__device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, const shares &sh, const float *xlast, u64 *AM,
+__device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, const g2p_rows &plm, const float *xlast, u64 *AM,
                                         u32x4 (&wa)[UMAX][4], bool preloaded, float *xres, float *xe, int xeo,
                                         float *xsc, float *part, float *red, float *amv, int *ami, lds_flag *flag)
 {
@@ -930,7 +921,7 @@ __device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, con
     const int pos = clampi(a.state[G2S_POS], 0, a.S - 1);
     const unsigned seq = (unsigned)a.state[G2S_SEQ];
     const f32x4 gf = ln_gload(tid, a.lnf_w, E);
-    const plan p = make_plan(a.lm_w, sh.lm);
+    const plan p = make_plan(a.lm_w, plm);
     const int rl = min(p.r0 + tid, V - 1); /* used by tid < nrows */
     const float c1 = gl(a.lm_c1)[rl], c2 = gl(a.lm_c2)[rl];
     if (!preloaded) load_set<UMAX, TAIL>(tid, wa, p, 0);
@@ -1009,6 +1000,12 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     const int pos = clampi(a.state[G2S_POS], 0, S - 1);
     const int tok = clampi(a.state[G2S_TOK], 0, V - 1);
     const unsigned seq = (unsigned)a.state[G2S_SEQ];
+    /* the row-plan table was built for another grid: do nothing (every
+     * work-group returns here) and report it */
+    if (a.nshares != nwg) {
+        if (wg == 0 && threadIdx.x == 0) atomicOr(a.state + G2S_ERR, G2_ERR_STEP_ARGS);
+        return;
+    }
     /* a plain launch earlier in this run found the grid not resident: skip
      * until the host has resumed the run */
     if (a.plain && (a.state[G2S_ERR] & G2_ERR_STEP_NOT_RESIDENT)) return;
@@ -1028,14 +1025,16 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     /* register sets: wa carries qkv -> fc -> fc2 -> next qkv (each loaded as
      * soon as the previous matrix is consumed), wp the proj rows */
     u32x4 wa[UMAX][4], wp[UPROJ][4];
-    const shares sh = make_shares<WT>(E, NH, F, V);
     /* padded positions of this thread's input quads: quad tid of a K =
      * n_embd input, quads tid + NT*i of the K = ffn input */
     constexpr int VE = chunk_t<WT>::V;
     int xeo[1], xfo[QMAX];
-    xeo[0] = g2p_x_slot(&sh.qkv, VE, 4 * min((int)threadIdx.x, E / 4 - 1));
+    {
+        const g2p_rows pq = row_plan(a, G2P_SH_QKV), p2 = row_plan(a, G2P_SH_FC2);
+        xeo[0] = g2p_x_slot(&pq, VE, 4 * min((int)threadIdx.x, E / 4 - 1));
 #pragma unroll
-    for (int i = 0; i < QMAX; ++i) xfo[i] = g2p_x_slot(&sh.fc2, VE, 4 * min((int)threadIdx.x + NT * i, F / 4 - 1));
+        for (int i = 0; i < QMAX; ++i) xfo[i] = g2p_x_slot(&p2, VE, 4 * min((int)threadIdx.x + NT * i, F / 4 - 1));
+    }
     {
         const G2_CONST g2_step_layer *LT0 = (const G2_CONST g2_step_layer *)a.layers;
         const int tid = fresh_tid();
@@ -1051,8 +1050,8 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             if (a.plain && !(a.plain == 2 && wg == 1))
                 ll_put(a.xbuf + G2X_ARRIVE(a.L, a.xlayer, nwg) + wg, 0.f, c.tag);
         }
-        load_set<UMAX, TAIL>(tid, wa, make_plan(LT0->qkv_w, sh.qkv), 0);
-        if (wg >= NH) load_set<UPROJ, TAIL>(tid, wp, make_plan(LT0->proj_w, sh.proj), 0);
+        load_set<UMAX, TAIL>(tid, wa, make_plan(LT0->qkv_w, row_plan(a, G2P_SH_QKV)), 0);
+        if (wg >= NH) load_set<UPROJ, TAIL>(tid, wp, make_plan(LT0->proj_w, row_plan(a, G2P_SH_PROJ)), 0);
         /* the padded matrix inputs: zero everywhere (the fetches write only
          * the data positions) */
         for (int q = tid; q < G2P_XE_FLOATS / 4; q += NT) *(f32x4 *)(xe + 4 * q) = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -1074,7 +1073,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         {
             const int tid = fresh_tid();
             TRACE(0);
-            const plan p = make_plan(y.qkv_w, sh.qkv);
+            const plan p = make_plan(y.qkv_w, row_plan(a, G2P_SH_QKV));
             const f32x4 g = ln_gload(tid, y.ln1_w, E);
             const int rq = min(p.r0 + tid, 3 * E - 1); /* used by tid < nrows */
             const float c1 = gl(y.qkv_c1)[rq], c2 = gl(y.qkv_c2)[rq];
@@ -1125,7 +1124,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             TRACE(3);
             /* the fc rows stream from here on; a work-group that merges a head
              * issues them after its merge, so its merge waits behind nothing */
-            if (wg >= NH) load_set<UMAX, TAIL>(tid, wa, make_plan(y.fc_w, sh.fc), 0);
+            if (wg >= NH) load_set<UMAX, TAIL>(tid, wa, make_plan(y.fc_w, row_plan(a, G2P_SH_FC)), 0);
         }
 
         /* ---- MERGE: head h by work-group h (g2k_attn_merge) */
@@ -1150,7 +1149,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         {
             const int tid = fresh_tid();
             TRACE(16);
-            if (wg < NH) load_set<UMAX, TAIL>(tid, wa, make_plan(y.fc_w, sh.fc), 0);
+            if (wg < NH) load_set<UMAX, TAIL>(tid, wa, make_plan(y.fc_w, row_plan(a, G2P_SH_FC)), 0);
             TRACE(4);
         }
 
@@ -1161,7 +1160,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             TRACE(6);
         } else {
             const int tid = fresh_tid();
-            const plan p = make_plan(y.proj_w, sh.proj);
+            const plan p = make_plan(y.proj_w, row_plan(a, G2P_SH_PROJ));
             const float bias = gl(y.proj_b)[min(p.r0 + tid, E - 1)];
             fetch4<NQE>(tid, c, RV + G2V_O(E), E, NH, xe, xeo, (lds_flag *)&flag);
             TRACE(5);
@@ -1173,14 +1172,14 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 vput(RV + G2V_X1(E) + r, RN + G2V_X1(E) + r, v + xres[r]);
             }
             TRACE(6);
-            if (l + 1 < a.L) load_set<UPROJ, TAIL>(tid, wp, make_plan(LT[l + 1].proj_w, sh.proj), 0);
+            if (l + 1 < a.L) load_set<UPROJ, TAIL>(tid, wp, make_plan(LT[l + 1].proj_w, row_plan(a, G2P_SH_PROJ)), 0);
             __syncthreads();
         }
 
         /* ---- FC: H = gelu(LayerNorm(X1) . Wfc + b), the LayerNorm folded in */
         {
             const int tid = fresh_tid();
-            const plan p = make_plan(y.fc_w, sh.fc);
+            const plan p = make_plan(y.fc_w, row_plan(a, G2P_SH_FC));
             const f32x4 g = ln_gload(tid, y.ln2_w, E);
             const int rf = min(p.r0 + tid, F - 1); /* used by tid < nrows */
             const float c1 = gl(y.fc_c1)[rf], c2 = gl(y.fc_c2)[rf];
@@ -1198,14 +1197,14 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 vput(RV + G2V_H(E) + r, RN + G2V_H(E) + r, gelu_f(v));
             }
             TRACE(8);
-            load_set<UMAX, TAIL>(tid, wa, make_plan(y.fc2_w, sh.fc2), 0);
+            load_set<UMAX, TAIL>(tid, wa, make_plan(y.fc2_w, row_plan(a, G2P_SH_FC2)), 0);
             __syncthreads();
         }
 
         /* ---- FC2: X2 = X1 + (H . Wfc2 + b) */
         {
             const int tid = fresh_tid();
-            const plan p = make_plan(y.fc2_w, sh.fc2);
+            const plan p = make_plan(y.fc2_w, row_plan(a, G2P_SH_FC2));
             const float bias = gl(y.fc2_b)[min(p.r0 + tid, E - 1)];
             fetch4<QMAX>(tid, c, RV + G2V_H(E), F, nwg, xf, xfo, (lds_flag *)&flag);
             TRACE(9);
@@ -1218,14 +1217,14 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 vput(RV + G2V_X2(E, F) + r, RN + G2V_X2(E, F) + r, v + xres[r]);
             }
             TRACE(10);
-            if (l + 1 < a.L) load_set<UMAX, TAIL>(tid, wa, make_plan(LT[l + 1].qkv_w, sh.qkv), 0);
-            else load_set<UMAX, TAIL>(tid, wa, make_plan(a.lm_w, sh.lm), 0);
+            if (l + 1 < a.L) load_set<UMAX, TAIL>(tid, wa, make_plan(LT[l + 1].qkv_w, row_plan(a, G2P_SH_QKV)), 0);
+            else load_set<UMAX, TAIL>(tid, wa, make_plan(a.lm_w, row_plan(a, G2P_SH_LM)), 0);
             __syncthreads();
         }
     }
 
     /* the first batch of lm_head rows was loaded by the last fc2 phase */
-    lm_pick<WT, TAIL>(a, c, sh, XV + 2 * VR * (a.L - 1) + G2V_X2(E, F), X + (size_t)a.L * a.xlayer, wa, true,
+    lm_pick<WT, TAIL>(a, c, row_plan(a, G2P_SH_LM), XV + 2 * VR * (a.L - 1) + G2V_X2(E, F), X + (size_t)a.L * a.xlayer, wa, true,
                 xres, xe, xeo[0], xsc, part, red, amv, ami, (lds_flag *)&flag);
 }
 

@@ -66,6 +66,20 @@ G2P_FN g2p_rows g2p_proj_plan(int E, int VE, int NH, long wg, long nwg)
     return g2p_rows_plan(E, E, VE, wg - NH, nwg - NH);
 }
 
+/* The row plans of work-group wg of nwg, in the order of the step kernel's
+ * per-work-group table (qkv, proj, fc, fc2, lm_head).  The host builds the
+ * table with this function; the kernel reads a plan from it when a phase
+ * needs it, so no plan stays in scalar registers across the layers. */
+enum { G2P_SH_QKV, G2P_SH_PROJ, G2P_SH_FC, G2P_SH_FC2, G2P_SH_LM, G2P_NSHARES };
+G2P_FN void g2p_shares(g2p_rows *s, int E, int NH, int F, int V, int VE, long wg, long nwg)
+{
+    s[G2P_SH_QKV] = g2p_rows_plan(3 * E, E, VE, wg, nwg);
+    s[G2P_SH_PROJ] = g2p_proj_plan(E, VE, NH, wg, nwg); /* none for a head-merging work-group */
+    s[G2P_SH_FC] = g2p_rows_plan(F, E, VE, wg, nwg);
+    s[G2P_SH_FC2] = g2p_rows_plan(E, F, VE, wg, nwg);
+    s[G2P_SH_LM] = g2p_rows_plan(V, E, VE, wg, nwg);
+}
+
 /* Unit j of a register set of UM units per wave, for the batch `batch` of
  * the share, as loaded by wave `wave`: unit u = batch*NW*UM + wave + NW*j,
  * its row's first chunk (base = row * C) and its column chunks [c0, clast].

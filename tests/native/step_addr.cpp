@@ -12,6 +12,9 @@
  *             biases and LayerNorm parameters, the embedding rows;
  *   KV cache  the attention units' 16-byte loads of K [E][S] and V [S][E]
  *             and the current position's K/V stores;
+ *   plans     the work-group's row plans in the host's table (g2p_shares):
+ *             each entry read inside the table and equal to the plan of its
+ *             matrix;
  *   exchange  every tagged word read or written: q/k/v, chunk partials,
  *             the argmax words, the arrival words; every plain value
  *             stored (merged O, X1, H, X2, in the region of either tag
@@ -28,8 +31,8 @@
  * Usage: step_addr L E NH V F VE POS NWG [plant]
  *   VE: elements per 16-byte chunk (8 fp16, 4 fp32); plant=1 replaces the
  *   clamped chunk of g2p_unit_chunk by the unclamped one, plant=2 shifts the
- *   dot products' x reads by one chunk (planted mistakes the check must
- *   catch).
+ *   dot products' x reads by one chunk, plant=3 swaps the fc and fc2 entries
+ *   of the row-plan table (planted mistakes the check must catch).
  */
 #include <cstdio>
 #include <cstdlib>
@@ -49,6 +52,15 @@ static void chk(const char *what, long lo, long hi_excl, long lim)
         }
         ++n_bad;
     }
+}
+
+/* a row-plan table entry must be the plan of its matrix, field for field */
+static void same_plan(const char *what, const g2p_rows &t, const g2p_rows &p)
+{
+    const bool eq = t.C == p.C && t.nseg == p.nseg && t.lseg == p.lseg && t.SL == p.SL && t.r0 == p.r0 &&
+                    t.nrows == p.nrows && t.nunits == p.nunits && t.tail == p.tail;
+    if (!eq && !n_bad) fprintf(stderr, "%s: table entry differs from the plan of its matrix\n", what);
+    chk(what, 0, eq ? 0 : 1, 0);
 }
 
 static int plant = 0;
@@ -137,10 +149,9 @@ static void dot_set(const char *what, const g2p_rows &p, int UM, int batch, int 
 
 /* a whole matrix share as matvec<UM> runs it (batch 0 preloaded, later
  * batches loaded on demand), its bias load and the row sums */
-static void matrix(const char *what, const void *bias_tag, int N, int K, int VE, int UM, long wg, long nwg,
+static void matrix(const char *what, const void *bias_tag, const g2p_rows &p, int N, int K, int VE, int UM,
                    long xcap = G2P_XE_FLOATS)
 {
-    const g2p_rows p = g2p_rows_plan(N, K, VE, wg, nwg);
     chk("rows per work-group", 0, p.nrows, G2_STEP_THREADS);
     for (int b = 0; b == 0 || b * G2P_NW * UM < p.nunits; ++b) {
         load_set(what, p, UM, b, N, VE);
@@ -200,6 +211,23 @@ int main(int argc, char **argv)
     };
     long proj_rows = 0; /* rows of proj over all work-groups and layers */
     for (long wg = 0; wg < nwg; ++wg) {
+        /* the work-group's row plans as the kernel reads them from the host's
+         * table (g2p_shares; entries wg * G2P_NSHARES + k of a [nwg][5]
+         * table), each the plan of its own matrix */
+        g2p_rows shp[G2P_NSHARES];
+        g2p_shares(shp, E, NH, F, V, VE, wg, nwg);
+        if (plant == 3) {
+            const g2p_rows t = shp[G2P_SH_FC];
+            shp[G2P_SH_FC] = shp[G2P_SH_FC2];
+            shp[G2P_SH_FC2] = t;
+        }
+        for (int k = 0; k < G2P_NSHARES; ++k)
+            chk("row-plan table read", wg * G2P_NSHARES + k, wg * G2P_NSHARES + k + 1, (long)nwg * G2P_NSHARES);
+        same_plan("qkv row plan", shp[G2P_SH_QKV], g2p_rows_plan(3 * E, E, VE, wg, nwg));
+        same_plan("proj row plan", shp[G2P_SH_PROJ], g2p_proj_plan(E, VE, NH, wg, nwg));
+        same_plan("fc row plan", shp[G2P_SH_FC], g2p_rows_plan(F, E, VE, wg, nwg));
+        same_plan("fc2 row plan", shp[G2P_SH_FC2], g2p_rows_plan(E, F, VE, wg, nwg));
+        same_plan("lm_head row plan", shp[G2P_SH_LM], g2p_rows_plan(V, E, VE, wg, nwg));
         /* embedding of the token at pos, LayerNorm parameters */
         for (int tid = 0; tid < NT; ++tid) {
             for (int d = tid; d < E; d += NT) {
@@ -216,8 +244,8 @@ int main(int argc, char **argv)
         for (int l = 0; l < L; ++l) {
             const long R = G2X_HEAD + (long)l * xlayer;
             /* QKV: rows, K/V cache stores at pos, q/k/v words */
-            matrix("qkv weights", "b", 3 * E, E, VE, 4, wg, nwg);
-            const g2p_rows pq = g2p_rows_plan(3 * E, E, VE, wg, nwg);
+            const g2p_rows &pq = shp[G2P_SH_QKV];
+            matrix("qkv weights", "b", pq, 3 * E, E, VE, 4);
             for (int tid = 0; tid < NT; ++tid) {
                 const int rq = g2p_min(pq.r0 + tid, 3 * E - 1);
                 chk("qkv LayerNorm fold sums", rq, rq + 1, 3L * E);
@@ -263,30 +291,30 @@ int main(int argc, char **argv)
             /* PROJ, FC, FC2 */
             /* proj: the work-groups merging no head */
             if (wg >= NH) {
-                matrix("proj weights", "b", E, E, VE, 1, wg - NH, nwg - NH);
+                matrix("proj weights", "b", shp[G2P_SH_PROJ], E, E, VE, 1);
                 for (int b = 0; b < 2; ++b) quads("O fetch", vreg(l, b) + vO, E, vreg(l, b) + vX1);
-                const g2p_rows pp = g2p_proj_plan(E, VE, NH, wg, nwg);
+                const g2p_rows &pp = shp[G2P_SH_PROJ];
                 vstore("X1 values", l, vX1, pp.r0, pp.r0 + pp.nrows, vH);
                 proj_rows += pp.nrows;
             }
             for (int b = 0; b < 2; ++b) quads("X1 fetch", vreg(l, b) + vX1, E, vreg(l, b) + vH);
-            matrix("fc weights", "b", F, E, VE, 4, wg, nwg);
-            const g2p_rows pf = g2p_rows_plan(F, E, VE, wg, nwg);
+            const g2p_rows &pf = shp[G2P_SH_FC];
+            matrix("fc weights", "b", pf, F, E, VE, 4);
             for (int tid = 0; tid < NT; ++tid) {
                 const int rf = g2p_min(pf.r0 + tid, F - 1);
                 chk("fc LayerNorm fold sums", rf, rf + 1, F);
             }
             vstore("H values", l, vH, pf.r0, pf.r0 + pf.nrows, vX2);
             for (int b = 0; b < 2; ++b) quads("H fetch", vreg(l, b) + vH, F, vreg(l, b) + vX2);
-            matrix("fc2 weights", "b", E, F, VE, 4, wg, nwg, G2P_XF_FLOATS);
-            const g2p_rows p2 = g2p_rows_plan(E, F, VE, wg, nwg);
+            const g2p_rows &p2 = shp[G2P_SH_FC2];
+            matrix("fc2 weights", "b", p2, E, F, VE, 4, G2P_XF_FLOATS);
             vstore("X2 values", l, vX2, p2.r0, p2.r0 + p2.nrows, VR);
 
         }
         /* LM head: X2 of the last layer, rows, logits, argmax words */
         for (int b = 0; b < 2; ++b) quads("LM X2 fetch", vreg(L - 1, b) + vX2, E, vreg(L - 1, b) + VR);
-        matrix("lm_head weights", nullptr, V, E, VE, 4, wg, nwg);
-        const g2p_rows pl = g2p_rows_plan(V, E, VE, wg, nwg);
+        const g2p_rows &pl = shp[G2P_SH_LM];
+        matrix("lm_head weights", nullptr, pl, V, E, VE, 4);
         chk("logits", pl.r0, pl.r0 + pl.nrows, V);
         for (int tid = 0; tid < NT; ++tid) {
             const int rl = g2p_min(pl.r0 + tid, V - 1);

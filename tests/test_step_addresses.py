@@ -76,3 +76,11 @@ def test_planted_unclamped_chunk_is_caught(checker):
     assert rc == 1 and "out of bounds" in out, out
     rc, out = run(checker, "tiny", 8, 5, 256, plant=1)
     assert rc == 1, out
+
+
+def test_planted_row_plan_table_swap_is_caught(checker):
+    """A row-plan table whose fc and fc2 entries are swapped must be caught
+    (each entry is checked against the plan of its own matrix)."""
+    for ve in (8, 4):
+        rc, out = run(checker, "xl", ve, 700, 256, plant=3)
+        assert rc == 1 and "row plan" in out, out
