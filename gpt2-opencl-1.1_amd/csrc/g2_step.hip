@@ -657,7 +657,7 @@ struct att_regs {
     f32x4 kv[4], vv[4];
 };
 
-__device__ __forceinline__ void attn_load(int tid, const g2_step_layer &y, att_regs &r, bool on, int h,
+__device__ __forceinline__ void attn_load(int tid, const G2_CONST g2_step_layer *y, att_regs &r, bool on, int h,
                                           int ch, int pos, int T, int E, int S)
 {
     const int t = tid & 255;
@@ -675,20 +675,20 @@ __device__ __forceinline__ void attn_load(int tid, const g2_step_layer &y, att_r
     long koff, voff[4];
     g2p_attn_offsets(t, on, h, ch, E, S, &koff, voff);
     const size_t kstr = on ? (size_t)(S / 4) : 0;
-    const G2_GLOBAL f32x4 *kb = gl((const f32x4 *)(y.k_cache + koff));
+    const G2_GLOBAL f32x4 *kb = gl((const f32x4 *)(y->k_cache + koff));
 #pragma unroll
     for (int d = 0; d < 4; ++d) r.kv[d] = kb[(size_t)d * kstr];
 }
 /* The values of the same chunk (needed only after the scores and the
  * softmax): issued once the unit's q/k/v have arrived, so the q/k/v reads
  * queue behind the keys only. */
-__device__ __forceinline__ void attn_load_v(int tid, const g2_step_layer &y, att_regs &r, bool on, int h,
+__device__ __forceinline__ void attn_load_v(int tid, const G2_CONST g2_step_layer *y, att_regs &r, bool on, int h,
                                             int ch, int E, int S)
 {
     long koff, voff[4];
     g2p_attn_offsets(tid & 255, on, h, ch, E, S, &koff, voff);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) r.vv[e] = *gl((const f32x4 *)(y.v_cache + voff[e]));
+    for (int e = 0; e < 4; ++e) r.vv[e] = *gl((const f32x4 *)(y->v_cache + voff[e]));
 }
 
 /* The attention of one 64-position chunk once L.q, L.kn and L.vn hold the
@@ -775,7 +775,7 @@ __device__ __forceinline__ void attn_compute(int tid, const ctx &c, float scale,
  * barriers. */
 __device__ __forceinline__ void attn_chunk(int tid, const ctx &c, float scale, const u64 *src, int qo,
                                            int ko, int vo, u64 *pout, att_lds &L, att_regs &r, bool on,
-                                           int ch, int pos, int T, const g2_step_layer &y, int h, int E, int S)
+                                           int ch, int pos, int T, const G2_CONST g2_step_layer *y, int h, int E, int S)
 {
     const int t = tid & 255;
     /* q, k and v of the head at this position: src[qo + d], src[ko + d],
@@ -1064,7 +1064,14 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
 
     const G2_CONST g2_step_layer *LT = (const G2_CONST g2_step_layer *)a.layers;
     for (int l = 0; l < a.L; ++l) {
-        const g2_step_layer y = LT[l];
+        /* this layer's pointers, read from the layer table where a phase
+         * uses them (the table address made opaque to the compiler, as for
+         * the row plans) */
+        auto layer = [&]() {
+            const G2_CONST g2_step_layer *p = LT + l;
+            asm volatile("" : "+s"(p));
+            return p;
+        };
         u64 *R = X + (size_t)l * a.xlayer;
         float *RV = XV + 2 * VR * l, *RN = XN + 2 * VR * l;
 
@@ -1073,10 +1080,11 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         {
             const int tid = fresh_tid();
             TRACE(0);
-            const plan p = make_plan(y.qkv_w, row_plan(a, G2P_SH_QKV));
-            const f32x4 g = ln_gload(tid, y.ln1_w, E);
+            const G2_CONST g2_step_layer *y = layer();
+            const plan p = make_plan(y->qkv_w, row_plan(a, G2P_SH_QKV));
+            const f32x4 g = ln_gload(tid, y->ln1_w, E);
             const int rq = min(p.r0 + tid, 3 * E - 1); /* used by tid < nrows */
-            const float c1 = gl(y.qkv_c1)[rq], c2 = gl(y.qkv_c2)[rq];
+            const float c1 = gl(y->qkv_c1)[rq], c2 = gl(y->qkv_c2)[rq];
             f32x4 xq;
             float x0;
             if (l > 0) {
@@ -1099,8 +1107,8 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 const int r = p.r0 + tid;
                 const float v = ln_fold_out(st, row_sum(p, part, tid), c1, c2);
                 ll_put(R + r, v, c.tag);
-                if (r >= 2 * E) glw(y.v_cache)[(size_t)pos * E + (r - 2 * E)] = v;
-                else if (r >= E) glw(y.k_cache)[(size_t)(r - E) * S + pos] = v;
+                if (r >= 2 * E) glw(y->v_cache)[(size_t)pos * E + (r - 2 * E)] = v;
+                else if (r >= E) glw(y->k_cache)[(size_t)(r - E) * S + pos] = v;
             }
             TRACE(2);
         }
@@ -1108,6 +1116,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         /* ---- ATTN: unit u = h * nch + chunk, work-group u % nwg, half */
         {
             const int tid = fresh_tid();
+            const G2_CONST g2_step_layer *y = layer();
             const int nunits = NH * nch;
             const int rounds = (nunits + 2 * nwg - 1) / (2 * nwg);
             const int hf = tid >> 8;
@@ -1124,7 +1133,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             TRACE(3);
             /* the fc rows stream from here on; a work-group that merges a head
              * issues them after its merge, so its merge waits behind nothing */
-            if (wg >= NH) load_set<UMAX, TAIL>(tid, wa, make_plan(y.fc_w, row_plan(a, G2P_SH_FC)), 0);
+            if (wg >= NH) load_set<UMAX, TAIL>(tid, wa, make_plan(y->fc_w, row_plan(a, G2P_SH_FC)), 0);
         }
 
         /* ---- MERGE: head h by work-group h (g2k_attn_merge) */
@@ -1149,7 +1158,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         {
             const int tid = fresh_tid();
             TRACE(16);
-            if (wg < NH) load_set<UMAX, TAIL>(tid, wa, make_plan(y.fc_w, row_plan(a, G2P_SH_FC)), 0);
+            if (wg < NH) load_set<UMAX, TAIL>(tid, wa, make_plan(layer()->fc_w, row_plan(a, G2P_SH_FC)), 0);
             TRACE(4);
         }
 
@@ -1160,8 +1169,9 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             TRACE(6);
         } else {
             const int tid = fresh_tid();
-            const plan p = make_plan(y.proj_w, row_plan(a, G2P_SH_PROJ));
-            const float bias = gl(y.proj_b)[min(p.r0 + tid, E - 1)];
+            const G2_CONST g2_step_layer *y = layer();
+            const plan p = make_plan(y->proj_w, row_plan(a, G2P_SH_PROJ));
+            const float bias = gl(y->proj_b)[min(p.r0 + tid, E - 1)];
             fetch4<NQE>(tid, c, RV + G2V_O(E), E, NH, xe, xeo, (lds_flag *)&flag);
             TRACE(5);
             matvec<WT, UPROJ, TAIL>(tid, wp, p, xe, part);
@@ -1179,10 +1189,11 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         /* ---- FC: H = gelu(LayerNorm(X1) . Wfc + b), the LayerNorm folded in */
         {
             const int tid = fresh_tid();
-            const plan p = make_plan(y.fc_w, row_plan(a, G2P_SH_FC));
-            const f32x4 g = ln_gload(tid, y.ln2_w, E);
+            const G2_CONST g2_step_layer *y = layer();
+            const plan p = make_plan(y->fc_w, row_plan(a, G2P_SH_FC));
+            const f32x4 g = ln_gload(tid, y->ln2_w, E);
             const int rf = min(p.r0 + tid, F - 1); /* used by tid < nrows */
-            const float c1 = gl(y.fc_c1)[rf], c2 = gl(y.fc_c2)[rf];
+            const float c1 = gl(y->fc_c1)[rf], c2 = gl(y->fc_c2)[rf];
             float x0;
             const f32x4 xq = fetch_q(tid, c, RV + G2V_X1(E), E, xres, x0);
             TRACE(7);
@@ -1197,15 +1208,16 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 vput(RV + G2V_H(E) + r, RN + G2V_H(E) + r, gelu_f(v));
             }
             TRACE(8);
-            load_set<UMAX, TAIL>(tid, wa, make_plan(y.fc2_w, row_plan(a, G2P_SH_FC2)), 0);
+            load_set<UMAX, TAIL>(tid, wa, make_plan(y->fc2_w, row_plan(a, G2P_SH_FC2)), 0);
             __syncthreads();
         }
 
         /* ---- FC2: X2 = X1 + (H . Wfc2 + b) */
         {
             const int tid = fresh_tid();
-            const plan p = make_plan(y.fc2_w, row_plan(a, G2P_SH_FC2));
-            const float bias = gl(y.fc2_b)[min(p.r0 + tid, E - 1)];
+            const G2_CONST g2_step_layer *y = layer();
+            const plan p = make_plan(y->fc2_w, row_plan(a, G2P_SH_FC2));
+            const float bias = gl(y->fc2_b)[min(p.r0 + tid, E - 1)];
             fetch4<QMAX>(tid, c, RV + G2V_H(E), F, nwg, xf, xfo, (lds_flag *)&flag);
             TRACE(9);
             matvec<WT, UMAX, TAIL>(tid, wa, p, xf, part);
