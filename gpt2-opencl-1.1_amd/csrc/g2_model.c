@@ -783,6 +783,9 @@ static int step_fid(const g2_model *m)
 {
     const g2_config *c = &m->cfg;
     const int tail = g2p_step_tail(c->n_embd, c->ffn_dim, m->dtype == G2_F16 ? 8 : 4);
+    if (m->trace) /* the variants with the phase timestamps */
+        return m->dtype == G2_F16 ? (tail ? G2F_STEP_F16T_TR : G2F_STEP_F16_TR)
+                                  : (tail ? G2F_STEP_F32T_TR : G2F_STEP_F32_TR);
     return m->dtype == G2_F16 ? (tail ? G2F_STEP_F16T : G2F_STEP_F16) : (tail ? G2F_STEP_F32T : G2F_STEP_F32);
 }
 

@@ -187,12 +187,13 @@ int g2_init(int device)
      * them co-resident: require cooperative launch support and an occupancy
      * of at least one work-group per CU for both weight types. */
     {
-        int coop = 0, nb[4] = { -1, -1, -1, -1 };
+        int coop = 0, nb[8] = { -1, -1, -1, -1, -1, -1, -1, -1 };
         hipError_t ea = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device);
-        hipError_t eo[4] = { hipSuccess, hipSuccess, hipSuccess, hipSuccess };
-        const int fids[4] = { G2F_STEP_F32, G2F_STEP_F16, G2F_STEP_F32T, G2F_STEP_F16T };
+        hipError_t eo[8] = { hipSuccess, hipSuccess, hipSuccess, hipSuccess, hipSuccess, hipSuccess, hipSuccess, hipSuccess };
+        const int fids[8] = { G2F_STEP_F32, G2F_STEP_F16, G2F_STEP_F32T, G2F_STEP_F16T,
+                              G2F_STEP_F32_TR, G2F_STEP_F16_TR, G2F_STEP_F32T_TR, G2F_STEP_F16T_TR };
         int ok = ea == hipSuccess && coop;
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 8; ++i) {
             eo[i] = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb[i], G.fn[fids[i]], G2_STEP_THREADS, 0);
             ok = ok && eo[i] == hipSuccess && nb[i] >= 1;
         }

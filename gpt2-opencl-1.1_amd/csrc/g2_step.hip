@@ -834,9 +834,11 @@ __device__ __forceinline__ void blk_argmax(int tid, float bv, int bi, float *amv
 }
 
 /* Phase timestamps (only when the caller passed a trace buffer). */
+/* Phase timestamps, compiled only into the traced kernel variants (TRACED):
+ * the untraced ones carry no trace pointer or stamp code in their layer loop. */
 #define TRACE(k)                                                                       \
     do {                                                                               \
-        if (a.trace && tid == 0)                                                       \
+        if (TRACED && a.trace && tid == 0)                                             \
             a.trace[(size_t)wg * G2_TRACE_STRIDE(a.L) + 24 * l + (k)] = wall_clock64(); \
     } while (0)
 
@@ -908,7 +910,7 @@ __device__ __forceinline__ bool grid_resident(int tid, const ctx &c, const u64 *
  * work-group's head rows -> first-max per work-group (argmax words AM) ->
  * work-group 0 merges them (g2k_argmax_merge with advance) and advances the
  * device state.  All threads of the work-group take part. */
-template <typename WT, bool TAIL>
+template <typename WT, bool TAIL, bool TRACED>
 __device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, const g2p_rows &plm, const float *xlast, u64 *AM,
                                         u32x4 (&wa)[UMAX][4], bool preloaded, float *xres, float *xe, int xeo,
                                         float *xsc, float *part, float *red, float *amv, int *ami, lds_flag *flag)
@@ -975,7 +977,7 @@ __device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, con
     TRACE(2);
 }
 
-template <typename WT, bool TAIL>
+template <typename WT, bool TAIL, bool TRACED>
 __device__ __forceinline__ void step_impl(const g2_step_args &a)
 {
     /* 16-byte alignment: the dot products read 16-byte chunks of these */
@@ -1236,7 +1238,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     }
 
     /* the first batch of lm_head rows was loaded by the last fc2 phase */
-    lm_pick<WT, TAIL>(a, c, row_plan(a, G2P_SH_LM), XV + 2 * VR * (a.L - 1) + G2V_X2(E, F), X + (size_t)a.L * a.xlayer, wa, true,
+    lm_pick<WT, TAIL, TRACED>(a, c, row_plan(a, G2P_SH_LM), XV + 2 * VR * (a.L - 1) + G2V_X2(E, F), X + (size_t)a.L * a.xlayer, wa, true,
                 xres, xe, xeo[0], xsc, part, red, amv, ami, (lds_flag *)&flag);
 }
 
@@ -1244,20 +1246,38 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
 
 extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f32(const g2_step_args a)
 {
-    g2step::step_impl<float, false>(a);
+    g2step::step_impl<float, false, false>(a);
 }
 extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f16(const g2_step_args a)
 {
-    g2step::step_impl<_Float16, false>(a);
+    g2step::step_impl<_Float16, false, false>(a);
 }
 /* The tail form, for models whose every four-unit plan is a tail plan
  * (g2p_step_tail: n_embd 1600, the rows of every matrix 200 chunks per
  * segment). */
 extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f32_tail(const g2_step_args a)
 {
-    g2step::step_impl<float, true>(a);
+    g2step::step_impl<float, true, false>(a);
 }
 extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f16_tail(const g2_step_args a)
 {
-    g2step::step_impl<_Float16, true>(a);
+    g2step::step_impl<_Float16, true, false>(a);
+}
+/* The same four with the phase timestamps of g2_step_args.trace (launched
+ * instead of them when a trace buffer is set). */
+extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f32_trace(const g2_step_args a)
+{
+    g2step::step_impl<float, false, true>(a);
+}
+extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f16_trace(const g2_step_args a)
+{
+    g2step::step_impl<_Float16, false, true>(a);
+}
+extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f32_tail_trace(const g2_step_args a)
+{
+    g2step::step_impl<float, true, true>(a);
+}
+extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f16_tail_trace(const g2_step_args a)
+{
+    g2step::step_impl<_Float16, true, true>(a);
 }
