@@ -60,6 +60,8 @@ extern "C" {
     X(STEP_F32_TR, "g2k_step_f32_trace") X(STEP_F16_TR, "g2k_step_f16_trace") \
     X(STEP_F32T_TR, "g2k_step_f32_tail_trace")                                \
     X(STEP_F16T_TR, "g2k_step_f16_tail_trace")                                \
+    X(STEP_F16TN, "g2k_step_f16_tailn")                                       \
+    X(STEP_F16TN_TR, "g2k_step_f16_tailn_trace")                              \
     X(HGEMM_STORE, "g2k_hgemm_store") X(HGEMM_GELU, "g2k_hgemm_gelu")         \
     X(HGEMM_RESID, "g2k_hgemm_resid") X(HGEMM_QKV, "g2k_hgemm_qkv")           \
     X(ATTN_PREFILL_MFMA, "g2k_attn_prefill_mfma")                             \

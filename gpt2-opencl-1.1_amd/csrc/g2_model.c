@@ -782,11 +782,16 @@ static int fused_step_launches(g2_model *m)
 static int step_fid(const g2_model *m)
 {
     const g2_config *c = &m->cfg;
-    const int tail = g2p_step_tail(c->n_embd, c->ffn_dim, m->dtype == G2_F16 ? 8 : 4);
+    const int VE = m->dtype == G2_F16 ? 8 : 4;
+    const int tail = g2p_step_tail(c->n_embd, c->ffn_dim, VE);
+    /* the fp16 tail form compiled for GPT-2 XL's shape, else the one that
+     * reads the shape from its arguments */
+    const int xl = tail && g2p_step_xl_shape(c->n_embd, c->ffn_dim, c->n_head, c->vocab_size, VE);
     if (m->trace) /* the variants with the phase timestamps */
-        return m->dtype == G2_F16 ? (tail ? G2F_STEP_F16T_TR : G2F_STEP_F16_TR)
+        return m->dtype == G2_F16 ? (tail ? (xl ? G2F_STEP_F16T_TR : G2F_STEP_F16TN_TR) : G2F_STEP_F16_TR)
                                   : (tail ? G2F_STEP_F32T_TR : G2F_STEP_F32_TR);
-    return m->dtype == G2_F16 ? (tail ? G2F_STEP_F16T : G2F_STEP_F16) : (tail ? G2F_STEP_F32T : G2F_STEP_F32);
+    return m->dtype == G2_F16 ? (tail ? (xl ? G2F_STEP_F16T : G2F_STEP_F16TN) : G2F_STEP_F16)
+                              : (tail ? G2F_STEP_F32T : G2F_STEP_F32);
 }
 
 /* One decode forward at state[POS] as one cooperative launch of the

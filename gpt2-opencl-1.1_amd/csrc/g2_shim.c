@@ -187,13 +187,19 @@ int g2_init(int device)
      * them co-resident: require cooperative launch support and an occupancy
      * of at least one work-group per CU for both weight types. */
     {
-        int coop = 0, nb[8] = { -1, -1, -1, -1, -1, -1, -1, -1 };
+        enum { NSTEP = 10 };
+        int coop = 0, nb[NSTEP];
         hipError_t ea = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device);
-        hipError_t eo[8] = { hipSuccess, hipSuccess, hipSuccess, hipSuccess, hipSuccess, hipSuccess, hipSuccess, hipSuccess };
-        const int fids[8] = { G2F_STEP_F32, G2F_STEP_F16, G2F_STEP_F32T, G2F_STEP_F16T,
-                              G2F_STEP_F32_TR, G2F_STEP_F16_TR, G2F_STEP_F32T_TR, G2F_STEP_F16T_TR };
+        hipError_t eo[NSTEP];
+        const int fids[NSTEP] = { G2F_STEP_F32, G2F_STEP_F16, G2F_STEP_F32T, G2F_STEP_F16T, G2F_STEP_F16TN,
+                                  G2F_STEP_F32_TR, G2F_STEP_F16_TR, G2F_STEP_F32T_TR, G2F_STEP_F16T_TR,
+                                  G2F_STEP_F16TN_TR };
         int ok = ea == hipSuccess && coop;
-        for (int i = 0; i < 8; ++i) {
+        for (int i = 0; i < NSTEP; ++i) {
+            nb[i] = -1;
+            eo[i] = hipSuccess;
+        }
+        for (int i = 0; i < NSTEP; ++i) {
             eo[i] = hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb[i], G.fn[fids[i]], G2_STEP_THREADS, 0);
             ok = ok && eo[i] == hipSuccess && nb[i] >= 1;
         }

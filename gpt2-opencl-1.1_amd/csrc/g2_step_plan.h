@@ -184,6 +184,19 @@ G2P_FN int g2p_step_tail(int E, int F, int VE)
     return g2p_rows_plan(1, E, VE, 0, 1).tail && g2p_rows_plan(1, F, VE, 0, 1).tail;
 }
 
+/* The model shape the fp16 tail-form step kernel is compiled for (GPT-2 XL:
+ * n_embd 1600, ffn 6400, 25 heads, vocabulary 50257): that kernel folds
+ * these sizes and the plans' per-matrix fields at compile time; other tail
+ * shapes run the form that reads them from its arguments. */
+#define G2P_XL_E 1600
+#define G2P_XL_F 6400
+#define G2P_XL_NH 25
+#define G2P_XL_V 50257
+G2P_FN int g2p_step_xl_shape(int E, int F, int NH, int V, int VE)
+{
+    return VE == 8 && E == G2P_XL_E && F == G2P_XL_F && NH == G2P_XL_NH && V == G2P_XL_V;
+}
+
 /* Attention unit (head h, 64-position chunk ch) by the 256 threads of one
  * half of a work-group, thread t: the K-cache floats it loads are
  * koff + d*S .. + 3 for d < 4 (transposed cache [E][S]: dims 4dg..4dg+3 of

@@ -43,12 +43,17 @@ def test_step_kernel_names(g2):
     profile by): the tail form when every matrix row splits into segments
     of 193..208 16-byte chunks (GPT-2 XL: rows of n_embd 1600 or ffn 6400
     inputs split into segments of 200 chunks, in fp16 and in fp32), the
-    plain form otherwise, none with the per-operator kernels."""
+    plain form otherwise, none with the per-operator kernels.  The fp16
+    tail form is compiled for GPT-2 XL's exact shape (g2k_step_f16_tail);
+    another tail shape (here XL width with a smaller vocabulary) runs the
+    form that reads the shape from its arguments (g2k_step_f16_tailn)."""
     cases = [("xl", g2.F16, "g2k_step_f16_tail"), ("xl", g2.F32, "g2k_step_f32_tail"),
              ("large", g2.F16, "g2k_step_f16"), ("large", g2.F32, "g2k_step_f32"),
-             ("small", g2.F32, "g2k_step_f32"), ("medium", g2.F32, "g2k_step_f32")]
+             ("small", g2.F32, "g2k_step_f32"), ("medium", g2.F32, "g2k_step_f32"),
+             (g2.make_config(2, 1600, 25, vocab_size=4096), g2.F16, "g2k_step_f16_tailn")]
     for preset, dtype, name in cases:
-        m = g2.Model.synth(g2.preset(preset), SEED, dtype, g2.PATH_FUSED)
+        cfg = g2.preset(preset) if isinstance(preset, str) else preset
+        m = g2.Model.synth(cfg, SEED, dtype, g2.PATH_FUSED)
         assert m.uses_step()
         assert m.step_kernel() == name, (preset, dtype, m.step_kernel())
         m.set_step(False)
@@ -106,6 +111,32 @@ def test_step_xl_width_to_end_of_context(g2):
         pos = P + k
         om.decode(tok, pos)
         m.decode(tok, pos)
+        _check(m.logits(), om.logits())
+        tok = om.greedy([tok], False, 1.0)
+    m.free()
+    om.close()
+
+
+def test_step_tail_form_other_shape(g2):
+    """The tail form that reads the model shape from its arguments
+    (g2k_step_f16_tailn: XL width, 4096-token vocabulary), two layers:
+    prefill and teacher-forced decode logits at positions 300..315 against
+    the oracle."""
+    cfg = g2.make_config(2, 1600, 25, vocab_size=4096)
+    w = g2.synth_weights(cfg, SEED, f16_round=True)
+    om = oracle.Model(cfg, w, kslice=4)
+    m = g2.Model.from_host(cfg, w, g2.F16, g2.PATH_FUSED)
+    assert m.step_kernel() == "g2k_step_f16_tailn"
+    P = 300
+    prompt = random_prompt(P, cfg.vocab_size, 78)
+    print(f"[step] tail form, vocab {cfg.vocab_size}, prompt {P}", flush=True)
+    om.prefill(prompt)
+    m.prefill(prompt)
+    _check(m.logits(), om.logits())
+    tok = om.greedy(prompt, False, 1.0)
+    for k in range(16):
+        om.decode(tok, P + k)
+        m.decode(tok, P + k)
         _check(m.logits(), om.logits())
         tok = om.greedy([tok], False, 1.0)
     m.free()
