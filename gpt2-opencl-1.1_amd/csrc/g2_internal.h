@@ -61,6 +61,10 @@ extern "C" {
     X(STEP_F32T_TR, "g2k_step_f32_tail_trace")                                \
     X(STEP_F16T_TR, "g2k_step_f16_tail_trace")                                \
     X(STEP_F16TN, "g2k_step_f16_tailn")                                       \
+    X(STEP_F32_E768, "g2k_step_f32_e768")                                     \
+    X(STEP_F32_E1024, "g2k_step_f32_e1024")                                   \
+    X(STEP_F32_E1280, "g2k_step_f32_e1280")                                   \
+    X(STEP_F16_E1280, "g2k_step_f16_e1280")                                   \
     X(STEP_F16TN_TR, "g2k_step_f16_tailn_trace")                              \
     X(HGEMM_STORE, "g2k_hgemm_store") X(HGEMM_GELU, "g2k_hgemm_gelu")         \
     X(HGEMM_RESID, "g2k_hgemm_resid") X(HGEMM_QKV, "g2k_hgemm_qkv")           \

@@ -782,16 +782,17 @@ static int fused_step_launches(g2_model *m)
 static int step_fid(const g2_model *m)
 {
     const g2_config *c = &m->cfg;
-    const int VE = m->dtype == G2_F16 ? 8 : 4;
+    const int VE = m->dtype == G2_F16 ? 8 : 4, f16 = m->dtype == G2_F16;
     const int tail = g2p_step_tail(c->n_embd, c->ffn_dim, VE);
-    /* the fp16 tail form compiled for GPT-2 XL's shape, else the one that
-     * reads the shape from its arguments */
-    const int xl = tail && g2p_step_xl_shape(c->n_embd, c->ffn_dim, c->n_head, c->vocab_size, VE);
+    /* the kernels compiled for a GPT-2 shape (g2p_step_shape), else the
+     * ones that read the shape from their arguments */
+    const int sh = g2p_step_shape(c->n_embd, c->ffn_dim, c->n_head, c->vocab_size);
     if (m->trace) /* the variants with the phase timestamps */
-        return m->dtype == G2_F16 ? (tail ? (xl ? G2F_STEP_F16T_TR : G2F_STEP_F16TN_TR) : G2F_STEP_F16_TR)
-                                  : (tail ? G2F_STEP_F32T_TR : G2F_STEP_F32_TR);
-    return m->dtype == G2_F16 ? (tail ? (xl ? G2F_STEP_F16T : G2F_STEP_F16TN) : G2F_STEP_F16)
-                              : (tail ? G2F_STEP_F32T : G2F_STEP_F32);
+        return f16 ? (tail ? (sh == G2P_SHAPE_XL ? G2F_STEP_F16T_TR : G2F_STEP_F16TN_TR) : G2F_STEP_F16_TR)
+                   : (tail ? G2F_STEP_F32T_TR : G2F_STEP_F32_TR);
+    if (tail) return f16 ? (sh == G2P_SHAPE_XL ? G2F_STEP_F16T : G2F_STEP_F16TN) : G2F_STEP_F32T;
+    if (f16) return sh == 3 ? G2F_STEP_F16_E1280 : G2F_STEP_F16;
+    return sh == 1 ? G2F_STEP_F32_E768 : (sh == 2 ? G2F_STEP_F32_E1024 : (sh == 3 ? G2F_STEP_F32_E1280 : G2F_STEP_F32));
 }
 
 /* One decode forward at state[POS] as one cooperative launch of the

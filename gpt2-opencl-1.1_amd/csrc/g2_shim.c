@@ -187,11 +187,12 @@ int g2_init(int device)
      * them co-resident: require cooperative launch support and an occupancy
      * of at least one work-group per CU for both weight types. */
     {
-        enum { NSTEP = 10 };
+        enum { NSTEP = 14 };
         int coop = 0, nb[NSTEP];
         hipError_t ea = hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, device);
         hipError_t eo[NSTEP];
         const int fids[NSTEP] = { G2F_STEP_F32, G2F_STEP_F16, G2F_STEP_F32T, G2F_STEP_F16T, G2F_STEP_F16TN,
+                                  G2F_STEP_F32_E768, G2F_STEP_F32_E1024, G2F_STEP_F32_E1280, G2F_STEP_F16_E1280,
                                   G2F_STEP_F32_TR, G2F_STEP_F16_TR, G2F_STEP_F32T_TR, G2F_STEP_F16T_TR,
                                   G2F_STEP_F16TN_TR };
         int ok = ea == hipSuccess && coop;

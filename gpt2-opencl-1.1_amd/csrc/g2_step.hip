@@ -469,15 +469,15 @@ __device__ __forceinline__ g2p_rows row_plan(const g2_step_args &a, int k)
 }
 
 /* row_plan with the fields that depend only on the matrix shape (chunks
- * per row, segments, segment length, tail) computed from XL's sizes, so the
- * compiler folds them; the work-group's rows and units still come from the
- * table. */
-template <bool XL>
+ * per row, segments, segment length, tail) computed from the sizes of
+ * shape SH, so the compiler folds them; the work-group's rows and units
+ * still come from the table. */
+template <typename WT, int SH>
 __device__ __forceinline__ g2p_rows row_plan_x(const g2_step_args &a, int k)
 {
     g2p_rows p = row_plan(a, k);
-    if constexpr (XL) {
-        const g2p_rows s = g2p_rows_plan(1, k == G2P_SH_FC2 ? G2P_XL_F : G2P_XL_E, 8, 0, 1);
+    if constexpr (SH != 0) {
+        const g2p_rows s = g2p_rows_plan(1, k == G2P_SH_FC2 ? G2P_SHAPE_F(SH) : G2P_SHAPE_E(SH), chunk_t<WT>::V, 0, 1);
         p.C = s.C;
         p.lseg = s.lseg;
         p.nseg = s.nseg;
@@ -996,7 +996,7 @@ __device__ __forceinline__ void lm_pick(const g2_step_args &a, const ctx &c, con
     TRACE(2);
 }
 
-template <typename WT, bool TAIL, bool TRACED, bool XL>
+template <typename WT, bool TAIL, bool TRACED, int SH>
 __device__ __forceinline__ void step_impl(const g2_step_args &a)
 {
     /* 16-byte alignment: the dot products read 16-byte chunks of these */
@@ -1017,18 +1017,18 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     constexpr int NQE = (G2_STEP_MAXE + 4 * NT - 1) / (4 * NT);    /* its value quads      */
     constexpr int NPM2 = (G2_STEP_MAXCH * 66 + 2 * NT - 1) / (2 * NT); /* a head's partials, in pairs */
     const int wg = blockIdx.x, nwg = gridDim.x;
-    /* XL: the sizes of the shape this kernel is compiled for (the host
-     * launches it only for that shape; a launch with others does nothing
-     * but report it) */
-    const int E = XL ? G2P_XL_E : a.E, F = XL ? G2P_XL_F : a.F, NH = XL ? G2P_XL_NH : a.NH;
-    const int S = XL ? G2_KV_MAX_SEQ : a.S, V = XL ? G2P_XL_V : a.V;
+    /* SH: the sizes of the model shape this kernel is compiled for (the
+     * host launches it only for that shape; a launch with others does
+     * nothing but report it) */
+    const int E = SH ? G2P_SHAPE_E(SH) : a.E, F = SH ? G2P_SHAPE_F(SH) : a.F, NH = SH ? G2P_SHAPE_NH(SH) : a.NH;
+    const int S = SH ? G2_KV_MAX_SEQ : a.S, V = SH ? G2P_SHAPE_V : a.V;
     const int pos = clampi(a.state[G2S_POS], 0, S - 1);
     const int tok = clampi(a.state[G2S_TOK], 0, V - 1);
     const unsigned seq = (unsigned)a.state[G2S_SEQ];
     /* the row-plan table was built for another grid, or the shape is not
      * the one this kernel is compiled for: do nothing (every work-group
      * returns here) and report it */
-    if (a.nshares != nwg || (XL && (a.E != E || a.F != F || a.NH != NH || a.S != S || a.V != V))) {
+    if (a.nshares != nwg || (SH && (a.E != E || a.F != F || a.NH != NH || a.S != S || a.V != V))) {
         if (wg == 0 && threadIdx.x == 0) atomicOr(a.state + G2S_ERR, G2_ERR_STEP_ARGS);
         return;
     }
@@ -1056,7 +1056,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     constexpr int VE = chunk_t<WT>::V;
     int xeo[1], xfo[QMAX];
     {
-        const g2p_rows pq = row_plan_x<XL>(a, G2P_SH_QKV), p2 = row_plan_x<XL>(a, G2P_SH_FC2);
+        const g2p_rows pq = row_plan_x<WT, SH>(a, G2P_SH_QKV), p2 = row_plan_x<WT, SH>(a, G2P_SH_FC2);
         xeo[0] = g2p_x_slot(&pq, VE, 4 * min((int)threadIdx.x, E / 4 - 1));
 #pragma unroll
         for (int i = 0; i < QMAX; ++i) xfo[i] = g2p_x_slot(&p2, VE, 4 * min((int)threadIdx.x + NT * i, F / 4 - 1));
@@ -1076,8 +1076,8 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             if (a.plain && !(a.plain == 2 && wg == 1))
                 ll_put(a.xbuf + G2X_ARRIVE(a.L, a.xlayer, nwg) + wg, 0.f, c.tag);
         }
-        load_set<UMAX, TAIL>(tid, wa, make_plan(LT0->qkv_w, row_plan_x<XL>(a, G2P_SH_QKV)), 0);
-        if (wg >= NH) load_set<UPROJ, TAIL>(tid, wp, make_plan(LT0->proj_w, row_plan_x<XL>(a, G2P_SH_PROJ)), 0);
+        load_set<UMAX, TAIL>(tid, wa, make_plan(LT0->qkv_w, row_plan_x<WT, SH>(a, G2P_SH_QKV)), 0);
+        if (wg >= NH) load_set<UPROJ, TAIL>(tid, wp, make_plan(LT0->proj_w, row_plan_x<WT, SH>(a, G2P_SH_PROJ)), 0);
         /* the padded matrix inputs: zero everywhere (the fetches write only
          * the data positions) */
         for (int q = tid; q < G2P_XE_FLOATS / 4; q += NT) *(f32x4 *)(xe + 4 * q) = (f32x4){0.f, 0.f, 0.f, 0.f};
@@ -1107,7 +1107,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             const int tid = fresh_tid();
             TRACE(0);
             const G2_CONST g2_step_layer *y = layer();
-            const plan p = make_plan(y->qkv_w, row_plan_x<XL>(a, G2P_SH_QKV));
+            const plan p = make_plan(y->qkv_w, row_plan_x<WT, SH>(a, G2P_SH_QKV));
             const f32x4 g = ln_gload(tid, y->ln1_w, E);
             const int rq = min(p.r0 + tid, 3 * E - 1); /* used by tid < nrows */
             const float c1 = gl(y->qkv_c1)[rq], c2 = gl(y->qkv_c2)[rq];
@@ -1159,7 +1159,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
             TRACE(3);
             /* the fc rows stream from here on; a work-group that merges a head
              * issues them after its merge, so its merge waits behind nothing */
-            if (wg >= NH) load_set<UMAX, TAIL>(tid, wa, make_plan(y->fc_w, row_plan_x<XL>(a, G2P_SH_FC)), 0);
+            if (wg >= NH) load_set<UMAX, TAIL>(tid, wa, make_plan(y->fc_w, row_plan_x<WT, SH>(a, G2P_SH_FC)), 0);
         }
 
         /* ---- MERGE: head h by work-group h (g2k_attn_merge) */
@@ -1184,7 +1184,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         {
             const int tid = fresh_tid();
             TRACE(16);
-            if (wg < NH) load_set<UMAX, TAIL>(tid, wa, make_plan(layer()->fc_w, row_plan_x<XL>(a, G2P_SH_FC)), 0);
+            if (wg < NH) load_set<UMAX, TAIL>(tid, wa, make_plan(layer()->fc_w, row_plan_x<WT, SH>(a, G2P_SH_FC)), 0);
             TRACE(4);
         }
 
@@ -1196,7 +1196,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         } else {
             const int tid = fresh_tid();
             const G2_CONST g2_step_layer *y = layer();
-            const plan p = make_plan(y->proj_w, row_plan_x<XL>(a, G2P_SH_PROJ));
+            const plan p = make_plan(y->proj_w, row_plan_x<WT, SH>(a, G2P_SH_PROJ));
             const float bias = gl(y->proj_b)[min(p.r0 + tid, E - 1)];
             fetch4<NQE>(tid, c, RV + G2V_O(E), E, NH, xe, xeo, (lds_flag *)&flag);
             TRACE(5);
@@ -1208,7 +1208,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 vput(RV + G2V_X1(E) + r, RN + G2V_X1(E) + r, v + xres[r]);
             }
             TRACE(6);
-            if (l + 1 < a.L) load_set<UPROJ, TAIL>(tid, wp, make_plan(LT[l + 1].proj_w, row_plan_x<XL>(a, G2P_SH_PROJ)), 0);
+            if (l + 1 < a.L) load_set<UPROJ, TAIL>(tid, wp, make_plan(LT[l + 1].proj_w, row_plan_x<WT, SH>(a, G2P_SH_PROJ)), 0);
             __syncthreads();
         }
 
@@ -1216,7 +1216,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         {
             const int tid = fresh_tid();
             const G2_CONST g2_step_layer *y = layer();
-            const plan p = make_plan(y->fc_w, row_plan_x<XL>(a, G2P_SH_FC));
+            const plan p = make_plan(y->fc_w, row_plan_x<WT, SH>(a, G2P_SH_FC));
             const f32x4 g = ln_gload(tid, y->ln2_w, E);
             const int rf = min(p.r0 + tid, F - 1); /* used by tid < nrows */
             const float c1 = gl(y->fc_c1)[rf], c2 = gl(y->fc_c2)[rf];
@@ -1234,7 +1234,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 vput(RV + G2V_H(E) + r, RN + G2V_H(E) + r, gelu_f(v));
             }
             TRACE(8);
-            load_set<UMAX, TAIL>(tid, wa, make_plan(y->fc2_w, row_plan_x<XL>(a, G2P_SH_FC2)), 0);
+            load_set<UMAX, TAIL>(tid, wa, make_plan(y->fc2_w, row_plan_x<WT, SH>(a, G2P_SH_FC2)), 0);
             __syncthreads();
         }
 
@@ -1242,7 +1242,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
         {
             const int tid = fresh_tid();
             const G2_CONST g2_step_layer *y = layer();
-            const plan p = make_plan(y->fc2_w, row_plan_x<XL>(a, G2P_SH_FC2));
+            const plan p = make_plan(y->fc2_w, row_plan_x<WT, SH>(a, G2P_SH_FC2));
             const float bias = gl(y->fc2_b)[min(p.r0 + tid, E - 1)];
             fetch4<QMAX>(tid, c, RV + G2V_H(E), F, nwg, xf, xfo, (lds_flag *)&flag);
             TRACE(9);
@@ -1255,63 +1255,83 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 vput(RV + G2V_X2(E, F) + r, RN + G2V_X2(E, F) + r, v + xres[r]);
             }
             TRACE(10);
-            if (l + 1 < a.L) load_set<UMAX, TAIL>(tid, wa, make_plan(LT[l + 1].qkv_w, row_plan_x<XL>(a, G2P_SH_QKV)), 0);
-            else load_set<UMAX, TAIL>(tid, wa, make_plan(a.lm_w, row_plan_x<XL>(a, G2P_SH_LM)), 0);
+            if (l + 1 < a.L) load_set<UMAX, TAIL>(tid, wa, make_plan(LT[l + 1].qkv_w, row_plan_x<WT, SH>(a, G2P_SH_QKV)), 0);
+            else load_set<UMAX, TAIL>(tid, wa, make_plan(a.lm_w, row_plan_x<WT, SH>(a, G2P_SH_LM)), 0);
             __syncthreads();
         }
     }
 
     /* the first batch of lm_head rows was loaded by the last fc2 phase */
-    lm_pick<WT, TAIL, TRACED>(a, c, row_plan_x<XL>(a, G2P_SH_LM), XV + 2 * VR * (a.L - 1) + G2V_X2(E, F), X + (size_t)a.L * a.xlayer, wa, true,
+    lm_pick<WT, TAIL, TRACED>(a, c, row_plan_x<WT, SH>(a, G2P_SH_LM), XV + 2 * VR * (a.L - 1) + G2V_X2(E, F), X + (size_t)a.L * a.xlayer, wa, true,
                 xres, xe, xeo[0], xsc, part, red, amv, ami, (lds_flag *)&flag);
 }
 
 } /* namespace g2step */
 
+/* The plain form with the model shape from the arguments, and compiled for
+ * the GPT-2 shapes of the benchmark configurations (g2p_step_shape: small,
+ * medium and large with fp32 weights, large with fp16 weights). */
 extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f32(const g2_step_args a)
 {
-    g2step::step_impl<float, false, false, false>(a);
+    g2step::step_impl<float, false, false, 0>(a);
 }
 extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f16(const g2_step_args a)
 {
-    g2step::step_impl<_Float16, false, false, false>(a);
+    g2step::step_impl<_Float16, false, false, 0>(a);
+}
+extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f32_e768(const g2_step_args a)
+{
+    g2step::step_impl<float, false, false, 1>(a);
+}
+extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f32_e1024(const g2_step_args a)
+{
+    g2step::step_impl<float, false, false, 2>(a);
+}
+extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f32_e1280(const g2_step_args a)
+{
+    g2step::step_impl<float, false, false, 3>(a);
+}
+extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f16_e1280(const g2_step_args a)
+{
+    g2step::step_impl<_Float16, false, false, 3>(a);
 }
 /* The tail form, for models whose every four-unit plan is a tail plan
  * (g2p_step_tail: n_embd 1600, the rows of every matrix 200 chunks per
- * segment).  g2k_step_f16_tail is compiled for GPT-2 XL's shape
- * (g2p_step_xl_shape); g2k_step_f16_tailn takes the shape from its
+ * segment).  g2k_step_f16_tail is compiled for GPT-2 XL's shape;
+ * g2k_step_f16_tailn and g2k_step_f32_tail take the shape from their
  * arguments. */
 extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f32_tail(const g2_step_args a)
 {
-    g2step::step_impl<float, true, false, false>(a);
+    g2step::step_impl<float, true, false, 0>(a);
 }
 extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f16_tail(const g2_step_args a)
 {
-    g2step::step_impl<_Float16, true, false, true>(a);
+    g2step::step_impl<_Float16, true, false, G2P_SHAPE_XL>(a);
 }
 extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f16_tailn(const g2_step_args a)
 {
-    g2step::step_impl<_Float16, true, false, false>(a);
+    g2step::step_impl<_Float16, true, false, 0>(a);
 }
 /* The same with the phase timestamps of g2_step_args.trace (launched
- * instead of them when a trace buffer is set). */
+ * instead of them when a trace buffer is set; shape from the arguments,
+ * except the XL tail form). */
 extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f32_trace(const g2_step_args a)
 {
-    g2step::step_impl<float, false, true, false>(a);
+    g2step::step_impl<float, false, true, 0>(a);
 }
 extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f16_trace(const g2_step_args a)
 {
-    g2step::step_impl<_Float16, false, true, false>(a);
+    g2step::step_impl<_Float16, false, true, 0>(a);
 }
 extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f32_tail_trace(const g2_step_args a)
 {
-    g2step::step_impl<float, true, true, false>(a);
+    g2step::step_impl<float, true, true, 0>(a);
 }
 extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f16_tail_trace(const g2_step_args a)
 {
-    g2step::step_impl<_Float16, true, true, true>(a);
+    g2step::step_impl<_Float16, true, true, G2P_SHAPE_XL>(a);
 }
 extern "C" __global__ __launch_bounds__(G2_STEP_THREADS) void g2k_step_f16_tailn_trace(const g2_step_args a)
 {
-    g2step::step_impl<_Float16, true, true, false>(a);
+    g2step::step_impl<_Float16, true, true, 0>(a);
 }

@@ -184,17 +184,20 @@ G2P_FN int g2p_step_tail(int E, int F, int VE)
     return g2p_rows_plan(1, E, VE, 0, 1).tail && g2p_rows_plan(1, F, VE, 0, 1).tail;
 }
 
-/* The model shape the fp16 tail-form step kernel is compiled for (GPT-2 XL:
- * n_embd 1600, ffn 6400, 25 heads, vocabulary 50257): that kernel folds
- * these sizes and the plans' per-matrix fields at compile time; other tail
- * shapes run the form that reads them from its arguments. */
-#define G2P_XL_E 1600
-#define G2P_XL_F 6400
-#define G2P_XL_NH 25
-#define G2P_XL_V 50257
-G2P_FN int g2p_step_xl_shape(int E, int F, int NH, int V, int VE)
+/* GPT-2 model shapes the step kernel is also compiled for, with the sizes
+ * and the plans' per-matrix fields folded at compile time (id 1..4: small,
+ * medium, large, XL: n_embd 768, 1024, 1280, 1600, ffn 4 n_embd, 64-dim
+ * heads, vocabulary 50257); id 0: sizes read from the kernel arguments. */
+#define G2P_SHAPE_E(id) ((id) == 1 ? 768 : (id) == 2 ? 1024 : (id) == 3 ? 1280 : (id) == 4 ? 1600 : 0)
+#define G2P_SHAPE_F(id) (4 * G2P_SHAPE_E(id))
+#define G2P_SHAPE_NH(id) (G2P_SHAPE_E(id) / 64)
+#define G2P_SHAPE_V 50257
+#define G2P_SHAPE_XL 4
+G2P_FN int g2p_step_shape(int E, int F, int NH, int V)
 {
-    return VE == 8 && E == G2P_XL_E && F == G2P_XL_F && NH == G2P_XL_NH && V == G2P_XL_V;
+    for (int id = 1; id <= 4; ++id)
+        if (E == G2P_SHAPE_E(id) && F == G2P_SHAPE_F(id) && NH == G2P_SHAPE_NH(id) && V == G2P_SHAPE_V) return id;
+    return 0;
 }
 
 /* Attention unit (head h, 64-position chunk ch) by the 256 threads of one

@@ -228,19 +228,20 @@ int main(int argc, char **argv)
         same_plan("fc row plan", shp[G2P_SH_FC], g2p_rows_plan(F, E, VE, wg, nwg));
         same_plan("fc2 row plan", shp[G2P_SH_FC2], g2p_rows_plan(E, F, VE, wg, nwg));
         same_plan("lm_head row plan", shp[G2P_SH_LM], g2p_rows_plan(V, E, VE, wg, nwg));
-        /* the XL-shape kernel folds each plan's shape fields from
-         * g2p_rows_plan(1, K, 8, 0, 1) and takes only rows and units from the
-         * table: the two must agree */
-        if (g2p_step_xl_shape(E, F, NH, V, VE))
+        /* a kernel compiled for a GPT-2 shape (g2p_step_shape) folds each
+         * plan's shape fields from g2p_rows_plan(1, K, VE, 0, 1) of that
+         * shape's sizes and takes only rows and units from the table: the
+         * two must agree */
+        if (const int sh = g2p_step_shape(E, F, NH, V))
             for (int k = 0; k < G2P_NSHARES; ++k) {
                 g2p_rows f = shp[k];
-                const g2p_rows c = g2p_rows_plan(1, k == G2P_SH_FC2 ? G2P_XL_F : G2P_XL_E, 8, 0, 1);
+                const g2p_rows c = g2p_rows_plan(1, k == G2P_SH_FC2 ? G2P_SHAPE_F(sh) : G2P_SHAPE_E(sh), VE, 0, 1);
                 f.C = c.C;
                 f.lseg = c.lseg;
                 f.nseg = c.nseg;
                 f.SL = c.SL;
                 f.tail = c.tail;
-                same_plan("XL-shape folded plan fields", f, shp[k]);
+                same_plan("folded plan fields of a GPT-2 shape", f, shp[k]);
             }
         /* embedding of the token at pos, LayerNorm parameters */
         for (int tid = 0; tid < NT; ++tid) {

@@ -43,14 +43,20 @@ def test_step_kernel_names(g2):
     profile by): the tail form when every matrix row splits into segments
     of 193..208 16-byte chunks (GPT-2 XL: rows of n_embd 1600 or ffn 6400
     inputs split into segments of 200 chunks, in fp16 and in fp32), the
-    plain form otherwise, none with the per-operator kernels.  The fp16
-    tail form is compiled for GPT-2 XL's exact shape (g2k_step_f16_tail);
-    another tail shape (here XL width with a smaller vocabulary) runs the
-    form that reads the shape from its arguments (g2k_step_f16_tailn)."""
+    plain form otherwise, none with the per-operator kernels.  The kernels
+    of the benchmark configurations are compiled for their GPT-2 shapes
+    (fp16 tail form for XL: g2k_step_f16_tail; plain form for small,
+    medium and large in fp32 and large in fp16: g2k_step_<w>_e<n_embd>);
+    other shapes (here XL width with a smaller vocabulary, and a small
+    custom model) run the forms that read the shape from their arguments
+    (g2k_step_f16_tailn, g2k_step_f32, g2k_step_f16)."""
     cases = [("xl", g2.F16, "g2k_step_f16_tail"), ("xl", g2.F32, "g2k_step_f32_tail"),
-             ("large", g2.F16, "g2k_step_f16"), ("large", g2.F32, "g2k_step_f32"),
-             ("small", g2.F32, "g2k_step_f32"), ("medium", g2.F32, "g2k_step_f32"),
-             (g2.make_config(2, 1600, 25, vocab_size=4096), g2.F16, "g2k_step_f16_tailn")]
+             ("large", g2.F16, "g2k_step_f16_e1280"), ("large", g2.F32, "g2k_step_f32_e1280"),
+             ("small", g2.F32, "g2k_step_f32_e768"), ("medium", g2.F32, "g2k_step_f32_e1024"),
+             ("small", g2.F16, "g2k_step_f16"),
+             (g2.make_config(2, 1600, 25, vocab_size=4096), g2.F16, "g2k_step_f16_tailn"),
+             (g2.make_config(2, 256, 4, vocab_size=1000), g2.F32, "g2k_step_f32"),
+             (g2.make_config(2, 256, 4, vocab_size=1000), g2.F16, "g2k_step_f16")]
     for preset, dtype, name in cases:
         cfg = g2.preset(preset) if isinstance(preset, str) else preset
         m = g2.Model.synth(cfg, SEED, dtype, g2.PATH_FUSED)
