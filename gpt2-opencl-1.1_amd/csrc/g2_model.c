@@ -786,7 +786,7 @@ static int step_fid(const g2_model *m)
     const int tail = g2p_step_tail(c->n_embd, c->ffn_dim, VE);
     /* the kernels compiled for a GPT-2 shape (g2p_step_shape), else the
      * ones that read the shape from their arguments */
-    const int sh = g2p_step_shape(c->n_embd, c->ffn_dim, c->n_head, c->vocab_size);
+    const int sh = g2p_step_shape(c->n_embd, c->ffn_dim, c->n_head, c->vocab_size, m->step_wgs);
     if (m->trace) /* the variants with the phase timestamps */
         return f16 ? (tail ? (sh == G2P_SHAPE_XL ? G2F_STEP_F16T_TR : G2F_STEP_F16TN_TR) : G2F_STEP_F16_TR)
                    : (tail ? G2F_STEP_F32T_TR : G2F_STEP_F32_TR);

@@ -475,16 +475,22 @@ __device__ __forceinline__ g2p_rows row_plan(const g2_step_args &a, int k)
 template <typename WT, int SH>
 __device__ __forceinline__ g2p_rows row_plan_x(const g2_step_args &a, int k)
 {
-    g2p_rows p = row_plan(a, k);
     if constexpr (SH != 0) {
-        const g2p_rows s = g2p_rows_plan(1, k == G2P_SH_FC2 ? G2P_SHAPE_F(SH) : G2P_SHAPE_E(SH), chunk_t<WT>::V, 0, 1);
-        p.C = s.C;
-        p.lseg = s.lseg;
-        p.nseg = s.nseg;
-        p.SL = s.SL;
-        p.tail = s.tail;
+        /* computed from the shape's sizes and the 256-work-group grid (the
+         * kernel refuses another), with the work-group index made opaque to
+         * the compiler so the plan is recomputed where it is used */
+        int w = (int)blockIdx.x;
+        asm volatile("" : "+s"(w));
+        constexpr int E = G2P_SHAPE_E(SH), F = G2P_SHAPE_F(SH), NH = G2P_SHAPE_NH(SH), V = G2P_SHAPE_V;
+        constexpr int VE = chunk_t<WT>::V, NWG = G2P_SHAPE_WGS;
+        if (k == G2P_SH_QKV) return g2p_rows_plan(3 * E, E, VE, w, NWG);
+        if (k == G2P_SH_PROJ) return g2p_proj_plan(E, VE, NH, w, NWG);
+        if (k == G2P_SH_FC) return g2p_rows_plan(F, E, VE, w, NWG);
+        if (k == G2P_SH_FC2) return g2p_rows_plan(E, F, VE, w, NWG);
+        return g2p_rows_plan(V, E, VE, w, NWG);
+    } else {
+        return row_plan(a, k);
     }
-    return p;
 }
 
 __device__ __forceinline__ plan make_plan(const void *W, const g2p_rows &r)
@@ -1028,7 +1034,7 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
     /* the row-plan table was built for another grid, or the shape is not
      * the one this kernel is compiled for: do nothing (every work-group
      * returns here) and report it */
-    if (a.nshares != nwg || (SH && (a.E != E || a.F != F || a.NH != NH || a.S != S || a.V != V))) {
+    if (a.nshares != nwg || (SH && (a.E != E || a.F != F || a.NH != NH || a.S != S || a.V != V || nwg != G2P_SHAPE_WGS))) {
         if (wg == 0 && threadIdx.x == 0) atomicOr(a.state + G2S_ERR, G2_ERR_STEP_ARGS);
         return;
     }

@@ -193,8 +193,12 @@ G2P_FN int g2p_step_tail(int E, int F, int VE)
 #define G2P_SHAPE_NH(id) (G2P_SHAPE_E(id) / 64)
 #define G2P_SHAPE_V 50257
 #define G2P_SHAPE_XL 4
-G2P_FN int g2p_step_shape(int E, int F, int NH, int V)
+/* ... and for a grid of 256 work-groups (one per CU of an MI355X): their
+ * row plans are computed in the kernel from these constants */
+#define G2P_SHAPE_WGS 256
+G2P_FN int g2p_step_shape(int E, int F, int NH, int V, int nwg)
 {
+    if (nwg != G2P_SHAPE_WGS) return 0;
     for (int id = 1; id <= 4; ++id)
         if (E == G2P_SHAPE_E(id) && F == G2P_SHAPE_F(id) && NH == G2P_SHAPE_NH(id) && V == G2P_SHAPE_V) return id;
     return 0;

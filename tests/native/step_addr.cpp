@@ -228,21 +228,18 @@ int main(int argc, char **argv)
         same_plan("fc row plan", shp[G2P_SH_FC], g2p_rows_plan(F, E, VE, wg, nwg));
         same_plan("fc2 row plan", shp[G2P_SH_FC2], g2p_rows_plan(E, F, VE, wg, nwg));
         same_plan("lm_head row plan", shp[G2P_SH_LM], g2p_rows_plan(V, E, VE, wg, nwg));
-        /* a kernel compiled for a GPT-2 shape (g2p_step_shape) folds each
-         * plan's shape fields from g2p_rows_plan(1, K, VE, 0, 1) of that
-         * shape's sizes and takes only rows and units from the table: the
-         * two must agree */
-        if (const int sh = g2p_step_shape(E, F, NH, V))
-            for (int k = 0; k < G2P_NSHARES; ++k) {
-                g2p_rows f = shp[k];
-                const g2p_rows c = g2p_rows_plan(1, k == G2P_SH_FC2 ? G2P_SHAPE_F(sh) : G2P_SHAPE_E(sh), VE, 0, 1);
-                f.C = c.C;
-                f.lseg = c.lseg;
-                f.nseg = c.nseg;
-                f.SL = c.SL;
-                f.tail = c.tail;
-                same_plan("folded plan fields of a GPT-2 shape", f, shp[k]);
-            }
+        /* a kernel compiled for a GPT-2 shape (g2p_step_shape) computes each
+         * plan from the shape's constant sizes and the 256-work-group grid
+         * instead of reading the table: its plans must be the table's (which
+         * this walk checks the addresses of) */
+        if (const int sh = g2p_step_shape(E, F, NH, V, nwg)) {
+            const int Es = G2P_SHAPE_E(sh), Fs = G2P_SHAPE_F(sh), NHs = G2P_SHAPE_NH(sh), Vs = G2P_SHAPE_V;
+            const g2p_rows c[G2P_NSHARES] = {
+                g2p_rows_plan(3 * Es, Es, VE, wg, G2P_SHAPE_WGS), g2p_proj_plan(Es, VE, NHs, wg, G2P_SHAPE_WGS),
+                g2p_rows_plan(Fs, Es, VE, wg, G2P_SHAPE_WGS), g2p_rows_plan(Es, Fs, VE, wg, G2P_SHAPE_WGS),
+                g2p_rows_plan(Vs, Es, VE, wg, G2P_SHAPE_WGS) };
+            for (int k = 0; k < G2P_NSHARES; ++k) same_plan("plan computed by a shape-compiled kernel", c[k], shp[k]);
+        }
         /* embedding of the token at pos, LayerNorm parameters */
         for (int tid = 0; tid < NT; ++tid) {
             for (int d = tid; d < E; d += NT) {
