@@ -671,8 +671,9 @@ __device__ __forceinline__ float xsum4(float a, float b, float c, float d)
 }
 
 /* Cached keys and values of one 64-position chunk, loaded into registers
- * ahead of their use (they do not depend on this position's q): the keys
- * before the q/k/v wait (attn_load), the values after it (attn_load_v).
+ * ahead of their use (they do not depend on this position's q), both
+ * before the q/k/v wait: the keys (attn_load), then the values
+ * (attn_load_v).
  * Scores: thread (pq = t%16, dg = t/16) of a half takes positions
  * j0+4pq..+3 and dims 4dg..+3 (four 16-byte loads of the transposed K
  * cache); weighted sum: thread (d4 = t%16, jg = t/16) takes dims 4d4..+3
@@ -705,8 +706,10 @@ __device__ __forceinline__ void attn_load(int tid, const G2_CONST g2_step_layer 
     for (int d = 0; d < 4; ++d) r.kv[d] = kb[(size_t)d * kstr];
 }
 /* The values of the same chunk (needed only after the scores and the
- * softmax): issued once the unit's q/k/v have arrived, so the q/k/v reads
- * queue behind the keys only. */
+ * softmax).  Issued behind the keys and ahead of the q/k/v wait: the q/k/v
+ * reads then queue behind both, which costs nothing measurable at
+ * E = 1600 and takes the value latency off the layer's attention chain at
+ * E = 768..1280, where a work-group has few units. */
 __device__ __forceinline__ void attn_load_v(int tid, const G2_CONST g2_step_layer *y, att_regs &r, bool on, int h,
                                             int ch, int E, int S)
 {
@@ -799,8 +802,8 @@ __device__ __forceinline__ void attn_compute(int tid, const ctx &c, float scale,
  * `on` is false for a half without a unit; it still takes part in the
  * barriers. */
 __device__ __forceinline__ void attn_chunk(int tid, const ctx &c, float scale, const u64 *src, int qo,
-                                           int ko, int vo, u64 *pout, att_lds &L, att_regs &r, bool on,
-                                           int ch, int pos, int T, const G2_CONST g2_step_layer *y, int h, int E, int S)
+                                           int ko, int vo, u64 *pout, att_lds &L, const att_regs &r, bool on,
+                                           int ch, int pos, int T)
 {
     const int t = tid & 255;
     /* q, k and v of the head at this position: src[qo + d], src[ko + d],
@@ -817,7 +820,6 @@ __device__ __forceinline__ void attn_chunk(int tid, const ctx &c, float scale, c
         dst[d + 1] = __uint_as_float(v[0].z);
     }
     __syncthreads();
-    attn_load_v(tid, y, r, on, h, ch, E, S);
     attn_compute(tid, c, scale, pout, L, r, on, ch, pos, T);
 }
 
@@ -1157,9 +1159,10 @@ __device__ __forceinline__ void step_impl(const g2_step_args &a)
                 const bool on = u < nunits;
                 const int h = on ? u / nch : 0, ch = on ? u % nch : 0;
                 attn_load(tid, y, ar[0], on, h, ch, pos, T, E, S);
+                attn_load_v(tid, y, ar[0], on, h, ch, E, S);
                 attn_chunk(tid, c, a.scale * 1.4426950408889634f, R, h * 64, E + h * 64, 2 * E + h * 64,
                                   R + G2X_ATT(E) + ((size_t)h * G2_STEP_MAXCH + ch) * 66, att[hf], ar[0],
-                                  on, ch, pos, T, y, h, E, S);
+                                  on, ch, pos, T);
                 __syncthreads();
             }
             TRACE(3);
