@@ -213,9 +213,13 @@ G2K void g2k_reduce(const g2_reduce_args a)
  * hi = fp16(v), lo = fp16(v - hi), both round-to-nearest-even. */
 __device__ __forceinline__ void split_store(uint16_t *hi, uint16_t *lo, size_t i, float v)
 {
-    /* v is the rounded fp32 value (no fusing of the producer's last product
-     * into v - hi), exactly what a consumer splitting the stored fp32 sees */
+    /* v is the rounded fp32 value, exactly what a consumer splitting the
+     * stored fp32 sees: the register barrier keeps the producer's last
+     * operation out of the conversions (a product would otherwise be
+     * rounded to fp16 once, by v_fma_mixlo_f16, instead of to fp32 first),
+     * and contract(off) keeps it out of v - hi */
 #pragma clang fp contract(off)
+    asm volatile("" : "+v"(v));
     const _Float16 h = (_Float16)v;
     const _Float16 l = (_Float16)(v - (float)h);
     hi[i] = __builtin_bit_cast(uint16_t, h);
@@ -237,7 +241,9 @@ __device__ __forceinline__ _Float16 lo16(float v)
  * the scalar conversion on 4M values down to fp16 subnormals). */
 __device__ __forceinline__ void split2(float a, float b, unsigned &h, unsigned &l)
 {
+    /* a, b rounded to fp32 before the conversions, as in split_store */
 #pragma clang fp contract(off)
+    asm volatile("" : "+v"(a), "+v"(b));
     typedef float f2 __attribute__((ext_vector_type(2)));
     typedef _Float16 h2 __attribute__((ext_vector_type(2)));
     const f2 v = {a, b};

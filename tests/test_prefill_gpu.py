@@ -55,7 +55,8 @@ def test_prefill_gemm_tiles_agree(g2, monkeypatch, P):
     fp16 halves by the kernels that produce them); it sums every output in
     the order of the 64x64-tile GEMM (G2_PREFILL_GEMM64=1), which splits
     the stored fp32 activations itself.  The logits agree to fp32 rounding
-    (1e-5; 1.3e-6 measured at P 65)."""
+    (1e-5; 2.4e-6 to 3.2e-6 measured at P 65 to 1023: the two forms split K
+    into different slices and sum them in different kernels)."""
     cfg = g2.make_config(2, 1600, 25, vocab_size=50257)
     w = g2.synth_weights(cfg, SEED, f16_round=True)
     prompt = random_prompt(P, cfg.vocab_size, 200 + P)
