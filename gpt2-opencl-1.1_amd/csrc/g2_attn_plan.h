@@ -24,14 +24,80 @@
  * g2a_grid(P, NH) work-groups; work-group w runs on XCD w % 8 (consecutive
  * work-groups go to consecutive XCDs), so every query block of head h runs
  * on XCD h % 8, whose L2 then fetches that head's keys and values once for
- * all of them.  Work-groups with h >= NH have no work. */
-G2A_FN void g2a_block(int w, int P, int *h, int *qb)
+ * all of them.  Work-groups with h >= NH have no work of their own (see the
+ * helpers below).  Index k = the work-group's position on its XCD counts
+ * down: the last head group (whose idle work-groups are the helpers) and,
+ * within a head group, the last query blocks (the longest) are dispatched
+ * first. */
+G2A_FN unsigned g2a_grid(int P, int NH) { return 8u * (unsigned)((NH + 7) / 8) * (unsigned)((P + 63) / 64); }
+G2A_FN int g2a_k(int w, int P, int NH) { return (int)(g2a_grid(P, NH) >> 3) - 1 - (w >> 3); }
+G2A_FN void g2a_block(int w, int P, int NH, int *h, int *qb)
 {
-    const int nqb = (P + 63) / 64, k = w >> 3;
+    const int nqb = (P + 63) / 64, k = g2a_k(w, P, NH);
     *h = (w & 7) + 8 * (k / nqb);
     *qb = k % nqb;
 }
-G2A_FN unsigned g2a_grid(int P, int NH) { return 8u * (unsigned)((NH + 7) / 8) * (unsigned)((P + 63) / 64); }
+
+/* Helpers.  A query block qb takes (qb + 2) / 2 iterations (its key blocks
+ * 0..qb, two at a time by the two key halves of the work-group), so the
+ * last query blocks set the kernel's length.  When the head count is not a
+ * multiple of 8 the grid has idle work-groups (h >= NH): (8 - NH % 8) per
+ * query block index.  If they are enough, each of the longest query blocks
+ * (those of the most iterations, n_long per head) gets one: the helper
+ * runs key blocks [0, 2 nh) of it and leaves its softmax partial in slot
+ * j; the block's own work-group runs key blocks [2 nh, qb] and merges the
+ * partial.  nh = half the iterations, so both take about half as long,
+ * below the next-longest blocks when there are at least 3 iterations.  A
+ * block waits for its helper, which waits for nothing; the host uses
+ * helpers only when the whole grid is resident at once (at most one
+ * work-group per CU), so no helper is dispatched behind a waiting block. */
+typedef struct {
+    int on;     /* helpers in use */
+    int nlong;  /* longest query blocks per head (the last one or two) */
+    int nh;     /* iterations (pairs of key blocks) a helper runs */
+    int nslots; /* helper slots = nlong * NH */
+} g2a_help;
+
+G2A_FN g2a_help g2a_help_plan(int P, int NH)
+{
+    g2a_help p;
+    const int nqb = (P + 63) / 64;
+    const int maxit = (nqb - 1 + 2) >> 1;
+    p.nlong = nqb >= 2 && ((nqb - 2 + 2) >> 1) == maxit ? 2 : 1;
+    p.nh = maxit >> 1;
+    p.nslots = p.nlong * NH;
+    const int idle = NH % 8 ? (8 - NH % 8) * nqb : 0;
+    p.on = maxit >= 3 && p.nslots <= idle;
+    return p;
+}
+/* helper index of idle work-group w (h >= NH), or -1 (past the helpers) */
+G2A_FN int g2a_helper_index(int w, int P, int NH, const g2a_help *hp)
+{
+    const int nqb = (P + 63) / 64, x = w & 7, k = g2a_k(w, P, NH), g = (NH + 7) / 8 - 1, x0 = NH % 8;
+    const int j = (k - g * nqb) * (8 - x0) + (x - x0);
+    return hp->on && j < hp->nslots ? j : -1;
+}
+/* the (head, query block) helper j works for */
+G2A_FN void g2a_helped_block(int j, int P, const g2a_help *hp, int *h, int *qb)
+{
+    const int nqb = (P + 63) / 64;
+    *h = j / hp->nlong;
+    *qb = nqb - hp->nlong + j % hp->nlong;
+}
+/* the helper slot of query block (h, qb), or -1 (no helper) */
+G2A_FN int g2a_help_slot(int h, int qb, int P, const g2a_help *hp)
+{
+    const int nqb = (P + 63) / 64;
+    return hp->on && qb >= nqb - hp->nlong ? h * hp->nlong + qb - (nqb - hp->nlong) : -1;
+}
+/* Slot j: 5 vectors of 4 floats per thread of the key half 0 (256
+ * threads): vector 0 = (max, sum, 0, 0) of the thread's row, vectors 1..4 =
+ * its unnormalised output tiles; vector q of thread t at (5 j + q) 256 + t
+ * (16-byte units). */
+#define G2A_HELP_SLOT_BYTES (5 * 256 * 16)
+G2A_FN int g2a_help_vec(int j, int q, int t) { return (5 * j + q) * 256 + t; }
+/* slots a buffer must hold for prompts of up to 1023 rows */
+#define G2A_HELP_MAX_SLOTS (7 * 16)
 
 /* The query row of a lane: row group rg (0..3) of the block, lane l holds
  * row 16 rg + l % 16. */

@@ -35,6 +35,9 @@ enum {
 #define G2_ERR_STEP_NOT_RESIDENT 8
 /* a step-kernel launch whose grid differs from its row-plan table did nothing */
 #define G2_ERR_STEP_ARGS 16
+/* a prompt-attention work-group waited too long for its helper's partial;
+ * the prefill's outputs and the helper slots are invalid */
+#define G2_ERR_ATTN_TIMEOUT 32
 
 /* GEMM: C[M,N] = A[M,K] * op(B) with an epilogue.
  * B layout G2_BKN: [K,N] row-major (the reference's device layout);
@@ -354,6 +357,12 @@ typedef struct {
      * to out_hi, out_lo [P,E] instead of to out */
     uint16_t *out_hi, *out_lo;
     const uint16_t *kh, *kl, *vth, *vtl;
+    /* g2k_attn_prefill_h16's helper slots (g2a_help_plan; NULL: no helpers),
+     * G2A_HELP_MAX_SLOTS of G2A_HELP_SLOT_BYTES, every float G2V_EMPTY
+     * between launches; err: the G2S_ERR word, which a timed-out wait for a
+     * helper's partial marks */
+    float *help;
+    int *err;
 } g2_attnp_args;
 
 #endif /* G2_KARGS_H */

@@ -1379,15 +1379,16 @@ __device__ __forceinline__ float row16_sum(float v)
     return v + apf_dpp<0x121>(v);
 }
 
-/* Work-group -> (head, 64-row query block) of the prompt attention: the
- * grid is 1-D, 8 * ceil(NH / 8) * nqb work-groups, and work-group w runs on
- * XCD w % 8 (consecutive work-groups go to consecutive XCDs), so every query
- * block of head h runs on XCD h % 8, whose L2 then fetches that head's keys
- * and values once for all of them.  Work-groups past the last head have no
- * work. */
+/* Work-group -> (head, 64-row query block) of the prompt attention
+ * (g2a_block): the grid is 1-D, 8 * ceil(NH / 8) * nqb work-groups, and
+ * work-group w runs on XCD w % 8 (consecutive work-groups go to consecutive
+ * XCDs), so every query block of head h runs on XCD h % 8, whose L2 then
+ * fetches that head's keys and values once for all of them; the longest
+ * query blocks and the helpers are dispatched first.  Work-groups past the
+ * last head have no work of their own. */
 __device__ __forceinline__ void attnp_block(const g2_attnp_args &a, int &h, int &qb)
 {
-    g2a_block((int)blockIdx.x, a.P, &h, &qb);
+    g2a_block((int)blockIdx.x, a.P, a.NH, &h, &qb);
 }
 
 extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_mfma(const g2_attnp_args a)
@@ -1647,6 +1648,92 @@ __device__ __forceinline__ void pt_operand(const f32x4 &d0, const f32x4 &d1, f16
     pl = __builtin_bit_cast(f16x8, ol);
 }
 
+/* The softmax partial of a query block's row split between a helper and
+ * the block's work-group (g2a_help_plan).  Both have combined their two key
+ * halves into max mx, sum lx and unnormalised output o f0 + x f1 (x: the
+ * other half's, in LDS at xw + 2).  The helper stores (mx, lx, 0, 0) and the
+ * four output tiles into slot j (thread t's vectors at g2a_help_vec) and is
+ * done; the block's work-group polls them (loads at the coherence point,
+ * sc1, as relaxed agent-scope atomics are) until no float is G2V_EMPTY,
+ * writes G2V_EMPTY back, and stores the merged row (helper's part first:
+ * its keys come first) at out + idx.  Every float of a slot is written
+ * once per launch by one store, so a float read non-empty is this
+ * launch's; a stored value with G2V_EMPTY's bits (only a NaN could have
+ * them) is stored as the canonical NaN.  The wait is bounded
+ * (G2_ERR_ATTN_TIMEOUT in *err, after which the slots must be refilled). */
+__device__ __forceinline__ void attn_help_merge(const g2_attnp_args &a, int j, bool helper, int t, float mx, float lx,
+                                                const f32x4 (&o)[4], const float *xw, float f0, float f1, size_t idx)
+{
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void *)a.help, (short)0,
+                                                                        G2A_HELP_MAX_SLOTS * G2A_HELP_SLOT_BYTES, 0x00020000);
+    f32x4 ox[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ox[q][r] = o[q][r] * f0 + xw[2 + 4 * q + r] * f1;
+    auto bits = [](float f) {
+        const unsigned b = __float_as_uint(f);
+        return b == G2V_EMPTY ? 0x7FC00000u : b;
+    };
+    if (helper) {
+        const u32x4 v0 = {bits(mx), bits(lx), 0u, 0u};
+        __builtin_amdgcn_raw_buffer_store_b128(v0, rs, g2a_help_vec(j, 0, t) * 16, 0, 16 /* sc1 */);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const u32x4 v = {bits(ox[q].x), bits(ox[q].y), bits(ox[q].z), bits(ox[q].w)};
+            __builtin_amdgcn_raw_buffer_store_b128(v, rs, g2a_help_vec(j, q + 1, t) * 16, 0, 16 /* sc1 */);
+        }
+        return;
+    }
+    auto empty = [](const u32x4 &v) {
+        return v.x == G2V_EMPTY || v.y == G2V_EMPTY || v.z == G2V_EMPTY || v.w == G2V_EMPTY;
+    };
+    u32x4 v[5];
+#pragma unroll
+    for (int q = 0; q < 5; ++q) v[q] = __builtin_amdgcn_raw_buffer_load_b128(rs, g2a_help_vec(j, q, t) * 16, 0, 16);
+    bool bad = empty(v[0]) || empty(v[1]) || empty(v[2]) || empty(v[3]) || empty(v[4]);
+    if (bad) {
+        const unsigned long long t0 = wall_clock64();
+        for (;;) {
+            __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+            for (int q = 0; q < 5; ++q)
+                if (empty(v[q])) v[q] = __builtin_amdgcn_raw_buffer_load_b128(rs, g2a_help_vec(j, q, t) * 16, 0, 16);
+            bad = empty(v[0]) || empty(v[1]) || empty(v[2]) || empty(v[3]) || empty(v[4]);
+            if (!bad) break;
+            if (wall_clock64() - t0 > 20000000ull) { /* 200 ms of the 100 MHz clock */
+                atomicOr(a.err, G2_ERR_ATTN_TIMEOUT);
+                break;
+            }
+        }
+    }
+    const u32x4 e4 = {G2V_EMPTY, G2V_EMPTY, G2V_EMPTY, G2V_EMPTY};
+#pragma unroll
+    for (int q = 0; q < 5; ++q) __builtin_amdgcn_raw_buffer_store_b128(e4, rs, g2a_help_vec(j, q, t) * 16, 0, 16 /* sc1 */);
+    const float mh = __uint_as_float(v[0].x), lh = __uint_as_float(v[0].y);
+    const float mm = fmaxf(mh, mx);
+    const float gh = mh == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mh - mm);
+    const float gx = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mx - mm);
+    const float inv = 1.0f / (lh * gh + lx * gx);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const f32x4 oh = __builtin_bit_cast(f32x4, v[q + 1]);
+        f32x4 y;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) y[r] = (oh[r] * gh + ox[q][r] * gx) * inv;
+        const size_t ix = idx + 16 * q;
+        if (a.out_hi) {
+            uint2 hv, lv;
+            split2(y[0], y[1], hv.x, lv.x);
+            split2(y[2], y[3], hv.y, lv.y);
+            *(uint2 *)(a.out_hi + ix) = hv;
+            *(uint2 *)(a.out_lo + ix) = lv;
+        } else {
+            *(f32x4 *)(a.out + ix) = y;
+        }
+    }
+}
+
 extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_attnp_args a)
 {
     constexpr int TILE = 64 * 64; /* halves per staged array */
@@ -1659,7 +1746,21 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
     const int lane = tid & 63, lr = lane & 15, lg = lane >> 4;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); /* uniform: key half and row group in SGPRs */
     const int rg = wave & 3, hs = wave >> 2;
-    if (h >= a.NH || qb * 64 >= a.P) return;
+    /* key blocks [kb_lo, kb_hi] of query block qb: all of them, or with a
+     * helper (g2a_help_plan) the helper's first 2 nh and the rest here;
+     * `helper`: the slot this work-group fills as a helper, else -1 */
+    const g2a_help hp = g2a_help_plan(a.P, a.NH);
+    int helper = -1, kb_lo = 0, kb_hi = qb;
+    if (h >= a.NH) {
+        if (!a.help) return;
+        helper = g2a_helper_index((int)blockIdx.x, a.P, a.NH, &hp);
+        if (helper < 0) return;
+        g2a_helped_block(helper, a.P, &hp, &h, &qb);
+        kb_hi = 2 * hp.nh - 1;
+    } else if (a.help && g2a_help_slot(h, qb, a.P, &hp) >= 0) {
+        kb_lo = 2 * hp.nh;
+    }
+    if (qb * 64 >= a.P) return;
     /* scores in base-2 units (scaled by log2 e): the softmax's
      * exponentials are single v_exp_f32 instructions */
     const float scale2 = a.scale * 1.4426950408889634f;
@@ -1718,15 +1819,15 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
             __builtin_amdgcn_global_load_lds(vlb + vof[e], (lds_t *)(dst + 3 * TB), 16, 0, 0);
         }
     };
-    const int nit = (qb + 2) >> 1;
-    if (hs <= qb) stage(hs, 0); /* wave-uniform */
+    const int nit = (kb_hi - kb_lo + 2) >> 1;
+    if (kb_lo + hs <= kb_hi) stage(kb_lo + hs, 0); /* wave-uniform */
     for (int it = 0; it < nit; ++it) {
-        const int kb = 2 * it + hs, j0 = kb * 64, b = it & 1;
+        const int kb = kb_lo + 2 * it + hs, j0 = kb * 64, b = it & 1;
         /* this wave's part of block kb has landed; every wave is past the
          * products of the block before, which read stage b ^ 1 */
         asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-        if (kb + 2 <= qb) stage(kb + 2, b ^ 1); /* wave-uniform */
-        if (kb > qb) continue;                   /* wave-uniform */
+        if (kb + 2 <= kb_hi) stage(kb + 2, b ^ 1); /* wave-uniform */
+        if (kb > kb_hi) continue;                   /* wave-uniform */
         const _Float16 *Kh = kvs + g2a_array(hs, b, 0), *Kl = Kh + TILE;
         const _Float16 *Vh = Kh + 2 * TILE, *Vl = Kh + 3 * TILE;
         /* S^T tiles: keys j0 + 16t + 4lg + r of row i */
@@ -1843,6 +1944,11 @@ extern "C" __global__ __launch_bounds__(512) void g2k_attn_prefill_h16(const g2_
     const float mx = fmaxf(m, m1);
     const float f0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mx);
     const float f1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mx);
+    if (helper >= 0 || kb_lo > 0) {
+        attn_help_merge(a, helper >= 0 ? helper : g2a_help_slot(h, qb, P, &hp), helper >= 0, tid, mx,
+                        l * f0 + l1 * f1, o, xw, f0, f1, (size_t)i * E + h * 64 + 4 * lg);
+        return;
+    }
     const float inv = 1.0f / (l * f0 + l1 * f1);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {

@@ -28,6 +28,7 @@
 #include "g2_host.h"
 #include "g2_step_plan.h"
 #include "g2_gemm_plan.h"
+#include "g2_attn_plan.h"
 
 typedef struct {
     float *ln1_w, *ln1_b, *qkv_b, *proj_b, *ln2_w, *ln2_b, *fc_b, *fc2_b;
@@ -48,6 +49,8 @@ struct g2_model {
     float *hidden, *ln_out, *attn, *attn_proj, *ffn1, *ffn2, *qkv_new, *qkv_full;
     float *last_hidden, *logits, *partial, *scores, *q;
     float *pf_part; /* split-K slices of the fp16 prefill GEMM */
+    float *pf_help; /* helper slots of the prompt attention, G2V_EMPTY between launches */
+    int help_ran;   /* a prompt attention with helpers ran since the last error check */
     uint16_t *pf_kv; /* the prompt's K and V as fp16 halves: kh, kl [S][E], vth, vtl [E][S] */
     int *ids_dev;
     /* fused path */
@@ -263,6 +266,35 @@ static int step_setup(g2_model *m)
     return rc;
 }
 
+/* every float of the prompt attention's helper slots G2V_EMPTY (at
+ * creation, and after a timed-out wait, which can leave a late partial
+ * behind) */
+static int help_fill(g2_model *m)
+{
+    return g2i_hip(hipMemsetD32Async((hipDeviceptr_t)m->pf_help, (int)G2V_EMPTY,
+                                     (size_t)G2A_HELP_MAX_SLOTS * G2A_HELP_SLOT_BYTES / 4, g2i_stream()),
+                   "attention helper slots fill");
+}
+
+/* After a prefill whose prompt attention had helpers: fail if a wait for a
+ * helper's partial timed out (the prefill's outputs are then invalid),
+ * after refilling the slots and clearing the bit. */
+static int prefill_check(g2_model *m)
+{
+    if (!m->help_ran) return G2_OK;
+    m->help_ran = 0;
+    int err = 0;
+    int rc = g2i_hip(hipMemcpyAsync(&err, m->state + G2S_ERR, sizeof err, hipMemcpyDeviceToHost, g2i_stream()),
+                     "prefill check");
+    if (!rc) rc = g2i_hip(hipStreamSynchronize(g2i_stream()), "prefill check sync");
+    if (rc || !(err & G2_ERR_ATTN_TIMEOUT)) return rc;
+    err &= ~G2_ERR_ATTN_TIMEOUT;
+    rc = help_fill(m);
+    if (!rc) rc = up(m->state + G2S_ERR, &err, sizeof err);
+    return rc ? rc : g2i_err(G2_E_HIP, "prompt attention: a wait for a helper's partial timed out; "
+                                       "the prefill's outputs are invalid");
+}
+
 static int alloc_workspaces(g2_model *m)
 {
     const size_t E = (size_t)m->cfg.n_embd, F = (size_t)m->cfg.ffn_dim, T = 3 * E;
@@ -276,6 +308,8 @@ static int alloc_workspaces(g2_model *m)
     if (m->path == G2_PATH_FUSED && m->dtype == G2_F16) A(m->pf_part, (size_t)G2_PF_MAXSPLIT * S * E * 4);
     if (m->path == G2_PATH_FUSED && m->dtype == G2_F32) A(m->pf_part, (size_t)G2_SG_PART_FLOATS * 4);
     if (m->path == G2_PATH_FUSED) {
+        A(m->pf_help, (size_t)G2A_HELP_MAX_SLOTS * G2A_HELP_SLOT_BYTES);
+        if (!rc) rc = help_fill(m);
         /* zeroed once: entries past a prompt are finite (zero or an earlier
          * prompt's), so the masked keys of a block contribute 0 x finite */
         A(m->pf_kv, 4 * S * E * 2);
@@ -334,7 +368,7 @@ int g2_model_free(g2_model *m)
                      m->attn, m->attn_proj, m->ffn1, m->ffn2, m->qkv_new, m->qkv_full,
                      m->last_hidden, m->logits, m->partial, m->scores, m->q, m->ids_dev,
                      m->state, m->att_part, m->am_part, m->step_layers, m->xbuf, m->xval, m->lnfold, m->trace, m->pf_part,
-                     m->pf_kv, m->step_shares };
+                     m->pf_kv, m->step_shares, m->pf_help };
     for (size_t i = 0; i < sizeof bufs / sizeof bufs[0]; ++i)
         if (bufs[i]) hipFree(bufs[i]);
     for (int l = 0; l < m->cfg.n_layer; ++l) {
@@ -1066,6 +1100,8 @@ static int fused_prefill(g2_model *m, int P)
     int ln_unused = 0;
     const char *ea = getenv("G2_PREFILL_ATTN32");
     const int attn32 = ea && ea[0] == '1'; /* attention on the fp32 matrix cores (reference point) */
+    const char *eh = getenv("G2_PREFILL_ATTN_HELP");
+    const int help_off = eh && eh[0] == '0';
     for (int l = 0; l < m->cfg.n_layer && !rc; ++l) {
         g2_layer *y = &m->L[l];
         g2_lnsplit_args ls = { m->hidden, ln_h, ln_l, y->ln1_w, y->ln1_b, E, P };
@@ -1082,7 +1118,16 @@ static int fused_prefill(g2_model *m, int P)
                       : sg  ? prefill_sgemm(m, G2_SG_QKV, &g, NULL, NULL, &ln_unused)
                             : g2i_launch(f_qkv, cdivu(3 * E, 64), cdivu(P, 64), 256, &g);
         g2_attnp_args t = { m->q, y->k_cache, y->v_cache, m->attn, P, E, NH, G2_KV_MAX_SEQ, 1.0f / sqrtf(64.0f),
-                            big ? at_h : NULL, big ? at_l : NULL, kv_kh, kv_kl, kv_vh, kv_vl };
+                            big ? at_h : NULL, big ? at_l : NULL, kv_kh, kv_kl, kv_vh, kv_vl, NULL, NULL };
+        /* the grid's idle work-groups help the longest query blocks
+         * (g2a_help_plan; G2_PREFILL_ATTN_HELP=0 turns them off), when the
+         * whole grid is resident at once (one work-group per CU), so a
+         * block's helper is never dispatched behind the block's wait */
+        if (!attn32 && !help_off && g2a_help_plan(P, NH).on && g2a_grid(P, NH) <= (unsigned)g2i_cus()) {
+            t.help = m->pf_help;
+            t.err = m->state + G2S_ERR;
+            m->help_ran = 1;
+        }
         /* 1-D grid: 8 XCDs x ceil(NH / 8) heads x query blocks (attnp_block) */
         if (!rc) rc = g2i_launch(attn32 ? G2F_ATTN_PREFILL_MFMA : G2F_ATTN_PREFILL_H16, 8 * cdivu(NH, 8) * cdivu(P, 64), 1,
                                  512, &t);
@@ -1130,6 +1175,7 @@ int g2_prefill(g2_model *m, const int *ids, int n)
     if (m->path == G2_PATH_REFERENCE) return ref_prefill(m, n);
     rc = set_state(m, n - 1, ids[n - 1], 0, 0);
     if (!rc) rc = fused_prefill(m, n);
+    if (!rc) rc = prefill_check(m);
     return rc;
 }
 
@@ -1249,6 +1295,7 @@ int g2_generate(g2_model *m, const int *prompt, int n_prompt, int max_new, int m
     if (m->events_ok) hipEventRecord(m->ev[1], g2i_stream());
     for (int s = 0; s < n_dec && !rc; ++s) rc = fused_step(m);
     if (m->events_ok) hipEventRecord(m->ev[2], g2i_stream());
+    if (!rc) rc = prefill_check(m);
     if (!rc) rc = step_check(m, 1 + n_dec); /* the prefill's pick + n_dec steps */
     if (rc) return rc;
     int *st = malloc((size_t)G2S_WORDS * sizeof(int));

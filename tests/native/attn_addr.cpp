@@ -14,7 +14,8 @@
  *     outputs [P][E] are each written exactly once.
  *
  * Usage: attn_addr P NH [plant]
- *   plant=1 stages one key block too far, plant=2 reads the fragments with a
+ *   plant=1 stages one key block too far, plant=3 lets a helper take one key
+ *   block of its block's own work-group, plant=2 reads the fragments with a
  *   4-slot instead of an 8-slot swizzle (planted mistakes the check must
  *   catch).
  * Exit status 0: all checks pass; 1: a check failed (first failure
@@ -61,7 +62,7 @@ int main(int argc, char **argv)
     std::vector<int> seen((size_t)NH * nqb, 0);
     for (unsigned w = 0; w < grid; ++w) {
         int h, qb;
-        g2a_block((int)w, P, &h, &qb);
+        g2a_block((int)w, P, NH, &h, &qb);
         if (h >= NH || qb * 64 >= P) continue;
         if (h < 0 || qb < 0 || qb >= nqb) {
             FAIL("work-group %u: head %d block %d outside the launch", w, h, qb);
@@ -73,15 +74,35 @@ int main(int argc, char **argv)
         for (int qb = 0; qb < nqb; ++qb)
             if (seen[(size_t)h * nqb + qb] != 1) FAIL("head %d block %d taken %d times", h, qb, seen[(size_t)h * nqb + qb]);
 
-    /* staging, placement, fragment reads, queries and outputs */
+    /* staging, placement, fragment reads, queries and outputs; the idle
+     * work-groups' helper roles (g2a_help_plan), as the kernel takes them */
+    const g2a_help hp = g2a_help_plan(P, NH);
     std::vector<int> slot_chunk(64 * 8), slot_hits(64 * 8), out_hits((size_t)P * E, 0);
+    std::vector<int> kcover((size_t)NH * nqb * nqb, 0), slot_w(hp.nslots + 1, 0), slot_r(hp.nslots + 1, 0);
+    const long slot_bytes = (long)G2A_HELP_MAX_SLOTS * G2A_HELP_SLOT_BYTES;
+    if (hp.on && hp.nslots > G2A_HELP_MAX_SLOTS) FAIL("%d helper slots, the buffer holds %d", hp.nslots, G2A_HELP_MAX_SLOTS);
     for (unsigned w = 0; w < grid && !fails; ++w) {
         int h, qb;
-        g2a_block((int)w, P, &h, &qb);
-        if (h >= NH || qb * 64 >= P) continue;
+        g2a_block((int)w, P, NH, &h, &qb);
+        int helper = -1, kb_lo = 0, kb_hi = qb;
+        if (h >= NH) {
+            if (!hp.on) continue;
+            helper = g2a_helper_index((int)w, P, NH, &hp);
+            if (helper < 0) continue;
+            g2a_helped_block(helper, P, &hp, &h, &qb);
+            kb_hi = 2 * hp.nh - 1 + (plant == 3 ? 1 : 0);
+            if (helper >= hp.nslots || h < 0 || h >= NH || qb < 0 || qb >= nqb) {
+                FAIL("work-group %u: helper %d of head %d block %d outside the launch", w, helper, h, qb);
+                continue;
+            }
+        } else if (hp.on && g2a_help_slot(h, qb, P, &hp) >= 0) {
+            kb_lo = 2 * hp.nh;
+        }
+        if (qb * 64 >= P) continue;
         for (int hs = 0; hs < 2; ++hs) {
-            /* the key blocks this half stages: hs, hs + 2, ... <= qb (stage it & 1) */
-            for (int kb = hs, it = 0; kb <= qb; kb += 2, ++it) {
+            /* the key blocks this half stages: kb_lo + hs, + 2, ... <= kb_hi (stage it & 1) */
+            for (int kb = kb_lo + hs, it = 0; kb <= kb_hi; kb += 2, ++it) {
+                if (kb >= 0 && kb < nqb) kcover[((size_t)h * nqb + qb) * nqb + kb]++;
                 const int b = it & 1, j0 = (kb + (plant == 1 ? 1 : 0)) * 64;
                 std::fill(slot_hits.begin(), slot_hits.end(), 0);
                 for (int w4 = 0; w4 < 4; ++w4)
@@ -122,13 +143,26 @@ int main(int argc, char **argv)
                         }
             }
         }
-        /* queries and outputs (the first key half's waves store) */
+        /* a helper's slot (stored by the first key half's threads), read by
+         * the helped block's work-group */
+        const int slot = helper >= 0 ? helper : (kb_lo > 0 ? g2a_help_slot(h, qb, P, &hp) : -1);
+        if (slot >= 0) {
+            if (slot > hp.nslots) FAIL("slot %d past %d", slot, hp.nslots);
+            else (helper >= 0 ? slot_w : slot_r)[slot]++;
+            for (int t = 0; t < 256; ++t)
+                for (int q = 0; q < 5; ++q) {
+                    const long o = (long)g2a_help_vec(slot, q, t) * 16;
+                    if (o < 0 || o + 16 > slot_bytes) FAIL("helper slot %d vector %d of thread %d outside the slots", slot, q, t);
+                }
+        }
+        /* queries and outputs (the first key half's waves store; a helper
+         * stores none) */
         for (int rg = 0; rg < 4; ++rg)
             for (int lane = 0; lane < 64; ++lane) {
                 const int i = g2a_query(qb, rg, lane), lg = lane >> 4;
                 const long q0 = (long)(i < P - 1 ? i : P - 1) * E + h * 64 + 8 * lg;
                 if (q0 < 0 || q0 + 36 + 4 > (long)P * E) FAIL("query load %ld outside q [P][E]", q0);
-                if (i >= P) continue;
+                if (i >= P || helper >= 0) continue;
                 for (int t = 0; t < 4; ++t) {
                     const long idx = (long)i * E + h * 64 + 16 * t + 4 * lg;
                     if (idx < 0 || idx + 4 > (long)P * E) {
@@ -145,10 +179,24 @@ int main(int argc, char **argv)
                 FAIL("output row %ld column %ld written %d times", k / E, k % E, out_hits[k]);
                 break;
             }
+    /* every key block 0..qb of every query block once (between a helper and
+     * the block's own work-group), every helper slot written and read once */
+    for (int h = 0; h < NH && !fails; ++h)
+        for (int qb = 0; qb < nqb; ++qb)
+            for (int kb = 0; kb < nqb; ++kb) {
+                const int c = kcover[((size_t)h * nqb + qb) * nqb + kb];
+                if (c != (kb <= qb ? 1 : 0)) {
+                    FAIL("head %d block %d: key block %d taken %d times", h, qb, kb, c);
+                    break;
+                }
+            }
+    if (hp.on)
+        for (int j = 0; j < hp.nslots; ++j)
+            if (slot_w[j] != 1 || slot_r[j] != 1) FAIL("helper slot %d written %d, read %d times", j, slot_w[j], slot_r[j]);
     if (fails) {
         std::printf("P %d NH %d: %ld failed checks\n", P, NH, fails);
         return 1;
     }
-    std::printf("P %d NH %d: %u work-groups: ok\n", P, NH, grid);
+    std::printf("P %d NH %d: %u work-groups, %d helpers: ok\n", P, NH, grid, hp.on ? hp.nslots : 0);
     return 0;
 }

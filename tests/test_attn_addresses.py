@@ -9,9 +9,13 @@ every work-group, key half, wave and lane of a launch: the staging loads
 stay inside the K halves [S][E] and the transposed V halves [E][S] and
 inside their LDS stage, every fragment read finds the chunk its product
 needs, the query loads stay inside the prompt's rows and every output is
-written once.  Prompt lengths 1 to 1023 (the cache limit), GPT-2 small to XL
-head counts.  Planted mistakes (a key block staged one block too far, a
-narrower read swizzle) must be caught.  No GPU is involved.
+written once.  The idle work-groups' helper roles (g2a_help_plan) are walked
+as the kernel takes them: every key block of every query block is taken
+once, by the block's own work-group or its helper, and every helper slot is
+written once, read once and inside the slot buffer.  Prompt lengths 1 to
+1023 (the cache limit), GPT-2 small to XL head counts.  Planted mistakes (a
+key block staged one block too far, a helper overlapping its block's own
+key range, a narrower read swizzle) must be caught.  No GPU is involved.
 """
 import os
 import shutil
@@ -53,6 +57,14 @@ def test_prompt_attention_addresses(checker):
 def test_planted_key_block_overrun_is_caught(checker):
     rc, out = run(checker, 1023, 25, plant=1)
     assert rc == 1 and "out of bounds" in out, out
+
+
+def test_planted_helper_overlap_is_caught(checker):
+    """A helper that also takes the first key block of its block's own
+    work-group (the key ranges overlap) must be caught."""
+    for P in (300, 512):
+        rc, out = run(checker, P, 25, plant=3)
+        assert rc == 1 and "taken 2 times" in out, out
 
 
 def test_planted_read_swizzle_is_caught(checker):

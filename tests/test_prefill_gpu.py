@@ -90,3 +90,39 @@ def test_prefill_attention_h16_matches_f32(g2, monkeypatch, P):
         out.append(m.logits().copy())
         m.free()
     np.testing.assert_allclose(out[0], out[1], rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("E,NH,P", [(1600, 25, 300), (1600, 25, 512), (768, 12, 700)])
+def test_prefill_attention_helpers(g2, monkeypatch, E, NH, P):
+    """The prompt attention with the grid's idle work-groups computing the
+    first key blocks of the longest query blocks (g2a_help_plan: 25 helpers
+    at 300 rows and 50 at 512 for 25 heads, 12 at 700 rows for 12 heads),
+    their softmax partials merged by the blocks' own work-groups, against
+    the same attention without helpers (G2_PREFILL_ATTN_HELP=0): the logits
+    agree to fp32 rounding of the split softmax (1e-5).  A second prompt on
+    the same model must give exactly what a fresh model gives (every helper
+    slot was left empty by the first).  Both runs are checked against the
+    oracle elsewhere (full depth at 512 rows)."""
+    cfg = g2.make_config(2, E, NH, vocab_size=50257)
+    w = g2.synth_weights(cfg, SEED, f16_round=True)
+    prompt = random_prompt(P, cfg.vocab_size, 800 + P)
+    prompt2 = random_prompt(P, cfg.vocab_size, 900 + P)
+    print(f"[prefill] E {E} NH {NH} L2, P {P}: attention helpers vs none", flush=True)
+    monkeypatch.setenv("G2_PREFILL_ATTN_HELP", "0")
+    m = g2.Model.from_host(cfg, w, g2.F16, g2.PATH_FUSED)
+    m.prefill(prompt)
+    lg_n = m.logits().copy()
+    m.free()
+    monkeypatch.setenv("G2_PREFILL_ATTN_HELP", "1")
+    m = g2.Model.from_host(cfg, w, g2.F16, g2.PATH_FUSED)
+    m.prefill(prompt)
+    lg_h = m.logits().copy()
+    m.prefill(prompt2)
+    lg_h2 = m.logits().copy()
+    m.free()
+    m = g2.Model.from_host(cfg, w, g2.F16, g2.PATH_FUSED)
+    m.prefill(prompt2)
+    lg_f2 = m.logits().copy()
+    m.free()
+    np.testing.assert_allclose(lg_h, lg_n, rtol=1e-5, atol=1e-5)
+    assert np.array_equal(lg_h2, lg_f2), "second prompt differs from a fresh model's"
