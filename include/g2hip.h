@@ -168,7 +168,7 @@ typedef struct {
     int n_layer, n_embd, n_head, n_ctx, vocab_size, ffn_dim;
 } g2_config;
 
-/* Ceilings of this build (the reference's are main.c:46-52; these admit GPT-2 XL). */
+/* Ceilings of this library (the reference's are main.c:46-52; these admit GPT-2 XL). */
 #define G2_MAX_EMBED 1600
 #define G2_MAX_LAYERS 48
 #define G2_MAX_HEADS 25

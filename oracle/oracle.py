@@ -1,7 +1,8 @@
 """ctypes wrapper of the CPU oracle (liboracle.so built from g2_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by __graft_entry__.smoke() and
-by bench.py's CPU-baseline leg, as the checker or as the timed CPU baseline.
+by bench.py's CPU-baseline leg, as the test reference or as the timed CPU
+baseline.
 The shipped library (gpt2-opencl-1.1_amd/) never imports it.
 
 Functions take and return numpy arrays; names follow the reference kernels

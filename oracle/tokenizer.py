@@ -1,7 +1,7 @@
 """CPU oracle for the GPT-2 text tokenizer -- TEST INFRASTRUCTURE ONLY.
 
 A plain-Python restatement of the reference's tokenizer (tokenizer.c), used
-by tests/ as the checker of the library's g2_tok_* entry points; nothing in
+by tests/ as the reference for the library's g2_tok_* entry points; nothing in
 the product path imports it.  Each function cites the lines it follows.
 
 Pinned by (tests/test_tokenizer.py): golden vectors written by the
