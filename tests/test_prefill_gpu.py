@@ -92,11 +92,12 @@ def test_prefill_attention_h16_matches_f32(g2, monkeypatch, P):
     np.testing.assert_allclose(out[0], out[1], rtol=1e-4, atol=1e-4)
 
 
-@pytest.mark.parametrize("E,NH,P", [(1600, 25, 300), (1600, 25, 512), (768, 12, 700)])
+@pytest.mark.parametrize("E,NH,P", [(1600, 25, 300), (1600, 25, 512), (768, 12, 700), (1280, 20, 640)])
 def test_prefill_attention_helpers(g2, monkeypatch, E, NH, P):
     """The prompt attention with the grid's idle work-groups computing the
     first key blocks of the longest query blocks (g2a_help_plan: 25 helpers
-    at 300 rows and 50 at 512 for 25 heads, 12 at 700 rows for 12 heads),
+    at 300 rows and 50 at 512 for 25 heads, 12 at 700 rows for 12 heads,
+    40 at 640 rows for 20 heads),
     their softmax partials merged by the blocks' own work-groups, against
     the same attention without helpers (G2_PREFILL_ATTN_HELP=0): the logits
     agree to fp32 rounding of the split softmax (1e-5).  A second prompt on
